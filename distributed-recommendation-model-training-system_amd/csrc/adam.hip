@@ -1,0 +1,778 @@
+// adam.hip -- duplicate-id aggregation fused with sparse (Lazy)Adam.
+//
+// Per unique row, one sub-wavefront group of G lanes (lane l owns columns
+// [4l, 4l+4)) sums the row's references in order from +0.0f -- acc = acc +
+// src * scale, separate multiply and add -- (ReduceGradients,
+// src/access/batch_access.cpp:73-93; ExpandCompactGradients,
+// src/access/compact_gradients.cpp:31-36; ReduceFeatureGradients,
+// src/cuda/cache_backend.cu:115-125), then reads the row's w, m, v once, applies
+//   m' = b1*m + (1-b1)*g;  v' = b2*v + ((1-b2)*g)*g;  w' = w - (lr_t*m')/(sqrt(v')+eps)
+// and the clamp (src/update/lazy_adam.cpp:31-35; AdamKernel,
+// src/cuda/cache_backend.cu:95-114), and writes w, m, v once.
+//
+// All-or-nothing without a second pass over the state.  The reference
+// validates every element before any write, with a second full state pass
+// (ValidateLazyAdam then ApplyLazyAdam; AdamKernel twice).  Here a guard decides
+// before the update whether overflow is impossible:
+//   * bounds domain: running maxima W >= |w|, M >= |m|, V >= v of every value
+//     this library ever wrote (init, admission, updates);
+//   * G >= |g| for every reduced gradient: max|source| * max(1, max|scale|) *
+//     references * (1+2^-24)^(references+2) (rounding growth of a sequential sum);
+//   * then |m'| <= b1*M + (1-b1)*G, v' <= b2*V + (1-b2)*G^2 and
+//     |w'| <= W + lr_t*|m'|/eps (since sqrt(v') + eps >= eps), each widened by 1%.
+// If every bound stays below 1e30 (far below FLT_MAX) no element can overflow and
+// the single fused pass runs ("fused").  Otherwise the same kernel runs in
+// validate-only mode and a second launch applies only if nothing failed
+// ("checked") -- the reference's two-pass behaviour.  A non-finite gradient value
+// or an out-of-range slot rejects the whole update before anything is written.
+#include "prepare.hpp"
+
+#include <cfloat>
+#include <cmath>
+
+namespace eps_hip {
+
+int LaunchFill(uint32_t* target, uint32_t value, uint64_t count, hipStream_t stream);
+
+namespace {
+
+constexpr uint32_t kErrorBits = EPS_HIP_STATUS_BAD_INDEX | EPS_HIP_STATUS_NONFINITE_GRAD |
+                                EPS_HIP_STATUS_REDUCE_OVERFLOW | EPS_HIP_STATUS_ADAM_OVERFLOW;
+constexpr uint32_t kFallbackGrid = 2048;
+
+// ---------------------------------------------------------------------------
+// Gradient maximum and the guard decision (last block).
+struct Span {
+  const float* p;
+  uint64_t count;
+  uint32_t block_begin, is_scale;
+};
+struct GuardTable { float beta1, beta2, lr, eps; };
+struct GuardArgs {
+  Span span[EPS_HIP_MAX_FEATURES + 1];
+  GuardTable t[EPS_HIP_MAX_TABLES];
+  uint32_t spans, tables, reset_scale, use_prep_status;
+  uint64_t refs_host;  // 0: take the prepared valid count
+  Control* ctrl;
+  const Bounds* bounds;
+};
+constexpr uint32_t kMaxItems = 16;  // float4 per thread per block
+
+__global__ void __launch_bounds__(kBlock) GradMaxKernel(GuardArgs a) {
+  Span sp = a.span[0];
+#pragma unroll
+  for (uint32_t i = 1; i <= EPS_HIP_MAX_FEATURES; ++i)
+    if (i < a.spans && blockIdx.x >= a.span[i].block_begin) sp = a.span[i];
+  const uint64_t per_block = uint64_t(kBlock) * kMaxItems * 4;
+  const uint64_t begin = uint64_t(blockIdx.x - sp.block_begin) * per_block;
+  const uint64_t end = min(begin + per_block, sp.count);
+  uint32_t m = 0;
+  if (reinterpret_cast<uintptr_t>(sp.p) % 16 == 0) {
+    const uint64_t vend = begin + ((end - begin) & ~uint64_t(3));
+    for (uint64_t i = begin + threadIdx.x * 4; i < vend; i += kBlock * 4) {
+      const float4 x = Load4(sp.p + i);
+      m = max(m, max(max(AbsBits(x.x), AbsBits(x.y)), max(AbsBits(x.z), AbsBits(x.w))));
+    }
+    for (uint64_t i = vend + threadIdx.x; i < end; i += kBlock) m = max(m, AbsBits(sp.p[i]));
+  } else {
+    for (uint64_t i = begin + threadIdx.x; i < end; i += kBlock) m = max(m, AbsBits(sp.p[i]));
+  }
+  __shared__ uint32_t s_max[4];
+  __shared__ bool s_last;
+  m = WaveMax(m);
+  if ((threadIdx.x & (kWave - 1)) == 0) s_max[threadIdx.x / kWave] = m;
+  __syncthreads();
+  Control* ctrl = a.ctrl;
+  if (threadIdx.x == 0) {
+    const uint32_t bm = max(max(s_max[0], s_max[1]), max(s_max[2], s_max[3]));
+    if (bm) atomicMax(sp.is_scale ? &ctrl->max_scale_bits : &ctrl->max_src_bits, bm);
+    __threadfence();
+    s_last = atomicAdd(&ctrl->done_counter, 1u) == gridDim.x - 1;
+  }
+  __syncthreads();
+  if (!s_last || threadIdx.x != 0) return;
+  __threadfence();
+  const uint32_t src_bits = __hip_atomic_load(&ctrl->max_src_bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const uint32_t scale_bits = __hip_atomic_load(&ctrl->max_scale_bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  uint32_t status = a.use_prep_status ? ctrl->prep_status : 0u;
+  uint32_t mode = kFused;
+  if (status & EPS_HIP_STATUS_BAD_INDEX) {
+    mode = kReject;
+  } else if (src_bits >= 0x7f800000u) {
+    status |= EPS_HIP_STATUS_NONFINITE_GRAD;
+    mode = kReject;
+  } else {
+    uint32_t wb = 0, mb = 0, vb = 0;
+    for (uint32_t s = 0; s < kBoundSlots; ++s) {
+      wb = max(wb, a.bounds->v[s][0]); mb = max(mb, a.bounds->v[s][1]); vb = max(vb, a.bounds->v[s][2]);
+    }
+    const double W = __uint_as_float(wb), M = __uint_as_float(mb), V = __uint_as_float(vb);
+    const double refs = double(a.refs_host ? a.refs_host : ctrl->valid_count);
+    const double scale = fmax(1.0, double(__uint_as_float(scale_bits)));
+    const double G = double(__uint_as_float(src_bits)) * scale * refs *
+                     exp((refs + 2.0) * 0x1.0p-24) * 1.01;
+    bool safe = G < 1e30;
+    for (uint32_t t = 0; t < a.tables && safe; ++t) {
+      const GuardTable& T = a.t[t];
+      const double b1 = T.beta1, b2 = T.beta2;
+      const double mbound = (b1 * M + (1.0 - b1) * G) * 1.01;
+      const double vbound = (b2 * V + (1.0 - b2) * G * G) * 1.01;
+      const double wbound = (W + double(T.lr) * mbound / double(T.eps)) * 1.01;
+      safe = mbound < 1e30 && vbound < 1e30 && wbound < 1e30 && double(T.eps) > 0.0;
+    }
+    if (!safe) { mode = kChecked; status |= EPS_HIP_STATUS_CHECKED_PATH; }
+  }
+  if (mode == kReject) status |= EPS_HIP_STATUS_REJECTED;
+  ctrl->mode = mode;
+  ctrl->status = status;
+  ctrl->max_src_bits = 0;
+  if (a.reset_scale) ctrl->max_scale_bits = 0;
+  ctrl->done_counter = 0;
+  __threadfence();
+}
+
+// ---------------------------------------------------------------------------
+// Shared per-row arithmetic.
+struct TableDesc {
+  float* state;
+  uint32_t dim;
+  float beta1, beta2, omb1, omb2, lr, eps, lo, hi;
+};
+
+struct RowStats {
+  uint32_t err = 0, bw = 0, bm = 0, bv = 0;
+};
+
+// One element: Adam in the reference's operation order; returns w (unclamped).
+__device__ __forceinline__ void AdamElement(const TableDesc& T, float g, float& w, float& m,
+                                            float& v, RowStats& st) {
+  const float mn = T.beta1 * m + T.omb1 * g;
+  const float vn = T.beta2 * v + (T.omb2 * g) * g;
+  const float wn = w - (T.lr * mn) / (sqrtf(vn) + T.eps);
+  if (!Finite(g)) st.err |= EPS_HIP_STATUS_REDUCE_OVERFLOW;
+  if (!(Finite(mn) && Finite(vn) && Finite(wn))) st.err |= EPS_HIP_STATUS_ADAM_OVERFLOW;
+  w = Clamp(wn, T.lo, T.hi);
+  m = mn;
+  v = vn;
+}
+
+__device__ __forceinline__ void Track(RowStats& st, float w, float m, float v) {
+  st.bw = max(st.bw, AbsBits(w));
+  st.bm = max(st.bm, AbsBits(m));
+  st.bv = max(st.bv, AbsBits(v));
+}
+
+// Vector row update: lane owns columns [c, c+4).
+__device__ __forceinline__ void AdamRow4(const TableDesc& T, uint64_t slot, uint32_t c, float4 g,
+                                         bool write, RowStats& st) {
+  float* row = T.state + slot * uint64_t(T.dim) * 3;
+  float4 w = Load4(row + c), m = Load4(row + T.dim + c), v = Load4(row + 2 * T.dim + c);
+  AdamElement(T, g.x, w.x, m.x, v.x, st);
+  AdamElement(T, g.y, w.y, m.y, v.y, st);
+  AdamElement(T, g.z, w.z, m.z, v.z, st);
+  AdamElement(T, g.w, w.w, m.w, v.w, st);
+  if (write) {
+    Store4(row + c, w);
+    Store4(row + T.dim + c, m);
+    Store4(row + 2 * T.dim + c, v);
+    Track(st, w.x, m.x, v.x); Track(st, w.y, m.y, v.y);
+    Track(st, w.z, m.z, v.z); Track(st, w.w, m.w, v.w);
+  }
+}
+
+__device__ __forceinline__ void AdamRow1(const TableDesc& T, uint64_t slot, uint32_t c, float g,
+                                         bool write, RowStats& st) {
+  float* row = T.state + slot * uint64_t(T.dim) * 3;
+  float w = row[c], m = row[T.dim + c], v = row[2 * T.dim + c];
+  AdamElement(T, g, w, m, v, st);
+  if (write) {
+    row[c] = w; row[T.dim + c] = m; row[2 * T.dim + c] = v;
+    Track(st, w, m, v);
+  }
+}
+
+__device__ __forceinline__ void Accumulate4(float4& acc, float4 x, float s) {
+  acc.x = acc.x + x.x * s;
+  acc.y = acc.y + x.y * s;
+  acc.z = acc.z + x.z * s;
+  acc.w = acc.w + x.w * s;
+}
+
+// Block-level fold of the per-lane statistics: error bits to the status word,
+// written maxima to one slot of the bounds domain.
+__device__ void FinishBlock(const RowStats& st, Control* ctrl, Bounds* bounds, bool wrote) {
+  __shared__ uint32_t s_red[4][4];
+  uint32_t e = st.err;
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) e |= uint32_t(__shfl_xor(int(e), o));
+  const uint32_t w = WaveMax(st.bw), m = WaveMax(st.bm), v = WaveMax(st.bv);
+  const uint32_t wave = threadIdx.x / kWave;
+  if ((threadIdx.x & (kWave - 1)) == 0) {
+    s_red[wave][0] = e; s_red[wave][1] = w; s_red[wave][2] = m; s_red[wave][3] = v;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    uint32_t E = 0, W = 0, M = 0, V = 0;
+    for (int i = 0; i < 4; ++i) {
+      E |= s_red[i][0]; W = max(W, s_red[i][1]); M = max(M, s_red[i][2]); V = max(V, s_red[i][3]);
+    }
+    if (E) atomicOr(&ctrl->status, E);
+    if (wrote && bounds) {
+      uint32_t* slot = bounds->v[blockIdx.x % kBoundSlots];
+      if (W) atomicMax(slot + 0, W);
+      if (M) atomicMax(slot + 1, M);
+      if (V) atomicMax(slot + 2, V);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Sorted driver: segments are runs of equal keys in the sorted key array.
+struct FusedArgs {
+  TableDesc t[EPS_HIP_MAX_TABLES];   // by key index
+  const float* grad[EPS_HIP_MAX_FEATURES];
+  const uint32_t* keys;
+  const uint64_t* rs;
+  const uint32_t* vals;              // reduce mode: sorted occurrence indices
+  const uint64_t* occ2u;             // reduce mode
+  float* reduce_out;
+  uint64_t reduce_stride;
+  Control* ctrl;
+  Bounds* bounds;
+  uint32_t row_bits, cls, log2g, ppb, vblocks, fallback, reduce, tables;
+};
+
+// First index q in [from, limit) with keys[q] != key, or limit.
+__device__ uint32_t SegmentEnd(const uint32_t* keys, uint32_t from, uint32_t limit, uint32_t key) {
+  if (from >= limit || keys[from] != key) return from;
+  uint32_t lo = from, step = 1, hi;
+  for (;;) {
+    const uint32_t q = lo + step;
+    if (q >= limit) { hi = limit; break; }
+    if (keys[q] != key) { hi = q; break; }
+    lo = q;
+    step <<= 1;
+  }
+  while (hi - lo > 1) {
+    const uint32_t mid = lo + ((hi - lo) >> 1);
+    if (keys[mid] == key) lo = mid; else hi = mid;
+  }
+  return hi;
+}
+
+template <bool kGeneric>
+__global__ void __launch_bounds__(kBlock) SortedUpdateKernel(FusedArgs a) {
+  __shared__ TableDesc s_t[EPS_HIP_MAX_TABLES];
+  __shared__ const float* s_grad[EPS_HIP_MAX_FEATURES];
+  __shared__ uint32_t s_heads[kBlock];
+  __shared__ uint32_t s_wave_heads[4];
+#pragma unroll
+  for (uint32_t i = 0; i < EPS_HIP_MAX_TABLES; ++i)
+    if (threadIdx.x == i) s_t[i] = a.t[i];
+#pragma unroll
+  for (uint32_t i = 0; i < EPS_HIP_MAX_FEATURES; ++i)
+    if (threadIdx.x == i) s_grad[i] = a.grad[i];
+  Control* ctrl = a.ctrl;
+  const uint32_t mode = ctrl->mode;
+  const uint32_t status = ctrl->status;
+  bool write;
+  if (a.reduce) {
+    write = true;
+  } else if (!a.fallback) {
+    if (mode == kReject) return;
+    write = mode == kFused;
+  } else {
+    if (mode != kChecked) return;
+    if (status & kErrorBits) {
+      if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(&ctrl->status, EPS_HIP_STATUS_REJECTED);
+      return;
+    }
+    write = true;
+  }
+  uint32_t start = 0;
+  for (uint32_t c = 0; c < a.cls; ++c) start += ctrl->class_count[c];
+  const uint32_t end = start + ctrl->class_count[a.cls];
+  const uint32_t G = kGeneric ? kWave : (1u << a.log2g);
+  const uint32_t lig = threadIdx.x & (G - 1);
+  const uint32_t gid = threadIdx.x / G, ngroups = kBlock / G;
+  const uint32_t row_mask = (1u << a.row_bits) - 1;
+  const uint32_t lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  RowStats st;
+  __syncthreads();
+  for (uint32_t vb = blockIdx.x; vb < a.vblocks; vb += gridDim.x) {
+    const uint32_t p0 = start + vb * a.ppb;
+    if (p0 >= end) break;  // uniform: later virtual blocks are further right
+    const uint32_t p1 = min(p0 + a.ppb, end);
+    // Head positions of this block's range, in order.
+    const uint32_t p = p0 + threadIdx.x;
+    const bool head = threadIdx.x < a.ppb && p < p1 && (p == start || a.keys[p] != a.keys[p - 1]);
+    const uint64_t ballot = __ballot(head);
+    if (lane == 0) s_wave_heads[wave] = uint32_t(__popcll(ballot));
+    __syncthreads();
+    uint32_t before = 0;
+    for (uint32_t w = 0; w < wave; ++w) before += s_wave_heads[w];
+    const uint32_t nheads = s_wave_heads[0] + s_wave_heads[1] + s_wave_heads[2] + s_wave_heads[3];
+    if (head) s_heads[before + uint32_t(__popcll(ballot & ((1ull << lane) - 1)))] = p;
+    __syncthreads();
+    for (uint32_t h = gid; h < nheads; h += ngroups) {
+      const uint32_t sb = s_heads[h];
+      const uint32_t key = a.keys[sb];
+      const uint32_t se = h + 1 < nheads ? s_heads[h + 1] : SegmentEnd(a.keys, p1, end, key);
+      const TableDesc& T = s_t[key >> a.row_bits];
+      const uint64_t slot = key & row_mask;
+      const uint32_t dim = T.dim;
+      const uint64_t u = a.reduce ? a.occ2u[a.vals[sb]] : 0;
+      if (!kGeneric) {
+        const uint32_t c = lig * 4;
+        const bool active = c < dim;
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+        for (uint32_t base = sb; base < se; base += G) {
+          const uint32_t cnt = min(G, se - base);
+          const uint64_t my = lig < cnt ? a.rs[base + lig] : 0ull;
+          for (uint32_t k = 0; k < cnt; k += 4) {
+            float4 x[4];
+            float s[4];
+#pragma unroll
+            for (uint32_t q = 0; q < 4; ++q) {
+              const uint64_t w = __shfl(my, int(k + q), int(G));
+              const uint32_t ref = uint32_t(w);
+              s[q] = __uint_as_float(uint32_t(w >> 32));
+              const float* src = s_grad[ref >> kRefRowBits] +
+                                 uint64_t(ref & ((1u << kRefRowBits) - 1)) * dim + c;
+              x[q] = (k + q < cnt && active) ? Load4(src) : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (uint32_t q = 0; q < 4; ++q)
+              if (k + q < cnt) Accumulate4(acc, x[q], s[q]);
+          }
+        }
+        if (!active) continue;
+        if (a.reduce) {
+          if (!(Finite(acc.x) && Finite(acc.y) && Finite(acc.z) && Finite(acc.w)))
+            st.err |= EPS_HIP_STATUS_REDUCE_OVERFLOW;
+          Store4(a.reduce_out + u * a.reduce_stride + c, acc);
+        } else {
+          AdamRow4(T, slot, c, acc, write, st);
+        }
+      } else {
+        for (uint32_t c0 = 0; c0 < dim; c0 += kWave) {
+          const uint32_t c = c0 + lig;
+          const bool active = c < dim;
+          float acc = 0.f;
+          for (uint32_t base = sb; base < se; base += kWave) {
+            const uint32_t cnt = min(kWave, se - base);
+            const uint64_t my = lig < cnt ? a.rs[base + lig] : 0ull;
+            for (uint32_t k = 0; k < cnt; ++k) {
+              const uint64_t w = __shfl(my, int(k), int(kWave));
+              const uint32_t ref = uint32_t(w);
+              const float s = __uint_as_float(uint32_t(w >> 32));
+              const float* src = s_grad[ref >> kRefRowBits] +
+                                 uint64_t(ref & ((1u << kRefRowBits) - 1)) * dim;
+              const float x = active ? src[c] : 0.f;
+              acc = acc + x * s;
+            }
+          }
+          if (!active) continue;
+          if (a.reduce) {
+            if (!Finite(acc)) st.err |= EPS_HIP_STATUS_REDUCE_OVERFLOW;
+            a.reduce_out[u * a.reduce_stride + c] = acc;
+          } else {
+            AdamRow1(T, slot, c, acc, write, st);
+          }
+        }
+      }
+    }
+    __syncthreads();
+  }
+  FinishBlock(st, ctrl, a.bounds, write && !a.reduce);
+}
+
+// ---------------------------------------------------------------------------
+// Row driver: explicit unique rows (ApplyHost) or CSR references (ApplyCompact).
+struct RowArgs {
+  TableDesc t;
+  const uint64_t* slots;
+  const uint64_t* offsets;   // NULL: row r has exactly gradient row r (ApplyHost)
+  const uint64_t* sources;
+  const float* scales;
+  const float* src;
+  uint64_t rows;
+  Control* ctrl;
+  Bounds* bounds;
+  uint32_t log2g, vblocks, fallback;
+};
+
+template <bool kGeneric>
+__global__ void __launch_bounds__(kBlock) RowUpdateKernel(RowArgs a) {
+  Control* ctrl = a.ctrl;
+  const uint32_t mode = ctrl->mode;
+  bool write;
+  if (!a.fallback) {
+    if (mode == kReject) return;
+    write = mode == kFused;
+  } else {
+    if (mode != kChecked) return;
+    if (ctrl->status & kErrorBits) {
+      if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(&ctrl->status, EPS_HIP_STATUS_REJECTED);
+      return;
+    }
+    write = true;
+  }
+  const TableDesc T = a.t;
+  const uint32_t dim = T.dim;
+  const uint32_t G = kGeneric ? kWave : (1u << a.log2g);
+  const uint32_t lig = threadIdx.x & (G - 1);
+  const uint32_t gid = threadIdx.x / G, ngroups = kBlock / G;
+  RowStats st;
+  for (uint32_t vb = blockIdx.x; vb < a.vblocks; vb += gridDim.x) {
+    const uint64_t r = uint64_t(vb) * ngroups + gid;
+    if (r >= a.rows) continue;
+    const uint64_t slot = a.slots[r];
+    if (!kGeneric) {
+      const uint32_t c = lig * 4;
+      const bool active = c < dim;
+      float4 g;
+      if (!a.offsets) {
+        g = active ? Load4(a.src + r * dim + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+      } else {
+        g = make_float4(0.f, 0.f, 0.f, 0.f);
+        const uint64_t b = a.offsets[r], e = a.offsets[r + 1];
+        for (uint64_t j = b; j < e; ++j) {
+          const float s = a.scales[j];
+          const float4 x = active ? Load4(a.src + a.sources[j] * dim + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+          Accumulate4(g, x, s);
+        }
+      }
+      if (active) AdamRow4(T, slot, c, g, write, st);
+    } else {
+      for (uint32_t c = lig; c < dim; c += kWave) {
+        float g;
+        if (!a.offsets) {
+          g = a.src[r * dim + c];
+        } else {
+          g = 0.f;
+          for (uint64_t j = a.offsets[r]; j < a.offsets[r + 1]; ++j)
+            g = g + a.src[a.sources[j] * dim + c] * a.scales[j];
+        }
+        AdamRow1(T, slot, c, g, write, st);
+      }
+    }
+  }
+  FinishBlock(st, ctrl, a.bounds, write);
+}
+
+// ---------------------------------------------------------------------------
+TableDesc MakeTable(const eps_hip_table& t, const eps_hip_optimizer& o) {
+  TableDesc d;
+  d.state = t.state;
+  d.dim = t.dim;
+  d.beta1 = o.beta1;
+  d.beta2 = o.beta2;
+  d.omb1 = 1.0f - o.beta1;  // (1 - o.beta1) in float, lazy_adam.cpp:31
+  d.omb2 = 1.0f - o.beta2;
+  // lr_t in float exactly as lazy_adam.cpp:27 / cache_backend.cu:341.
+  d.lr = o.learning_rate * std::sqrt(1 - o.beta2_power) / (1 - o.beta1_power);
+  d.eps = o.epsilon;
+  d.lo = o.bounded ? o.weight_min : -FLT_MAX;
+  d.hi = o.bounded ? o.weight_max : FLT_MAX;
+  return d;
+}
+
+int CheckOptimizer(const eps_hip_optimizer& o) {
+  // UpdateContext validation, src/cuda/cache_backend.cu:321-325.
+  if (!(std::isfinite(o.learning_rate) && o.learning_rate > 0 && o.beta1_power >= 0 &&
+        o.beta1_power < 1 && o.beta2_power >= 0 && o.beta2_power < 1))
+    return Fail(EPS_HIP_INVALID_ARGUMENT, "invalid update context");
+  if (o.bounded && !(std::isfinite(o.weight_min) && std::isfinite(o.weight_max) &&
+                     o.weight_min <= o.weight_max))
+    return Fail(EPS_HIP_INVALID_ARGUMENT, "invalid optimizer weight bounds");
+  const float lr = o.learning_rate * std::sqrt(1 - o.beta2_power) / (1 - o.beta1_power);
+  if (!std::isfinite(lr)) return Fail(EPS_HIP_INVALID_ARGUMENT, "optimizer learning-rate overflow");
+  return EPS_HIP_OK;
+}
+
+uint32_t Log2G(uint32_t dim) {
+  uint32_t log2g = 2;
+  while ((1u << log2g) < dim / 4) ++log2g;
+  return log2g;
+}
+
+int LaunchGuard(GuardArgs& g, uint64_t blocks, hipStream_t s) {
+  if (!blocks) {  // nothing to scan: still decide (one block over an empty span)
+    g.span[0] = Span{nullptr, 0, 0, 0};
+    g.spans = 1;
+    blocks = 1;
+  }
+  hipLaunchKernelGGL(GradMaxKernel, dim3(unsigned(blocks)), dim3(kBlock), 0, s, g);
+  EPS_HIP_LAUNCHED("gradient guard");
+  return EPS_HIP_OK;
+}
+
+uint64_t SpanBlocks(uint64_t count) {
+  const uint64_t per = uint64_t(kBlock) * kMaxItems * 4;
+  return (count + per - 1) / per;
+}
+
+constexpr int kPrimary = 1, kSecond = 2;
+
+int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, uint32_t table_count,
+              const eps_hip_push_feature* features, uint32_t feature_count, const PushPlan& plan,
+              const PushLayout& L, uint8_t* ws, bool reduce, const uint64_t* occ2u, float* out,
+              uint64_t stride, Bounds* bounds, hipStream_t s, int phases) {
+  FusedArgs a{};
+  const bool in_b = plan.passes % 2 == 1;
+  a.keys = reinterpret_cast<const uint32_t*>(ws + (in_b ? L.keys_b : L.keys_a));
+  a.vals = reinterpret_cast<const uint32_t*>(ws + (in_b ? L.vals_b : L.vals_a));
+  a.rs = reinterpret_cast<const uint64_t*>(ws + L.sorted_rs);
+  a.occ2u = occ2u;
+  a.reduce_out = out;
+  a.reduce_stride = stride;
+  a.ctrl = reinterpret_cast<Control*>(ws);
+  a.bounds = bounds;
+  a.row_bits = plan.row_bits;
+  a.reduce = reduce ? 1 : 0;
+  a.tables = table_count;
+  for (uint32_t k = 0; k < table_count; ++k) {
+    const uint32_t t = plan.table_of_key[k];
+    eps_hip_optimizer o{};
+    if (optimizers) o = optimizers[t];
+    else { o.learning_rate = 1; o.beta1 = 0; o.beta2 = 0; o.epsilon = 1; }
+    a.t[k] = MakeTable(tables[t], o);
+  }
+  for (uint32_t f = 0; f < feature_count; ++f) a.grad[f] = features[f].gradients;
+  for (uint32_t cls = 0; cls < kClasses; ++cls) {
+    if (!plan.class_occurrences[cls]) continue;
+    a.cls = cls;
+    a.log2g = cls + 2;
+    a.ppb = PositionsPerBlock(cls);
+    const uint64_t vb = (plan.class_occurrences[cls] + a.ppb - 1) / a.ppb;
+    a.vblocks = uint32_t(vb);
+    auto kernel = cls == 5 ? SortedUpdateKernel<true> : SortedUpdateKernel<false>;
+    if (phases & kPrimary) {
+      a.fallback = 0;
+      hipLaunchKernelGGL(kernel, dim3(a.vblocks), dim3(kBlock), 0, s, a);
+      EPS_HIP_LAUNCHED("sorted update");
+    }
+    if (!reduce && (phases & kSecond)) {
+      a.fallback = 1;
+      hipLaunchKernelGGL(kernel, dim3(std::min<uint32_t>(a.vblocks, kFallbackGrid)), dim3(kBlock), 0,
+                         s, a);
+      EPS_HIP_LAUNCHED("sorted update (checked apply)");
+    }
+  }
+  return EPS_HIP_OK;
+}
+
+}  // namespace
+}  // namespace eps_hip
+
+using namespace eps_hip;
+
+extern "C" {
+
+// Shared validation of the push entry points.
+static int PushSetup(const eps_hip_table* tables, const eps_hip_optimizer* optimizers,
+                     uint32_t table_count, const eps_hip_push_feature* features,
+                     uint32_t feature_count, void* workspace, uint64_t workspace_bytes,
+                     void* bounds, PushPlan& plan) {
+  EPS_HIP_TRY(PlanPush(tables, table_count, features, feature_count, plan));
+  const PushLayout L(plan.occurrences);
+  if (!workspace || workspace_bytes < L.total)
+    return Fail(EPS_HIP_CAPACITY_EXCEEDED, "push workspace too small");
+  if (!optimizers || !bounds) return Fail(EPS_HIP_INVALID_ARGUMENT, "push needs optimizers and bounds");
+  for (uint32_t t = 0; t < table_count; ++t) EPS_HIP_TRY(CheckOptimizer(optimizers[t]));
+  for (uint32_t f = 0; f < feature_count; ++f) {
+    const auto& in = features[f];
+    const uint64_t rows = in.pooling == EPS_HIP_POOL_SEQUENCE ? in.occurrences : in.bags;
+    if (rows && !in.gradients) return Fail(EPS_HIP_INVALID_ARGUMENT, "null feature gradient");
+  }
+  return EPS_HIP_OK;
+}
+
+int eps_hip_push_begin(const eps_hip_table* tables, const eps_hip_optimizer* optimizers,
+                       uint32_t table_count, const eps_hip_push_feature* features,
+                       uint32_t feature_count, void* workspace, uint64_t workspace_bytes,
+                       void* bounds, void* stream) {
+  PushPlan plan;
+  EPS_HIP_TRY(PushSetup(tables, optimizers, table_count, features, feature_count, workspace,
+                        workspace_bytes, bounds, plan));
+  GuardArgs g{};
+  uint64_t blocks = 0;
+  for (uint32_t f = 0; f < feature_count; ++f) {
+    const auto& in = features[f];
+    const uint64_t rows = in.pooling == EPS_HIP_POOL_SEQUENCE ? in.occurrences : in.bags;
+    const uint64_t count = rows * tables[in.table].dim;
+    if (!count) continue;
+    g.span[g.spans++] = Span{in.gradients, count, uint32_t(blocks), 0};
+    blocks += SpanBlocks(count);
+  }
+  for (uint32_t t = 0; t < table_count; ++t) {
+    const TableDesc d = MakeTable(tables[t], optimizers[t]);
+    g.t[t] = GuardTable{optimizers[t].beta1, optimizers[t].beta2, d.lr, optimizers[t].epsilon};
+  }
+  g.tables = table_count;
+  g.reset_scale = 0;
+  g.use_prep_status = 1;
+  g.refs_host = 0;
+  g.ctrl = static_cast<Control*>(workspace);
+  g.bounds = static_cast<const Bounds*>(bounds);
+  return LaunchGuard(g, blocks, AsStream(stream));
+}
+
+static int PushPhase(const eps_hip_table* tables, const eps_hip_optimizer* optimizers,
+                     uint32_t table_count, const eps_hip_push_feature* features,
+                     uint32_t feature_count, void* workspace, uint64_t workspace_bytes,
+                     void* bounds, void* stream, int phase) {
+  PushPlan plan;
+  EPS_HIP_TRY(PushSetup(tables, optimizers, table_count, features, feature_count, workspace,
+                        workspace_bytes, bounds, plan));
+  if (!plan.occurrences) return EPS_HIP_OK;
+  const PushLayout L(plan.occurrences);
+  return RunSorted(tables, optimizers, table_count, features, feature_count, plan, L,
+                   static_cast<uint8_t*>(workspace), false, nullptr, nullptr, 0,
+                   static_cast<Bounds*>(bounds), AsStream(stream), phase);
+}
+
+int eps_hip_push_apply(const eps_hip_table* tables, const eps_hip_optimizer* optimizers,
+                       uint32_t table_count, const eps_hip_push_feature* features,
+                       uint32_t feature_count, void* workspace, uint64_t workspace_bytes,
+                       void* bounds, void* stream) {
+  return PushPhase(tables, optimizers, table_count, features, feature_count, workspace,
+                   workspace_bytes, bounds, stream, kPrimary);
+}
+
+int eps_hip_push_end(const eps_hip_table* tables, const eps_hip_optimizer* optimizers,
+                     uint32_t table_count, const eps_hip_push_feature* features,
+                     uint32_t feature_count, void* workspace, uint64_t workspace_bytes,
+                     void* bounds, void* stream) {
+  return PushPhase(tables, optimizers, table_count, features, feature_count, workspace,
+                   workspace_bytes, bounds, stream, kSecond);
+}
+
+int eps_hip_push(const eps_hip_table* tables, const eps_hip_optimizer* optimizers,
+                 uint32_t table_count, const eps_hip_push_feature* features,
+                 uint32_t feature_count, void* workspace, uint64_t workspace_bytes, void* bounds,
+                 void* stream) {
+  EPS_HIP_TRY(eps_hip_push_begin(tables, optimizers, table_count, features, feature_count,
+                                 workspace, workspace_bytes, bounds, stream));
+  EPS_HIP_TRY(eps_hip_push_apply(tables, optimizers, table_count, features, feature_count,
+                                 workspace, workspace_bytes, bounds, stream));
+  return eps_hip_push_end(tables, optimizers, table_count, features, feature_count, workspace,
+                          workspace_bytes, bounds, stream);
+}
+
+int eps_hip_reduce(const eps_hip_table* tables, uint32_t table_count,
+                   const eps_hip_push_feature* features, uint32_t feature_count,
+                   void* workspace, uint64_t workspace_bytes, const uint64_t* occurrence_to_unique,
+                   float* values, uint64_t row_stride, void* stream) {
+  PushPlan plan;
+  EPS_HIP_TRY(PlanPush(tables, table_count, features, feature_count, plan));
+  const PushLayout L(plan.occurrences);
+  if (!workspace || workspace_bytes < L.total)
+    return Fail(EPS_HIP_CAPACITY_EXCEEDED, "push workspace too small");
+  if (!occurrence_to_unique || !values) return Fail(EPS_HIP_INVALID_ARGUMENT, "null reduce buffers");
+  uint32_t max_dim = 0;
+  for (uint32_t t = 0; t < table_count; ++t) max_dim = std::max(max_dim, tables[t].dim);
+  if (row_stride < max_dim || (row_stride % 4 && max_dim % 4 == 0 && max_dim <= 256))
+    return Fail(EPS_HIP_INVALID_ARGUMENT, "row stride must cover every dimension (multiple of 4)");
+  if (!plan.occurrences) return EPS_HIP_OK;
+  auto* ws = static_cast<uint8_t*>(workspace);
+  return RunSorted(tables, nullptr, table_count, features, feature_count, plan, L, ws, true,
+                   occurrence_to_unique, values, row_stride, nullptr, AsStream(stream), kPrimary);
+}
+
+uint64_t eps_hip_update_workspace_bytes(void) { return sizeof(Control); }
+
+static int RunRows(const eps_hip_table* table, const eps_hip_optimizer* optimizer,
+                   const uint64_t* slots, uint64_t rows, const uint64_t* offsets,
+                   const uint64_t* sources, const float* scales, const float* src,
+                   uint64_t src_values, uint64_t references, void* workspace, void* bounds,
+                   void* stream) {
+  if (!table || !table->state || table->dim == 0 || table->dim > 65536)
+    return Fail(EPS_HIP_INVALID_ARGUMENT, "invalid update table");
+  if (!optimizer || !workspace || !bounds) return Fail(EPS_HIP_INVALID_ARGUMENT, "null update argument");
+  EPS_HIP_TRY(CheckOptimizer(*optimizer));
+  const hipStream_t s = AsStream(stream);
+  auto* ctrl = static_cast<Control*>(workspace);
+  EPS_HIP_TRY(LaunchFill(reinterpret_cast<uint32_t*>(ctrl), 0, sizeof(Control) / 4, s));
+  if (!rows) return EPS_HIP_OK;
+  if (!slots || !src) return Fail(EPS_HIP_INVALID_ARGUMENT, "null update buffers");
+  GuardArgs g{};
+  uint64_t blocks = 0;
+  if (src_values) {
+    g.span[g.spans++] = Span{src, src_values, 0, 0};
+    blocks += SpanBlocks(src_values);
+  }
+  if (scales && references) {
+    g.span[g.spans++] = Span{scales, references, uint32_t(blocks), 1};
+    blocks += SpanBlocks(references);
+  }
+  const TableDesc d = MakeTable(*table, *optimizer);
+  g.t[0] = GuardTable{optimizer->beta1, optimizer->beta2, d.lr, optimizer->epsilon};
+  g.tables = 1;
+  g.reset_scale = 1;
+  g.use_prep_status = 0;
+  g.refs_host = std::max<uint64_t>(1, offsets ? references : 1);
+  g.ctrl = ctrl;
+  g.bounds = static_cast<const Bounds*>(bounds);
+  EPS_HIP_TRY(LaunchGuard(g, blocks, s));
+  RowArgs a{};
+  a.t = d;
+  a.slots = slots;
+  a.offsets = offsets;
+  a.sources = sources;
+  a.scales = scales;
+  a.src = src;
+  a.rows = rows;
+  a.ctrl = ctrl;
+  a.bounds = static_cast<Bounds*>(bounds);
+  const uint32_t cls = DimClass(table->dim);
+  const bool generic = cls == 5 || reinterpret_cast<uintptr_t>(src) % 16 != 0;
+  a.log2g = generic ? 6 : Log2G(table->dim);
+  const uint32_t groups = kBlock >> a.log2g;
+  const uint64_t vb = (rows + groups - 1) / groups;
+  if (vb > 0xffffffffull) return Fail(EPS_HIP_CAPACITY_EXCEEDED, "too many rows");
+  a.vblocks = uint32_t(vb);
+  auto kernel = generic ? RowUpdateKernel<true> : RowUpdateKernel<false>;
+  a.fallback = 0;
+  hipLaunchKernelGGL(kernel, dim3(a.vblocks), dim3(kBlock), 0, s, a);
+  EPS_HIP_LAUNCHED("row update");
+  a.fallback = 1;
+  hipLaunchKernelGGL(kernel, dim3(std::min<uint32_t>(a.vblocks, kFallbackGrid)), dim3(kBlock), 0, s, a);
+  EPS_HIP_LAUNCHED("row update (checked apply)");
+  return EPS_HIP_OK;
+}
+
+int eps_hip_adam_rows(const eps_hip_table* table, const eps_hip_optimizer* optimizer,
+                      const uint64_t* slots, const float* gradients, uint64_t rows,
+                      void* workspace, void* bounds, void* stream) {
+  const uint64_t values = table ? rows * table->dim : 0;
+  return RunRows(table, optimizer, slots, rows, nullptr, nullptr, nullptr, gradients, values,
+                 0, workspace, bounds, stream);
+}
+
+int eps_hip_adam_compact(const eps_hip_table* table, const eps_hip_optimizer* optimizer,
+                         const uint64_t* slots, uint64_t rows, const uint64_t* row_offsets,
+                         const uint64_t* source_rows, const float* scales,
+                         const float* source_values, uint64_t source_count, uint64_t references,
+                         void* workspace, void* bounds, void* stream) {
+  if (rows && (!row_offsets || (references && (!source_rows || !scales))))
+    return Fail(EPS_HIP_INVALID_ARGUMENT, "null compact buffers");
+  const uint64_t values = table ? source_count * table->dim : 0;
+  return RunRows(table, optimizer, slots, rows, row_offsets, source_rows, scales, source_values,
+                 values, references, workspace, bounds, stream);
+}
+
+uint32_t* eps_hip_status_word(void* workspace) {
+  return workspace ? &static_cast<Control*>(workspace)->status : nullptr;
+}
+
+int eps_hip_read_status(void* workspace, uint32_t* status, void* stream) {
+  if (!workspace || !status) return Fail(EPS_HIP_INVALID_ARGUMENT, "null status arguments");
+  EPS_HIP_TRY(Check(hipStreamSynchronize(AsStream(stream)), "hipStreamSynchronize"));
+  EPS_HIP_TRY(Check(hipMemcpy(status, &static_cast<Control*>(workspace)->status, 4,
+                              hipMemcpyDeviceToHost), "status copy"));
+  return EPS_HIP_OK;
+}
+
+}  // extern "C"

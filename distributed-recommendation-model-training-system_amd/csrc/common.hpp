@@ -1,0 +1,102 @@
+// common.hpp -- shared definitions of the gfx950 kernel library (libeps_hip.so).
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "eps_hip.h"
+
+namespace eps_hip {
+
+constexpr uint32_t kBlock = 256;          // 4 wavefronts of 64
+constexpr uint32_t kWave = 64;
+constexpr uint64_t kHole = ~0ull;         // "row not on this device" (UINT64_MAX)
+constexpr uint32_t kBoundSlots = 64;      // spread of the bound atomics
+constexpr uint32_t kSortTile = 4096;      // keys per radix-sort tile (256 x 16)
+constexpr uint32_t kSortItems = 16;
+constexpr uint32_t kMaxPasses = 4;
+constexpr uint32_t kKeygenItems = 4;      // occurrences per keygen thread
+constexpr uint32_t kClasses = 6;          // 5 vector widths + generic
+constexpr uint32_t kRefRowBits = 27;      // gradient row bits in a reference word
+
+// Control block at offset 0 of a push or update workspace (256 bytes).
+struct Control {
+  uint32_t status;          // result of the last push/update (0 = applied)
+  uint32_t prep_status;     // prepare-time findings (bad slots)
+  uint32_t max_src_bits;    // max |gradient| as float bits (self-resetting)
+  uint32_t max_scale_bits;  // max |scale| of the prepared references
+  uint32_t valid_count;     // prepared occurrences that are on this device
+  uint32_t mode;            // guard decision of the last push
+  uint32_t done_counter;    // last-block detection (self-resetting)
+  uint32_t unique_count;
+  uint32_t tile_counter[kMaxPasses];
+  uint32_t class_count[8];
+  uint32_t pad[44];
+};
+static_assert(sizeof(Control) == 256, "control block is 256 bytes");
+
+enum Mode : uint32_t { kFused = 0, kChecked = 1, kReject = 2 };
+
+// Bounds domain: kBoundSlots x {W, M, V, unused} as non-negative float bits.
+struct Bounds { uint32_t v[kBoundSlots][4]; };
+
+// Workspace layout of a push, for `n` occurrences.
+struct PushLayout {
+  uint64_t n, tiles;
+  uint64_t hist, look, keys_a, keys_b, vals_a, vals_b, refscale, sorted_rs, flags, ranks,
+      block_sums, total;
+  explicit PushLayout(uint64_t occurrences) {
+    n = occurrences;
+    tiles = (n + kSortTile - 1) / kSortTile;
+    auto align = [](uint64_t x) { return (x + 255) & ~uint64_t(255); };
+    uint64_t at = sizeof(Control);
+    hist = at; at = align(at + kMaxPasses * 256 * 4);
+    look = at; at = align(at + kMaxPasses * tiles * 256 * 4);
+    keys_a = at; at = align(at + n * 4);
+    keys_b = at; at = align(at + n * 4);
+    vals_a = at; at = align(at + n * 4);
+    vals_b = at; at = align(at + n * 4);
+    refscale = at; at = align(at + n * 8);
+    sorted_rs = at; at = align(at + n * 8);
+    flags = at; at = align(at + n * 4);
+    ranks = at; at = align(at + n * 4);
+    block_sums = at; at = align(at + ((n + 1023) / 1024 + 1) * 4);
+    total = at;
+  }
+};
+
+// ---- host-side error plumbing ----
+void SetError(const std::string& message);
+int Fail(int code, const std::string& message);
+int Check(hipError_t e, const char* what);
+#define EPS_HIP_TRY(expr) do { int rc_ = (expr); if (rc_) return rc_; } while (0)
+#define EPS_HIP_LAUNCHED(what) EPS_HIP_TRY(::eps_hip::Check(hipGetLastError(), what))
+
+inline hipStream_t AsStream(void* s) { return static_cast<hipStream_t>(s); }
+
+// ---- device helpers ----
+__device__ __forceinline__ float4 Load4(const float* p) {
+  return *reinterpret_cast<const float4*>(p);
+}
+__device__ __forceinline__ void Store4(float* p, float4 v) {
+  *reinterpret_cast<float4*>(p) = v;
+}
+__device__ __forceinline__ uint32_t AbsBits(float x) { return __float_as_uint(x) & 0x7fffffffu; }
+__device__ __forceinline__ bool Finite(float x) { return AbsBits(x) < 0x7f800000u; }
+
+// Maximum over the lanes of a wavefront (DPP/permute lowering by the compiler).
+__device__ __forceinline__ uint32_t WaveMax(uint32_t x) {
+#pragma unroll
+  for (int offset = 32; offset > 0; offset >>= 1) x = max(x, (uint32_t)__shfl_xor((int)x, offset));
+  return x;
+}
+
+// BoundWeight (src/common/optimizer_bounds.hpp:14-18) written as std::clamp so
+// signed zeros match the CPU exactly.
+__device__ __forceinline__ float Clamp(float v, float lo, float hi) {
+  return v < lo ? lo : (hi < v ? hi : v);
+}
+
+}  // namespace eps_hip

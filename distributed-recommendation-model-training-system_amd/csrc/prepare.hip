@@ -1,0 +1,546 @@
+// prepare.hip -- device-side dedup of pushed occurrences by row.
+//
+// The reference dedups on the host with a hash map in first-occurrence order
+// (PrepareFeature, src/access/batch_access.cpp:32-36; ReduceGradients, :73-93)
+// and ships either reduced rows or a host-built CSR to the device
+// (BuildCompactGradients, src/access/compact_gradients.cpp:43-72).  Here the
+// grouping is a stable LSD radix sort of 32-bit keys (key index << row_bits |
+// slot) carrying the occurrence index, so equal rows end up adjacent in
+// occurrence order -- exactly the CSR order of the reference's references
+// (repeats kept, (feature, bag, position) order).
+//
+//   keygen : one pass over the occurrences -> key, occurrence index, packed
+//            (gradient row | scale) reference word, all-pass digit histograms,
+//            per-class valid counts, max |scale|.
+//   passes : onesweep (single pass per digit): per-tile stable ranking with
+//            wavefront ballots, decoupled look-back across tiles for the digit
+//            prefix, LDS-staged scatter so each digit run is written
+//            contiguously.  The last pass also scatters the reference words.
+//   unique : first-occurrence ranks (PrepareFeature's unique order) from a
+//            head-flag scan in occurrence space.
+#include "prepare.hpp"
+
+#include <algorithm>
+
+namespace eps_hip {
+
+int LaunchFill(uint32_t* target, uint32_t value, uint64_t count, hipStream_t stream);
+
+namespace {
+
+constexpr uint32_t kFlagAggregate = 1u << 30;
+constexpr uint32_t kFlagInclusive = 2u << 30;
+constexpr uint32_t kValueMask = (1u << 30) - 1;
+
+struct PrepFeature {
+  const uint64_t* indices;
+  const uint64_t* offsets;
+  const uint64_t* lengths;
+  const float* weights;
+  uint64_t occ_begin, occurrences, bags, table_rows;
+  uint32_t key_index, pooling, block_begin, feature;
+};
+struct PrepArgs {
+  PrepFeature f[EPS_HIP_MAX_FEATURES];
+  uint32_t count, row_bits, sentinel, passes;
+  uint32_t shift[kMaxPasses], bits[kMaxPasses];
+  uint32_t class_start[kClasses + 1];
+  Control* ctrl;
+  uint32_t* hist;
+  uint32_t* keys;
+  uint32_t* vals;
+  uint64_t* refscale;
+};
+
+__device__ __forceinline__ uint64_t BagOf(const uint64_t* offsets, uint64_t bags, uint64_t i) {
+  // Largest b with offsets[b] <= i (upper_bound - 1); empty bags are skipped.
+  uint64_t lo = 0, hi = bags;  // answer in [lo, hi)
+  while (hi - lo > 1) {
+    const uint64_t mid = (lo + hi) >> 1;
+    if (offsets[mid] <= i) lo = mid; else hi = mid;
+  }
+  return lo;
+}
+
+__global__ void __launch_bounds__(kBlock) KeygenKernel(PrepArgs args) {
+  PrepFeature f = args.f[0];
+  uint32_t fi = 0;
+#pragma unroll
+  for (uint32_t i = 1; i < EPS_HIP_MAX_FEATURES; ++i)
+    if (i < args.count && blockIdx.x >= args.f[i].block_begin) { f = args.f[i]; fi = i; }
+  (void)fi;
+  __shared__ uint32_t s_hist[kMaxPasses][256];
+  __shared__ uint32_t s_class[8];
+  __shared__ uint32_t s_misc[2];  // [0] bad, [1] max scale
+  for (uint32_t i = threadIdx.x; i < kMaxPasses * 256; i += kBlock) (&s_hist[0][0])[i] = 0;
+  if (threadIdx.x < 8) s_class[threadIdx.x] = 0;
+  if (threadIdx.x < 2) s_misc[threadIdx.x] = 0;
+  __syncthreads();
+
+  uint32_t cls = 0;
+  while (cls + 1 < kClasses && f.key_index >= args.class_start[cls + 1]) ++cls;
+  const uint64_t local0 = uint64_t(blockIdx.x - f.block_begin) * (kBlock * kKeygenItems);
+  uint32_t valid = 0, scale_max = 0;
+  bool bad = false;
+  for (uint32_t k = 0; k < kKeygenItems; ++k) {
+    const uint64_t li = local0 + k * kBlock + threadIdx.x;
+    if (li >= f.occurrences) break;
+    const uint64_t gi = f.occ_begin + li;
+    uint64_t slot = f.indices[li];
+    if (slot != kHole && slot >= f.table_rows) { bad = true; slot = kHole; }
+    uint32_t key = args.sentinel;
+    if (slot != kHole) { key = (f.key_index << args.row_bits) | uint32_t(slot); ++valid; }
+    uint64_t row;
+    float scale = 1.0f;
+    if (f.pooling == EPS_HIP_POOL_SEQUENCE) {
+      row = li;
+    } else {
+      row = BagOf(f.offsets, f.bags, li);
+      if (f.pooling == EPS_HIP_POOL_MEAN) {
+        const uint64_t len = f.lengths[row];
+        if (len) scale = 1.0f / (float)len;  // batch_access.cpp:79-80
+      } else if (f.pooling == EPS_HIP_POOL_WEIGHTED_SUM) {
+        scale = f.weights[li];
+      }
+    }
+    if (slot != kHole) scale_max = max(scale_max, AbsBits(scale));
+    args.keys[gi] = key;
+    args.vals[gi] = uint32_t(gi);
+    args.refscale[gi] = (uint64_t(__float_as_uint(scale)) << 32) |
+                        (uint64_t(f.feature) << kRefRowBits) | row;
+    for (uint32_t p = 0; p < args.passes; ++p)
+      atomicAdd(&s_hist[p][(key >> args.shift[p]) & ((1u << args.bits[p]) - 1)], 1u);
+  }
+  if (valid) atomicAdd(&s_class[cls], valid);
+  if (bad) s_misc[0] = 1;
+  scale_max = WaveMax(scale_max);
+  if ((threadIdx.x & (kWave - 1)) == 0 && scale_max) atomicMax(&s_misc[1], scale_max);
+  __syncthreads();
+  for (uint32_t i = threadIdx.x; i < args.passes * 256; i += kBlock) {
+    const uint32_t c = (&s_hist[0][0])[i];
+    if (c) atomicAdd(args.hist + i, c);
+  }
+  if (threadIdx.x < kClasses && s_class[threadIdx.x]) {
+    atomicAdd(&args.ctrl->class_count[threadIdx.x], s_class[threadIdx.x]);
+    atomicAdd(&args.ctrl->valid_count, s_class[threadIdx.x]);
+  }
+  if (threadIdx.x == 0) {
+    if (s_misc[0]) atomicOr(&args.ctrl->prep_status, EPS_HIP_STATUS_BAD_INDEX);
+    if (s_misc[1]) atomicMax(&args.ctrl->max_scale_bits, s_misc[1]);
+  }
+}
+
+// Exclusive scan of one value per thread over a 256-thread block.
+__device__ __forceinline__ uint32_t BlockExclusiveScan(uint32_t x, uint32_t* s_wave) {
+  const uint32_t lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  uint32_t inc = x;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = __shfl_up(inc, o);
+    if (lane >= uint32_t(o)) inc += y;
+  }
+  if (lane == kWave - 1) s_wave[wave] = inc;
+  __syncthreads();
+  uint32_t before = 0;
+  for (uint32_t w = 0; w < wave; ++w) before += s_wave[w];
+  __syncthreads();
+  return before + inc - x;
+}
+
+template <bool kLast>
+__global__ void __launch_bounds__(kBlock) RadixPassKernel(
+    const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
+    uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out,
+    const uint64_t* __restrict__ refscale, uint64_t* __restrict__ sorted_rs, uint32_t n,
+    uint32_t shift, uint32_t bits, const uint32_t* __restrict__ hist, uint32_t* look,
+    uint32_t* tile_counter) {
+  __shared__ uint32_t s_tile;
+  __shared__ uint32_t s_wcount[4][256];
+  __shared__ uint32_t s_tile_start[256];
+  __shared__ uint32_t s_global[256];
+  __shared__ uint32_t s_scan[4];
+  __shared__ uint32_t s_keys[kSortTile];
+  __shared__ uint32_t s_vals[kSortTile];
+
+  const uint32_t t = threadIdx.x, lane = t & (kWave - 1), wave = t / kWave;
+  if (t == 0) s_tile = atomicAdd(tile_counter, 1u);
+  for (uint32_t i = t; i < 4 * 256; i += kBlock) (&s_wcount[0][0])[i] = 0;
+  __syncthreads();
+  const uint32_t tile = s_tile;
+  const uint32_t mask = (1u << bits) - 1;
+  const uint32_t base = tile * kSortTile + wave * (kSortTile / 4);
+  uint32_t key[kSortItems], val[kSortItems], rank[kSortItems];
+#pragma unroll
+  for (uint32_t i = 0; i < kSortItems; ++i) {
+    const uint32_t p = base + i * kWave + lane;
+    key[i] = p < n ? keys_in[p] : 0u;
+    val[i] = p < n ? vals_in[p] : 0u;
+  }
+  const uint64_t lt_mask = (1ull << lane) - 1;
+#pragma unroll
+  for (uint32_t i = 0; i < kSortItems; ++i) {
+    const uint32_t p = base + i * kWave + lane;
+    const bool valid = p < n;
+    const uint32_t digit = (key[i] >> shift) & mask;
+    uint64_t match = __ballot(valid);
+    for (uint32_t b = 0; b < bits; ++b) {
+      const bool bit = (digit >> b) & 1u;
+      const uint64_t ones = __ballot(bit);
+      match &= bit ? ones : ~ones;
+    }
+    rank[i] = 0;
+    if (valid) {
+      const uint32_t before = s_wcount[wave][digit];
+      rank[i] = before + uint32_t(__popcll(match & lt_mask));
+      if (lane == uint32_t(__ffsll((unsigned long long)match) - 1))
+        s_wcount[wave][digit] = before + uint32_t(__popcll(match));
+    }
+  }
+  __syncthreads();
+  // Per digit (one per thread): wave prefixes, tile total, look-back.
+  const uint32_t d = t;
+  uint32_t total = 0;
+#pragma unroll
+  for (uint32_t w = 0; w < 4; ++w) {
+    const uint32_t c = s_wcount[w][d];
+    s_wcount[w][d] = total;
+    total += c;
+  }
+  uint32_t* mine = look + uint64_t(tile) * 256 + d;
+  uint32_t exclusive = 0;
+  if (tile == 0) {
+    __hip_atomic_store(mine, kFlagInclusive | total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    __hip_atomic_store(mine, kFlagAggregate | total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    int64_t j = int64_t(tile) - 1;
+    while (j >= 0) {
+      const uint32_t v = __hip_atomic_load(look + uint64_t(j) * 256 + d, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t flag = v & ~kValueMask;
+      if (flag == 0) continue;  // predecessor tile has not published yet
+      exclusive += v & kValueMask;
+      if (flag == kFlagInclusive) break;
+      --j;
+    }
+    __hip_atomic_store(mine, kFlagInclusive | (exclusive + total), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  }
+  const uint32_t digit_base = BlockExclusiveScan(hist[d], s_scan);
+  const uint32_t tile_start = BlockExclusiveScan(total, s_scan);
+  s_tile_start[d] = tile_start;
+  s_global[d] = digit_base + exclusive;
+  __syncthreads();
+#pragma unroll
+  for (uint32_t i = 0; i < kSortItems; ++i) {
+    const uint32_t p = base + i * kWave + lane;
+    if (p < n) {
+      const uint32_t digit = (key[i] >> shift) & mask;
+      const uint32_t at = s_tile_start[digit] + s_wcount[wave][digit] + rank[i];
+      s_keys[at] = key[i];
+      s_vals[at] = val[i];
+    }
+  }
+  __syncthreads();
+  const uint32_t tile_n = min(kSortTile, n - tile * kSortTile);
+  for (uint32_t q = t; q < tile_n; q += kBlock) {
+    const uint32_t k = s_keys[q];
+    const uint32_t digit = (k >> shift) & mask;
+    const uint32_t dest = s_global[digit] + (q - s_tile_start[digit]);
+    keys_out[dest] = k;
+    vals_out[dest] = s_vals[q];
+    if (kLast) sorted_rs[dest] = refscale[s_vals[q]];
+  }
+}
+
+// ---- first-occurrence ranking ----
+__global__ void HeadFlagKernel(const uint32_t* keys, const uint32_t* vals, const Control* ctrl,
+                               uint32_t* flags, uint32_t n) {
+  const uint32_t valid = ctrl->valid_count;
+  for (uint32_t p = blockIdx.x * blockDim.x + threadIdx.x; p < n && p < valid;
+       p += blockDim.x * gridDim.x)
+    if (p == 0 || keys[p] != keys[p - 1]) flags[vals[p]] = 1;
+}
+
+__global__ void ScanBlockSumsKernel(const uint32_t* flags, uint32_t* block_sums, uint32_t n) {
+  __shared__ uint32_t s_wave[4];
+  const uint32_t b = blockIdx.x;
+  uint32_t sum = 0;
+  for (uint32_t k = 0; k < 4; ++k) {
+    const uint32_t i = b * 1024 + k * kBlock + threadIdx.x;
+    if (i < n) sum += flags[i];
+  }
+  const uint32_t lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  for (int o = 32; o > 0; o >>= 1) sum += __shfl_xor(sum, o);
+  if (lane == 0) s_wave[wave] = sum;
+  __syncthreads();
+  if (threadIdx.x == 0) block_sums[b] = s_wave[0] + s_wave[1] + s_wave[2] + s_wave[3];
+}
+
+__global__ void ScanTopKernel(uint32_t* block_sums, uint32_t blocks, Control* ctrl,
+                              uint64_t* unique_count) {
+  __shared__ uint32_t s_scan[4];
+  __shared__ uint32_t s_carry;
+  if (threadIdx.x == 0) s_carry = 0;
+  __syncthreads();
+  for (uint32_t start = 0; start < blocks; start += kBlock) {
+    const uint32_t i = start + threadIdx.x;
+    const uint32_t x = i < blocks ? block_sums[i] : 0;
+    const uint32_t ex = BlockExclusiveScan(x, s_scan);
+    const uint32_t carry = s_carry;
+    if (i < blocks) block_sums[i] = carry + ex;
+    __syncthreads();
+    if (threadIdx.x == kBlock - 1) s_carry = carry + ex + x;
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    ctrl->unique_count = s_carry;
+    if (unique_count) *unique_count = s_carry;
+  }
+}
+
+__global__ void ScanApplyKernel(const uint32_t* flags, const uint32_t* block_sums, uint32_t* ranks,
+                                uint32_t n) {
+  __shared__ uint32_t s_scan[4];
+  __shared__ uint32_t s_carry;
+  const uint32_t b = blockIdx.x;
+  if (threadIdx.x == 0) s_carry = block_sums[b];
+  __syncthreads();
+  for (uint32_t k = 0; k < 4; ++k) {
+    const uint32_t i = b * 1024 + k * kBlock + threadIdx.x;
+    const uint32_t x = i < n ? flags[i] : 0;
+    const uint32_t ex = BlockExclusiveScan(x, s_scan);
+    const uint32_t carry = s_carry;
+    if (i < n) ranks[i] = carry + ex;
+    __syncthreads();
+    if (threadIdx.x == kBlock - 1) s_carry = carry + ex + x;
+    __syncthreads();
+  }
+}
+
+struct UniqueArgs {
+  uint32_t table_of_key[EPS_HIP_MAX_TABLES];
+};
+
+__global__ void UniqueWriteKernel(const uint32_t* keys, const uint32_t* vals, const uint32_t* ranks,
+                                  const Control* ctrl, uint32_t n, uint32_t row_bits,
+                                  UniqueArgs args, uint64_t* unique_slots, uint32_t* unique_tables,
+                                  uint64_t* occurrence_to_unique) {
+  const uint32_t valid = ctrl->valid_count;
+  __shared__ uint32_t s_table[EPS_HIP_MAX_TABLES];
+#pragma unroll
+  for (uint32_t i = 0; i < EPS_HIP_MAX_TABLES; ++i)
+    if (threadIdx.x == i) s_table[i] = args.table_of_key[i];
+  __syncthreads();
+  for (uint32_t p = blockIdx.x * blockDim.x + threadIdx.x; p < n && p < valid;
+       p += blockDim.x * gridDim.x) {
+    const uint32_t key = keys[p];
+    uint32_t lo = 0, hi = p;  // first index with this key (lower bound) in [lo, hi]
+    while (lo < hi) {
+      const uint32_t mid = (lo + hi) >> 1;
+      if (keys[mid] < key) lo = mid + 1; else hi = mid;
+    }
+    const uint32_t u = ranks[vals[lo]];
+    occurrence_to_unique[vals[p]] = u;
+    if (lo == p) {
+      unique_slots[u] = key & ((1u << row_bits) - 1);
+      unique_tables[u] = s_table[key >> row_bits];
+    }
+  }
+}
+
+unsigned Grid(uint64_t n, unsigned cap) {
+  const uint64_t b = (n + kBlock - 1) / kBlock;
+  return unsigned(std::max<uint64_t>(1, std::min<uint64_t>(b, cap)));
+}
+
+uint32_t BitLength(uint64_t x) {
+  uint32_t b = 0;
+  while (x) { ++b; x >>= 1; }
+  return b;
+}
+
+}  // namespace
+
+int PlanPush(const eps_hip_table* tables, uint32_t table_count,
+             const eps_hip_push_feature* features, uint32_t feature_count, PushPlan& plan) {
+  if (!tables || table_count == 0 || table_count > EPS_HIP_MAX_TABLES)
+    return Fail(EPS_HIP_INVALID_ARGUMENT, "push needs 1..32 tables");
+  if (!features || feature_count == 0 || feature_count > EPS_HIP_MAX_FEATURES)
+    return Fail(EPS_HIP_INVALID_ARGUMENT, "push needs 1..32 features");
+  uint64_t max_rows = 1;
+  for (uint32_t t = 0; t < table_count; ++t) {
+    if (!tables[t].state || tables[t].dim == 0 || tables[t].dim > 65536)
+      return Fail(EPS_HIP_INVALID_ARGUMENT, "invalid push table");
+    if (reinterpret_cast<uintptr_t>(tables[t].state) % 16)
+      return Fail(EPS_HIP_INVALID_ARGUMENT, "table state must be 16-byte aligned");
+    max_rows = std::max<uint64_t>(max_rows, tables[t].rows);
+  }
+  plan.row_bits = std::max<uint32_t>(1, BitLength(max_rows - 1));
+  // Table key indices ordered by dimension class, so each class is one
+  // contiguous range of the sorted keys.
+  std::vector<uint32_t> order(table_count);
+  for (uint32_t t = 0; t < table_count; ++t) order[t] = t;
+  std::stable_sort(order.begin(), order.end(), [&](uint32_t a, uint32_t b) {
+    return DimClass(tables[a].dim) < DimClass(tables[b].dim);
+  });
+  plan.key_index.assign(table_count, 0);
+  plan.table_of_key = order;
+  for (uint32_t k = 0; k < table_count; ++k) plan.key_index[order[k]] = k;
+  for (uint32_t c = 0; c <= kClasses; ++c) {
+    uint32_t k = 0;
+    while (k < table_count && DimClass(tables[order[k]].dim) < c) ++k;
+    plan.class_start[c] = k;
+  }
+  const uint64_t max_valid = (uint64_t(table_count - 1) << plan.row_bits) | (max_rows - 1);
+  plan.key_bits = BitLength(max_valid + 1);
+  if (plan.key_bits > 32) return Fail(EPS_HIP_CAPACITY_EXCEEDED, "table rows exceed 32-bit sort keys");
+  plan.passes = (plan.key_bits + 7) / 8;
+  uint32_t at = 0;
+  for (uint32_t p = 0; p < plan.passes; ++p) {
+    const uint32_t remaining = plan.key_bits - at, left = plan.passes - p;
+    plan.bits[p] = (remaining + left - 1) / left;
+    plan.shift[p] = at;
+    at += plan.bits[p];
+  }
+  plan.occurrences = 0;
+  plan.class_occurrences.fill(0);
+  for (uint32_t i = 0; i < feature_count; ++i) {
+    const auto& f = features[i];
+    if (f.table >= table_count || f.pooling > EPS_HIP_POOL_WEIGHTED_SUM)
+      return Fail(EPS_HIP_INVALID_ARGUMENT, "invalid push feature");
+    if (f.occurrences && !f.indices) return Fail(EPS_HIP_INVALID_ARGUMENT, "null feature indices");
+    if (f.pooling != EPS_HIP_POOL_SEQUENCE && (!f.offsets || (f.pooling == EPS_HIP_POOL_MEAN && !f.valid_lengths)))
+      return Fail(EPS_HIP_INVALID_ARGUMENT, "pooled feature needs offsets (and lengths for mean)");
+    if (f.pooling == EPS_HIP_POOL_WEIGHTED_SUM && f.occurrences && !f.weights)
+      return Fail(EPS_HIP_INVALID_ARGUMENT, "weighted feature needs weights");
+    const uint64_t rows = f.pooling == EPS_HIP_POOL_SEQUENCE ? f.occurrences : f.bags;
+    if (rows >= (1ull << kRefRowBits)) return Fail(EPS_HIP_CAPACITY_EXCEEDED, "feature has too many rows");
+    plan.occurrences += f.occurrences;
+    plan.class_occurrences[DimClass(tables[f.table].dim)] += f.occurrences;
+  }
+  if (plan.occurrences >= (1ull << 30)) return Fail(EPS_HIP_CAPACITY_EXCEEDED, "too many occurrences");
+  return EPS_HIP_OK;
+}
+
+// Final sorted buffers after `passes` passes starting from A.
+inline bool SortedInB(uint32_t passes) { return passes % 2 == 1; }
+
+}  // namespace eps_hip
+
+using namespace eps_hip;
+
+extern "C" {
+
+uint64_t eps_hip_push_workspace_bytes(uint64_t occurrences) {
+  return PushLayout(occurrences).total;
+}
+
+int eps_hip_prepare(const eps_hip_table* tables, uint32_t table_count,
+                    const eps_hip_push_feature* features, uint32_t feature_count,
+                    void* workspace, uint64_t workspace_bytes, void* stream) {
+  PushPlan plan;
+  EPS_HIP_TRY(PlanPush(tables, table_count, features, feature_count, plan));
+  const PushLayout L(plan.occurrences);
+  if (!workspace || workspace_bytes < L.total)
+    return Fail(EPS_HIP_CAPACITY_EXCEEDED, "push workspace too small");
+  auto* ws = static_cast<uint8_t*>(workspace);
+  auto* ctrl = reinterpret_cast<Control*>(ws);
+  const hipStream_t s = AsStream(stream);
+  // Control block, histograms and look-back flags start at zero.
+  EPS_HIP_TRY(LaunchFill(reinterpret_cast<uint32_t*>(ws), 0, L.keys_a / 4, s));
+  if (!plan.occurrences) return EPS_HIP_OK;
+
+  PrepArgs args{};
+  args.count = feature_count;
+  args.row_bits = plan.row_bits;
+  args.sentinel = plan.key_bits >= 32 ? 0xffffffffu : ((1u << plan.key_bits) - 1);
+  args.passes = plan.passes;
+  for (uint32_t p = 0; p < kMaxPasses; ++p) { args.shift[p] = plan.shift[p]; args.bits[p] = plan.bits[p]; }
+  for (uint32_t c = 0; c <= kClasses; ++c) args.class_start[c] = plan.class_start[c];
+  args.ctrl = ctrl;
+  args.hist = reinterpret_cast<uint32_t*>(ws + L.hist);
+  args.keys = reinterpret_cast<uint32_t*>(ws + L.keys_a);
+  args.vals = reinterpret_cast<uint32_t*>(ws + L.vals_a);
+  args.refscale = reinterpret_cast<uint64_t*>(ws + L.refscale);
+  uint64_t occ = 0, blocks = 0;
+  for (uint32_t i = 0; i < feature_count; ++i) {
+    const auto& in = features[i];
+    PrepFeature& f = args.f[i];
+    f.indices = in.indices; f.offsets = in.offsets; f.lengths = in.valid_lengths;
+    f.weights = in.weights; f.occ_begin = occ; f.occurrences = in.occurrences; f.bags = in.bags;
+    f.table_rows = tables[in.table].rows; f.key_index = plan.key_index[in.table];
+    f.pooling = in.pooling; f.feature = i; f.block_begin = uint32_t(blocks);
+    occ += in.occurrences;
+    blocks += (in.occurrences + kBlock * kKeygenItems - 1) / (kBlock * kKeygenItems);
+  }
+  if (blocks) {
+    hipLaunchKernelGGL(KeygenKernel, dim3(unsigned(blocks)), dim3(kBlock), 0, s, args);
+    EPS_HIP_LAUNCHED("keygen");
+  }
+  uint32_t* keys[2] = {reinterpret_cast<uint32_t*>(ws + L.keys_a), reinterpret_cast<uint32_t*>(ws + L.keys_b)};
+  uint32_t* vals[2] = {reinterpret_cast<uint32_t*>(ws + L.vals_a), reinterpret_cast<uint32_t*>(ws + L.vals_b)};
+  auto* look = reinterpret_cast<uint32_t*>(ws + L.look);
+  const uint32_t n = uint32_t(plan.occurrences);
+  for (uint32_t p = 0; p < plan.passes; ++p) {
+    const bool last = p + 1 == plan.passes;
+    auto kernel = last ? RadixPassKernel<true> : RadixPassKernel<false>;
+    hipLaunchKernelGGL(kernel, dim3(unsigned(L.tiles)), dim3(kBlock), 0, s, keys[p % 2], vals[p % 2],
+                       keys[(p + 1) % 2], vals[(p + 1) % 2],
+                       reinterpret_cast<const uint64_t*>(ws + L.refscale),
+                       reinterpret_cast<uint64_t*>(ws + L.sorted_rs), n, plan.shift[p], plan.bits[p],
+                       args.hist + p * 256, look + uint64_t(p) * L.tiles * 256,
+                       &ctrl->tile_counter[p]);
+    EPS_HIP_LAUNCHED("radix pass");
+  }
+  return EPS_HIP_OK;
+}
+
+int eps_hip_unique(const eps_hip_table* tables, uint32_t table_count,
+                   const eps_hip_push_feature* features, uint32_t feature_count,
+                   void* workspace, uint64_t workspace_bytes, uint64_t* unique_slots,
+                   uint32_t* unique_tables, uint64_t* occurrence_to_unique,
+                   uint64_t* unique_count, void* stream) {
+  PushPlan plan;
+  EPS_HIP_TRY(PlanPush(tables, table_count, features, feature_count, plan));
+  const PushLayout L(plan.occurrences);
+  if (!workspace || workspace_bytes < L.total)
+    return Fail(EPS_HIP_CAPACITY_EXCEEDED, "push workspace too small");
+  if (!unique_slots || !unique_tables || !occurrence_to_unique)
+    return Fail(EPS_HIP_INVALID_ARGUMENT, "null unique outputs");
+  auto* ws = static_cast<uint8_t*>(workspace);
+  auto* ctrl = reinterpret_cast<Control*>(ws);
+  const hipStream_t s = AsStream(stream);
+  const uint32_t n = uint32_t(plan.occurrences);
+  // Holes keep UINT64_MAX (include/eps/types.hpp:139; cache_backend.cu:281).
+  EPS_HIP_TRY(LaunchFill(reinterpret_cast<uint32_t*>(occurrence_to_unique), 0xffffffffu, 2ull * n, s));
+  if (!n) {
+    if (unique_count) EPS_HIP_TRY(LaunchFill(reinterpret_cast<uint32_t*>(unique_count), 0, 2, s));
+    return EPS_HIP_OK;
+  }
+  const bool in_b = SortedInB(plan.passes);
+  const auto* keys = reinterpret_cast<const uint32_t*>(ws + (in_b ? L.keys_b : L.keys_a));
+  const auto* vals = reinterpret_cast<const uint32_t*>(ws + (in_b ? L.vals_b : L.vals_a));
+  auto* flags = reinterpret_cast<uint32_t*>(ws + L.flags);
+  auto* ranks = reinterpret_cast<uint32_t*>(ws + L.ranks);
+  auto* sums = reinterpret_cast<uint32_t*>(ws + L.block_sums);
+  const uint32_t scan_blocks = (n + 1023) / 1024;
+  EPS_HIP_TRY(LaunchFill(flags, 0, n, s));
+  if (unique_count) EPS_HIP_TRY(LaunchFill(reinterpret_cast<uint32_t*>(unique_count), 0, 2, s));
+  hipLaunchKernelGGL(HeadFlagKernel, dim3(Grid(n, 8192)), dim3(kBlock), 0, s, keys, vals, ctrl, flags, n);
+  EPS_HIP_LAUNCHED("head flags");
+  hipLaunchKernelGGL(ScanBlockSumsKernel, dim3(scan_blocks), dim3(kBlock), 0, s, flags, sums, n);
+  EPS_HIP_LAUNCHED("scan sums");
+  hipLaunchKernelGGL(ScanTopKernel, dim3(1), dim3(kBlock), 0, s, sums, scan_blocks, ctrl, unique_count);
+  EPS_HIP_LAUNCHED("scan top");
+  hipLaunchKernelGGL(ScanApplyKernel, dim3(scan_blocks), dim3(kBlock), 0, s, flags, sums, ranks, n);
+  EPS_HIP_LAUNCHED("scan apply");
+  UniqueArgs uargs{};
+  for (uint32_t k = 0; k < table_count; ++k) uargs.table_of_key[k] = plan.table_of_key[k];
+  hipLaunchKernelGGL(UniqueWriteKernel, dim3(Grid(n, 8192)), dim3(kBlock), 0, s, keys, vals, ranks,
+                     ctrl, n, plan.row_bits, uargs, unique_slots, unique_tables,
+                     occurrence_to_unique);
+  EPS_HIP_LAUNCHED("unique write");
+  return EPS_HIP_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,46 @@
+"""The C-ABI library loads and exports every symbol include/eps_hip.h declares.
+
+No compute calls: this runs without a GPU.
+"""
+import ctypes
+import pathlib
+import re
+
+ROOT = pathlib.Path(__file__).resolve().parents[1]
+
+
+def declared(header):
+    text = (ROOT / "include" / header).read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(eps_hip_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_path():
+    names = declared("eps_hip.h")
+    for required in ("eps_hip_gather", "eps_hip_prepare", "eps_hip_push", "eps_hip_unique",
+                     "eps_hip_reduce", "eps_hip_adam_rows", "eps_hip_adam_compact",
+                     "eps_hip_scatter_rows", "eps_hip_gather_rows", "eps_hip_init_rows"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol(pkg):
+    lib = ctypes.CDLL(str(pkg.eps_hip.LIB_PATH))
+    missing = [n for n in declared("eps_hip.h") if not hasattr(lib, n)]
+    assert not missing, f"not exported: {missing}"
+
+
+def test_binding_covers_the_header(pkg):
+    assert set(declared("eps_hip.h")) == set(pkg.eps_hip.SYMBOLS)
+
+
+def test_host_only_queries(pkg):
+    L = pkg.eps_hip.lib()
+    assert L.eps_hip_abi_version() == 1
+    assert L.eps_hip_bounds_bytes() == 64 * 16
+    assert L.eps_hip_update_workspace_bytes() == 256
+    small, big = L.eps_hip_push_workspace_bytes(1000), L.eps_hip_push_workspace_bytes(10**6)
+    assert 256 < small < big
+    # Validation errors are reported without touching a device.
+    rc = L.eps_hip_prepare(None, 0, None, 0, None, 0, None)
+    assert rc == pkg.eps_hip.INVALID_ARGUMENT
+    assert b"tables" in L.eps_hip_last_error()
