@@ -83,7 +83,11 @@ __global__ void __launch_bounds__(kBlock) GatherKernel(GatherArgs args) {
     for (uint32_t r = threadIdx.x; r <= nrows; r += kBlock) s_off[r] = d.offsets[row0 + r];
   __syncthreads();
   const uint64_t occ_begin = seq ? row0 : s_off[0];
-  const uint64_t occ_end = seq ? row_end : s_off[nrows];
+  // A part without indices has no occurrences (every bag empty): nothing is
+  // read, and offsets that claim occurrences are reported as bad indices.
+  const bool none = d.indices == nullptr;
+  if (none && !seq && s_off[nrows] != s_off[0] && threadIdx.x == 0) s_bad = 1;
+  const uint64_t occ_end = none ? occ_begin : (seq ? row_end : s_off[nrows]);
   const bool staged = occ_end - occ_begin <= kIdCap;
   bool bad = false;
   if (staged) {
@@ -102,7 +106,7 @@ __global__ void __launch_bounds__(kBlock) GatherKernel(GatherArgs args) {
     const bool active = c < d.dim;
     for (uint32_t r = threadIdx.x >> d.log2g; r < nrows; r += ngroups) {
       const uint64_t beg = seq ? row0 + r : s_off[r];
-      const uint64_t end = seq ? row0 + r + 1 : s_off[r + 1];
+      const uint64_t end = none ? beg : (seq ? row0 + r + 1 : s_off[r + 1]);
       float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
       for (uint64_t pos = beg; pos < end; pos += 4) {
         float4 v[4];
@@ -152,7 +156,7 @@ __global__ void __launch_bounds__(kBlock) GatherKernel(GatherArgs args) {
     const uint32_t lane = threadIdx.x & (kWave - 1);
     for (uint32_t r = threadIdx.x / kWave; r < nrows; r += kBlock / kWave) {
       const uint64_t beg = seq ? row0 + r : s_off[r];
-      const uint64_t end = seq ? row0 + r + 1 : s_off[r + 1];
+      const uint64_t end = none ? beg : (seq ? row0 + r + 1 : s_off[r + 1]);
       float div = 0.f;
       if (d.pooling == EPS_HIP_POOL_MEAN && d.lengths) div = (float)d.lengths[row0 + r];
       for (uint32_t c = lane; c < d.dim; c += kWave) {
@@ -416,8 +420,11 @@ int eps_hip_gather(const eps_hip_gather_part* parts, uint32_t count, uint32_t* s
     if (in.dim == 0 || in.pooling > EPS_HIP_POOL_WEIGHTED_SUM)
       return Fail(EPS_HIP_INVALID_ARGUMENT, "invalid gather part");
     if (in.rows == 0) continue;
-    if (!in.source || !in.indices || !in.output || (in.pooling != EPS_HIP_POOL_SEQUENCE && !in.offsets) ||
-        (in.pooling == EPS_HIP_POOL_WEIGHTED_SUM && !in.weights))
+    // indices (and weights) may be NULL only for a pooled part whose bags are
+    // all empty; offsets that claim occurrences then raise the bad-index bit.
+    if (!in.source || !in.output || (in.pooling == EPS_HIP_POOL_SEQUENCE && !in.indices) ||
+        (in.pooling != EPS_HIP_POOL_SEQUENCE && !in.offsets) ||
+        (in.pooling == EPS_HIP_POOL_WEIGHTED_SUM && in.indices && !in.weights))
       return Fail(EPS_HIP_INVALID_ARGUMENT, "null gather buffer");
     GatherDesc& d = args.part[used++];
     d.source = in.source; d.indices = in.indices; d.remap = in.remap; d.offsets = in.offsets;

@@ -81,7 +81,8 @@ typedef struct eps_hip_optimizer {
  * (:251-308). */
 typedef struct eps_hip_gather_part {
   const float* source;            /* table state (stride 3*dim) or unique vectors (stride dim) */
-  const uint64_t* indices;        /* per occurrence; UINT64_MAX = not here (skipped) */
+  const uint64_t* indices;        /* per occurrence; UINT64_MAX = not here (skipped);
+                                     NULL allowed for a pooled part of empty bags */
   const uint64_t* remap;          /* optional: slot = remap[indices[i]] (unique -> slot) */
   const uint64_t* offsets;        /* bag_count + 1 (pooled modes) */
   const uint64_t* valid_lengths;  /* mean only: divide by it when non-NULL (client mean) */
