@@ -33,7 +33,8 @@ from __graft_entry__ import package  # noqa: E402
 
 METRIC = "pooled lookups/s + Adam rows/s on 1 GPU; achieved HBM GB/s (% of peak)"
 HBM_PEAK_GBPS = 8000.0
-PROFILE_SUMMARY = ROOT / "profiles" / "fused_update_criteo26.json"
+PROFILE_SUMMARY = ROOT / "profiles" / "fused_update_criteo26.md"
+COPY_BYTES = 1 << 30
 
 
 def cpu_model() -> str:
@@ -117,6 +118,8 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--batches", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run three plain 1 GiB device copies (counter calibration)")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py measures one GPU only (asked for {args.gpus}): the parameter shard runs on a "
@@ -124,6 +127,16 @@ def main(argv=None):
         return 2
 
     import torch
+
+    if args.copy_calibration:
+        # A copy of known size: the FETCH_SIZE / WRITE_SIZE reading of this
+        # kernel divided by 1 GiB is the counter's scale for HBM bytes.
+        src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     pkg = package()
     W, H = pkg.workloads, pkg.eps_hip
@@ -175,7 +188,9 @@ def main(argv=None):
     achieved = mean["fused_bytes"] / (fused_ms * 1e-3) / 1e9
     traffic = None
     if PROFILE_SUMMARY.exists():
-        traffic = json.loads(PROFILE_SUMMARY.read_text()).get("traffic_bytes_per_launch")
+        for line in PROFILE_SUMMARY.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                traffic = float(line.split(":", 1)[1])
     result = {
         "metric": METRIC,
         "value": mean["lookups"] / (ms * 1e-3),

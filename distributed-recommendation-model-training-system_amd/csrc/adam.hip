@@ -68,11 +68,17 @@ __global__ void __launch_bounds__(kBlock) GradMaxKernel(GuardArgs a) {
   const uint64_t end = min(begin + per_block, sp.count);
   uint32_t m = 0;
   if (reinterpret_cast<uintptr_t>(sp.p) % 16 == 0) {
+    // All kMaxItems loads of a thread are issued before any is consumed.
     const uint64_t vend = begin + ((end - begin) & ~uint64_t(3));
-    for (uint64_t i = begin + threadIdx.x * 4; i < vend; i += kBlock * 4) {
-      const float4 x = Load4(sp.p + i);
-      m = max(m, max(max(AbsBits(x.x), AbsBits(x.y)), max(AbsBits(x.z), AbsBits(x.w))));
+    float4 x[kMaxItems];
+#pragma unroll
+    for (uint32_t k = 0; k < kMaxItems; ++k) {
+      const uint64_t i = begin + (uint64_t(k) * kBlock + threadIdx.x) * 4;
+      x[k] = i < vend ? Load4(sp.p + i) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
+#pragma unroll
+    for (uint32_t k = 0; k < kMaxItems; ++k)
+      m = max(m, max(max(AbsBits(x[k].x), AbsBits(x[k].y)), max(AbsBits(x[k].z), AbsBits(x[k].w))));
     for (uint64_t i = vend + threadIdx.x; i < end; i += kBlock) m = max(m, AbsBits(sp.p[i]));
   } else {
     for (uint64_t i = begin + threadIdx.x; i < end; i += kBlock) m = max(m, AbsBits(sp.p[i]));
@@ -242,24 +248,6 @@ struct FusedArgs {
   uint32_t row_bits, cls, log2g, ppb, vblocks, fallback, reduce, tables;
 };
 
-// First index q in [from, limit) with keys[q] != key, or limit.
-__device__ uint32_t SegmentEnd(const uint32_t* keys, uint32_t from, uint32_t limit, uint32_t key) {
-  if (from >= limit || keys[from] != key) return from;
-  uint32_t lo = from, step = 1, hi;
-  for (;;) {
-    const uint32_t q = lo + step;
-    if (q >= limit) { hi = limit; break; }
-    if (keys[q] != key) { hi = q; break; }
-    lo = q;
-    step <<= 1;
-  }
-  while (hi - lo > 1) {
-    const uint32_t mid = lo + ((hi - lo) >> 1);
-    if (keys[mid] == key) lo = mid; else hi = mid;
-  }
-  return hi;
-}
-
 template <bool kGeneric>
 __global__ void __launch_bounds__(kBlock) SortedUpdateKernel(FusedArgs a) {
   __shared__ TableDesc s_t[EPS_HIP_MAX_TABLES];
@@ -317,7 +305,7 @@ __global__ void __launch_bounds__(kBlock) SortedUpdateKernel(FusedArgs a) {
     for (uint32_t h = gid; h < nheads; h += ngroups) {
       const uint32_t sb = s_heads[h];
       const uint32_t key = a.keys[sb];
-      const uint32_t se = h + 1 < nheads ? s_heads[h + 1] : SegmentEnd(a.keys, p1, end, key);
+      const uint32_t se = h + 1 < nheads ? s_heads[h + 1] : SegmentEndSearch(a.keys, p1, end, key);
       const TableDesc& T = s_t[key >> a.row_bits];
       const uint64_t slot = key & row_mask;
       const uint32_t dim = T.dim;
@@ -385,6 +373,209 @@ __global__ void __launch_bounds__(kBlock) SortedUpdateKernel(FusedArgs a) {
     __syncthreads();
   }
   FinishBlock(st, ctrl, a.bounds, write && !a.reduce);
+}
+
+// ---------------------------------------------------------------------------
+// Segment-list driver (vector dimension classes).  The prepared push holds one
+// segment per unique row (seg_start, in key order) and the list of segments
+// with more than kShortRefs references.
+//
+//  * Long units: (long segment, 16-column slice), one wavefront each.  The
+//    wave stages products src*scale of up to kChunk references into its own
+//    LDS tile ([column][reference]), and 16 lanes (one per column) add them in
+//    reference order; the next chunk's loads are in flight during the adds.
+//    Adam is elementwise, so the slices of one row are independent and a hot
+//    row's serial chain is spread over dim/16 wavefronts.
+//  * Short segments: a group of G = dim/4 lanes per row (lane = 4 columns)
+//    loads the row's w, m, v and all of its <= kShortRefs gradient rows at
+//    once, sums them in order and applies Adam.
+// Long units are taken first by every block of the first class's launch, so
+// the longest chains start at the beginning of the update.
+constexpr uint32_t kChunk = 128;
+constexpr uint32_t kChunkPad = kChunk + 4;
+
+struct SegUpdateArgs {
+  TableDesc t[EPS_HIP_MAX_TABLES];   // by key index
+  const float* grad[EPS_HIP_MAX_FEATURES];
+  const uint32_t* keys;
+  const uint64_t* rs;
+  const uint32_t* seg_start;
+  const uint32_t* long_list;
+  Control* ctrl;
+  Bounds* bounds;
+  uint32_t row_bits, cls, fallback, slices;
+};
+
+// Orders a wavefront's LDS writes before its later LDS reads (and the reverse).
+__device__ __forceinline__ void WaveSync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+__device__ __forceinline__ const float* RefSource(const float* const* grad, uint64_t word,
+                                                  uint32_t dim, uint32_t col, float& scale) {
+  const uint32_t ref = uint32_t(word);
+  scale = __uint_as_float(uint32_t(word >> 32));
+  return grad[ref >> kRefRowBits] + uint64_t(ref & ((1u << kRefRowBits) - 1)) * dim + col;
+}
+
+template <uint32_t kLog2G, bool kLong>
+__global__ void __launch_bounds__(kBlock) SegmentUpdateKernel(SegUpdateArgs a) {
+  __shared__ TableDesc s_t[EPS_HIP_MAX_TABLES];
+  __shared__ const float* s_grad[EPS_HIP_MAX_FEATURES];
+  __shared__ __align__(16) float s_buf[kLong ? kBlock / kWave : 1][kSlice][kChunkPad];
+#pragma unroll
+  for (uint32_t i = 0; i < EPS_HIP_MAX_TABLES; ++i)
+    if (threadIdx.x == i) s_t[i] = a.t[i];
+#pragma unroll
+  for (uint32_t i = 0; i < EPS_HIP_MAX_FEATURES; ++i)
+    if (threadIdx.x == i) s_grad[i] = a.grad[i];
+  Control* ctrl = a.ctrl;
+  const uint32_t mode = ctrl->mode;
+  bool write;
+  if (!a.fallback) {
+    if (mode == kReject) return;
+    write = mode == kFused;
+  } else {
+    if (mode != kChecked) return;
+    if (ctrl->status & kErrorBits) {
+      if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(&ctrl->status, EPS_HIP_STATUS_REJECTED);
+      return;
+    }
+    write = true;
+  }
+  const uint32_t U = ctrl->unique_count, valid = ctrl->valid_count;
+  const uint32_t row_mask = (1u << a.row_bits) - 1;
+  const uint32_t lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  RowStats st;
+  __syncthreads();
+
+  if constexpr (kLong) {
+    const uint32_t units = ctrl->long_count * a.slices;
+    const uint32_t q = lane & 3, rr = lane >> 2;  // staging: float4 q of reference rr
+    float (*buf)[kChunkPad] = s_buf[wave];
+    for (uint32_t u = blockIdx.x * (kBlock / kWave) + wave; u < units;
+         u += gridDim.x * (kBlock / kWave)) {
+      const uint32_t s = a.long_list[u / a.slices];
+      const uint32_t col0 = (u % a.slices) * kSlice;
+      const uint32_t start = a.seg_start[s];
+      const uint32_t end = s + 1 < U ? a.seg_start[s + 1] : valid;
+      const uint32_t key = a.keys[start];
+      const TableDesc& T = s_t[key >> a.row_bits];
+      const uint32_t dim = T.dim;
+      if (col0 >= dim) continue;  // wave-uniform
+      float* row = T.state + uint64_t(key & row_mask) * dim * 3;
+      const uint32_t cc = col0 + lane;
+      const bool chain = lane < kSlice && cc < dim;
+      float w = 0.f, m = 0.f, v = 0.f;
+      if (chain) { w = row[cc]; m = row[dim + cc]; v = row[2 * dim + cc]; }
+      const uint32_t sc = col0 + 4 * q;
+      const bool sact = sc < dim;
+      float4 x[kChunk / 16];
+      float scl[kChunk / 16];
+      auto issue = [&](uint32_t cbase) {
+#pragma unroll
+        for (uint32_t k = 0; k < kChunk / 16; ++k) {
+          const uint32_t ref = cbase + 16 * k + rr;
+          x[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+          scl[k] = 0.f;
+          if (ref < end) {
+            const float* src = RefSource(s_grad, a.rs[ref], dim, sc, scl[k]);
+            if (sact) x[k] = Load4(src);
+          }
+        }
+      };
+      issue(start);
+      float acc = 0.f;
+      for (uint32_t cbase = start; cbase < end; cbase += kChunk) {
+#pragma unroll
+        for (uint32_t k = 0; k < kChunk / 16; ++k) {
+          const uint32_t r = 16 * k + rr;
+          buf[4 * q + 0][r] = x[k].x * scl[k];
+          buf[4 * q + 1][r] = x[k].y * scl[k];
+          buf[4 * q + 2][r] = x[k].z * scl[k];
+          buf[4 * q + 3][r] = x[k].w * scl[k];
+        }
+        WaveSync();
+        const uint32_t n = min(kChunk, end - cbase);
+        if (cbase + kChunk < end) issue(cbase + kChunk);
+        if (chain) {
+          const float* mine = buf[lane];
+          if (n == kChunk) {
+#pragma unroll 8
+            for (uint32_t r = 0; r < kChunk; r += 4) {
+              const float4 p = *reinterpret_cast<const float4*>(mine + r);
+              acc = acc + p.x;
+              acc = acc + p.y;
+              acc = acc + p.z;
+              acc = acc + p.w;
+            }
+          } else {
+            for (uint32_t r = 0; r < n; ++r) acc = acc + mine[r];
+          }
+        }
+        WaveSync();
+      }
+      if (chain) {
+        AdamElement(T, acc, w, m, v, st);
+        if (write) {
+          row[cc] = w; row[dim + cc] = m; row[2 * dim + cc] = v;
+          Track(st, w, m, v);
+        }
+      }
+    }
+  }
+
+  // Short segments of this class.
+  constexpr uint32_t G = 1u << kLog2G;
+  constexpr uint32_t ngroups = kBlock / G;
+  uint32_t seg_begin = 0;
+  for (uint32_t c = 0; c < a.cls; ++c) seg_begin += ctrl->seg_class_count[c];
+  const uint32_t seg_end = seg_begin + ctrl->seg_class_count[a.cls];
+  const uint32_t lig = threadIdx.x & (G - 1), gid = threadIdx.x >> kLog2G;
+  const uint32_t c = lig * 4;
+  for (uint32_t s = seg_begin + blockIdx.x * ngroups + gid; s < seg_end; s += gridDim.x * ngroups) {
+    const uint32_t start = a.seg_start[s];
+    const uint32_t end = s + 1 < U ? a.seg_start[s + 1] : valid;
+    const uint32_t len = end - start;
+    if (len > kShortRefs) continue;
+    const uint32_t key = a.keys[start];
+    const TableDesc& T = s_t[key >> a.row_bits];
+    const uint32_t dim = T.dim;
+    const bool active = c < dim;
+    float* row = T.state + uint64_t(key & row_mask) * dim * 3;
+    float4 w = make_float4(0.f, 0.f, 0.f, 0.f), m = w, v = w;
+    if (active) { w = Load4(row + c); m = Load4(row + dim + c); v = Load4(row + 2 * dim + c); }
+    float4 x[kShortRefs];
+    float scl[kShortRefs];
+#pragma unroll
+    for (uint32_t k = 0; k < kShortRefs; ++k) {
+      x[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+      scl[k] = 0.f;
+      if (k < len) {
+        const float* src = RefSource(s_grad, a.rs[start + k], dim, c, scl[k]);
+        if (active) x[k] = Load4(src);
+      }
+    }
+    float4 g = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (uint32_t k = 0; k < kShortRefs; ++k)
+      if (k < len) Accumulate4(g, x[k], scl[k]);
+    if (!active) continue;
+    AdamElement(T, g.x, w.x, m.x, v.x, st);
+    AdamElement(T, g.y, w.y, m.y, v.y, st);
+    AdamElement(T, g.z, w.z, m.z, v.z, st);
+    AdamElement(T, g.w, w.w, m.w, v.w, st);
+    if (write) {
+      Store4(row + c, w);
+      Store4(row + dim + c, m);
+      Store4(row + 2 * dim + c, v);
+      Track(st, w.x, m.x, v.x); Track(st, w.y, m.y, v.y);
+      Track(st, w.z, m.z, v.z); Track(st, w.w, m.w, v.w);
+    }
+  }
+  FinishBlock(st, ctrl, a.bounds, write);
 }
 
 // ---------------------------------------------------------------------------
@@ -514,6 +705,30 @@ uint64_t SpanBlocks(uint64_t count) {
 }
 
 constexpr int kPrimary = 1, kSecond = 2;
+constexpr uint64_t kSegmentGrid = 2048;  // persistent grid of the segment kernels
+constexpr uint64_t kSecondGrid = 256;
+
+template <uint32_t kLog2G>
+int LaunchSegmentUpdateG(bool with_long, unsigned grid, const SegUpdateArgs& a, hipStream_t s) {
+  if (with_long)
+    hipLaunchKernelGGL((SegmentUpdateKernel<kLog2G, true>), dim3(grid), dim3(kBlock), 0, s, a);
+  else
+    hipLaunchKernelGGL((SegmentUpdateKernel<kLog2G, false>), dim3(grid), dim3(kBlock), 0, s, a);
+  EPS_HIP_LAUNCHED("segment update");
+  return EPS_HIP_OK;
+}
+
+int LaunchSegmentUpdate(uint32_t cls, bool with_long, unsigned grid, const SegUpdateArgs& a,
+                        hipStream_t s) {
+  switch (cls) {
+    case 0: return LaunchSegmentUpdateG<2>(with_long, grid, a, s);
+    case 1: return LaunchSegmentUpdateG<3>(with_long, grid, a, s);
+    case 2: return LaunchSegmentUpdateG<4>(with_long, grid, a, s);
+    case 3: return LaunchSegmentUpdateG<5>(with_long, grid, a, s);
+    case 4: return LaunchSegmentUpdateG<6>(with_long, grid, a, s);
+    default: return Fail(EPS_HIP_INVALID_ARGUMENT, "no segment kernel for this dimension class");
+  }
+}
 
 int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, uint32_t table_count,
               const eps_hip_push_feature* features, uint32_t feature_count, const PushPlan& plan,
@@ -540,8 +755,47 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
     a.t[k] = MakeTable(tables[t], o);
   }
   for (uint32_t f = 0; f < feature_count; ++f) a.grad[f] = features[f].gradients;
+  if (!reduce) {
+    // Vector classes: the segment-list kernels (long units in the first launch).
+    SegUpdateArgs sa{};
+    for (uint32_t k = 0; k < table_count; ++k) sa.t[k] = a.t[k];
+    for (uint32_t f = 0; f < feature_count; ++f) sa.grad[f] = features[f].gradients;
+    sa.keys = a.keys;
+    sa.rs = a.rs;
+    sa.seg_start = reinterpret_cast<const uint32_t*>(ws + L.seg_start);
+    sa.long_list = reinterpret_cast<const uint32_t*>(ws + L.long_list);
+    sa.ctrl = a.ctrl;
+    sa.bounds = bounds;
+    sa.row_bits = plan.row_bits;
+    sa.slices = 1;
+    for (uint32_t t = 0; t < table_count; ++t)
+      if (DimClass(tables[t].dim) < kClasses - 1)
+        sa.slices = std::max(sa.slices, (tables[t].dim + kSlice - 1) / kSlice);
+    uint64_t vector_occurrences = 0;
+    for (uint32_t cls = 0; cls + 1 < kClasses; ++cls) vector_occurrences += plan.class_occurrences[cls];
+    const uint64_t long_units = (vector_occurrences / (kShortRefs + 1)) * sa.slices;
+    bool first = true;
+    for (uint32_t cls = 0; cls + 1 < kClasses; ++cls) {
+      if (!plan.class_occurrences[cls]) continue;
+      sa.cls = cls;
+      const uint64_t groups = kBlock >> (cls + 2);
+      uint64_t blocks = (plan.class_occurrences[cls] + groups - 1) / groups;
+      if (first) blocks = std::max<uint64_t>(blocks, (long_units + 3) / 4);
+      for (int phase = kPrimary; phase <= kSecond; phase <<= 1) {
+        if (!(phases & phase)) continue;
+        sa.fallback = phase == kSecond;
+        // The checked apply runs only after a validate-only pass; its launch
+        // usually exits at once, so it gets a small grid.
+        const unsigned grid = unsigned(std::max<uint64_t>(1, std::min<uint64_t>(
+            blocks, phase == kSecond ? kSecondGrid : kSegmentGrid)));
+        EPS_HIP_TRY(LaunchSegmentUpdate(cls, first, grid, sa, s));
+      }
+      first = false;
+    }
+  }
   for (uint32_t cls = 0; cls < kClasses; ++cls) {
     if (!plan.class_occurrences[cls]) continue;
+    if (!reduce && cls + 1 < kClasses) continue;  // handled above
     a.cls = cls;
     a.log2g = cls + 2;
     a.ppb = PositionsPerBlock(cls);

@@ -20,6 +20,10 @@ constexpr uint32_t kMaxPasses = 4;
 constexpr uint32_t kKeygenItems = 4;      // occurrences per keygen thread
 constexpr uint32_t kClasses = 6;          // 5 vector widths + generic
 constexpr uint32_t kRefRowBits = 27;      // gradient row bits in a reference word
+constexpr uint32_t kShortRefs = 16;       // segments up to this many references: short path
+constexpr uint32_t kSlice = 16;           // columns per long-path work unit
+constexpr uint32_t kSliceLog2 = 4;
+constexpr uint32_t kMaxSlices = 16;       // 256 / kSlice (vector classes have dim <= 256)
 
 // Control block at offset 0 of a push or update workspace (256 bytes).
 struct Control {
@@ -30,10 +34,12 @@ struct Control {
   uint32_t valid_count;     // prepared occurrences that are on this device
   uint32_t mode;            // guard decision of the last push
   uint32_t done_counter;    // last-block detection (self-resetting)
-  uint32_t unique_count;
+  uint32_t unique_count;    // segments (unique rows) of the prepared push
   uint32_t tile_counter[kMaxPasses];
-  uint32_t class_count[8];
-  uint32_t pad[44];
+  uint32_t class_count[8];  // prepared occurrences per dimension class
+  uint32_t long_count;      // entries of the long-segment list
+  uint32_t seg_class_count[8];  // segments per dimension class
+  uint32_t pad[35];
 };
 static_assert(sizeof(Control) == 256, "control block is 256 bytes");
 
@@ -46,7 +52,7 @@ struct Bounds { uint32_t v[kBoundSlots][4]; };
 struct PushLayout {
   uint64_t n, tiles;
   uint64_t hist, look, keys_a, keys_b, vals_a, vals_b, refscale, sorted_rs, flags, ranks,
-      block_sums, total;
+      block_sums, tile_heads, seg_start, long_list, total;
   explicit PushLayout(uint64_t occurrences) {
     n = occurrences;
     tiles = (n + kSortTile - 1) / kSortTile;
@@ -63,6 +69,9 @@ struct PushLayout {
     flags = at; at = align(at + n * 4);
     ranks = at; at = align(at + n * 4);
     block_sums = at; at = align(at + ((n + 1023) / 1024 + 1) * 4);
+    tile_heads = at; at = align(at + (tiles + 1) * 4);
+    seg_start = at; at = align(at + (n + 1) * 4);
+    long_list = at; at = align(at + (n / kShortRefs + 1) * 4);
     total = at;
   }
 };
@@ -91,6 +100,26 @@ __device__ __forceinline__ uint32_t WaveMax(uint32_t x) {
 #pragma unroll
   for (int offset = 32; offset > 0; offset >>= 1) x = max(x, (uint32_t)__shfl_xor((int)x, offset));
   return x;
+}
+
+// First index q in [from, limit) with keys[q] != key, or limit (keys sorted):
+// exponential then binary search, so long runs cost O(log run).
+__device__ inline uint32_t SegmentEndSearch(const uint32_t* keys, uint32_t from, uint32_t limit,
+                                            uint32_t key) {
+  if (from >= limit || keys[from] != key) return from;
+  uint32_t lo = from, step = 1, hi;
+  for (;;) {
+    const uint32_t q = lo + step;
+    if (q >= limit || q < lo) { hi = limit; break; }
+    if (keys[q] != key) { hi = q; break; }
+    lo = q;
+    step <<= 1;
+  }
+  while (hi - lo > 1) {
+    const uint32_t mid = lo + ((hi - lo) >> 1);
+    if (keys[mid] == key) lo = mid; else hi = mid;
+  }
+  return hi;
 }
 
 // BoundWeight (src/common/optimizer_bounds.hpp:14-18) written as std::clamp so
