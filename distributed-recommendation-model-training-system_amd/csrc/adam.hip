@@ -189,10 +189,10 @@ __device__ __forceinline__ void AdamRow4(const TableDesc& T, uint64_t slot, uint
 __device__ __forceinline__ void AdamRow1(const TableDesc& T, uint64_t slot, uint32_t c, float g,
                                          bool write, RowStats& st) {
   float* row = T.state + slot * uint64_t(T.dim) * 3;
-  float w = row[c], m = row[T.dim + c], v = row[2 * T.dim + c];
+  float w = LoadF(row + c), m = LoadF(row + T.dim + c), v = LoadF(row + 2 * T.dim + c);
   AdamElement(T, g, w, m, v, st);
   if (write) {
-    row[c] = w; row[T.dim + c] = m; row[2 * T.dim + c] = v;
+    StoreF(row + c, w); StoreF(row + T.dim + c, m); StoreF(row + 2 * T.dim + c, v);
     Track(st, w, m, v);
   }
 }
@@ -356,7 +356,7 @@ __global__ void __launch_bounds__(kBlock) SortedUpdateKernel(FusedArgs a) {
               const float s = __uint_as_float(uint32_t(w >> 32));
               const float* src = s_grad[ref >> kRefRowBits] +
                                  uint64_t(ref & ((1u << kRefRowBits) - 1)) * dim;
-              const float x = active ? src[c] : 0.f;
+              const float x = active ? LoadF(src + c) : 0.f;
               acc = acc + x * s;
             }
           }
@@ -376,31 +376,34 @@ __global__ void __launch_bounds__(kBlock) SortedUpdateKernel(FusedArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Segment-list driver (vector dimension classes).  The prepared push holds one
-// segment per unique row (seg_start, in key order) and the list of segments
-// with more than kShortRefs references.
+// Vector-class update (dim % 4 == 0, dim <= 256).  Two kernels:
 //
-//  * Long units: (long segment, 16-column slice), one wavefront each.  The
-//    wave stages products src*scale of up to kChunk references into its own
-//    LDS tile ([column][reference]), and 16 lanes (one per column) add them in
-//    reference order; the next chunk's loads are in flight during the adds.
-//    Adam is elementwise, so the slices of one row are independent and a hot
-//    row's serial chain is spread over dim/16 wavefronts.
-//  * Short segments: a group of G = dim/4 lanes per row (lane = 4 columns)
-//    loads the row's w, m, v and all of its <= kShortRefs gradient rows at
-//    once, sums them in order and applies Adam.
-// Long units are taken first by every block of the first class's launch, so
-// the longest chains start at the beginning of the update.
-constexpr uint32_t kChunk = 128;
+//  * HotSliceKernel: rows with more than kLongRefs references (listed at
+//    prepare time).  Work unit = (hot row, 8-column slice), one wavefront.
+//    The wave stages products src*scale of kChunk references into its own LDS
+//    tile ([column][reference]); 8 lanes (one per column) then add them in
+//    reference order.  The next chunk's gradient loads and the chunk after
+//    that's reference words are in flight during the adds.  Adam is
+//    elementwise, so the slices of one row are independent and a hot row's
+//    serial chain is spread over dim/8 wavefronts.
+//  * RowRunKernel: every other row.  A block owns kRunPositions sorted
+//    positions; it stages their keys and reference words (plus kLongRefs
+//    positions of look-ahead) in LDS with coalesced loads, finds the segment
+//    heads with a ballot, and a group of G = dim/4 lanes per row (lane = 4
+//    columns) loads the row's w, m, v together with its gradient rows, sums
+//    them in order and applies Adam.
+constexpr uint32_t kChunk = 512;
 constexpr uint32_t kChunkPad = kChunk + 4;
+constexpr uint32_t kStageLoads = kChunk / kWave;        // staging loads per lane per chunk
+constexpr uint32_t kRunPositions = 128;
+constexpr uint32_t kRefBatch = 8;                       // gradient rows in flight per group
 
-struct SegUpdateArgs {
+struct VecArgs {
   TableDesc t[EPS_HIP_MAX_TABLES];   // by key index
   const float* grad[EPS_HIP_MAX_FEATURES];
   const uint32_t* keys;
   const uint64_t* rs;
-  const uint32_t* seg_start;
-  const uint32_t* long_list;
+  const uint32_t* hot;
   Control* ctrl;
   Bounds* bounds;
   uint32_t row_bits, cls, fallback, slices;
@@ -420,159 +423,292 @@ __device__ __forceinline__ const float* RefSource(const float* const* grad, uint
   return grad[ref >> kRefRowBits] + uint64_t(ref & ((1u << kRefRowBits) - 1)) * dim + col;
 }
 
-template <uint32_t kLog2G, bool kLong>
-__global__ void __launch_bounds__(kBlock) SegmentUpdateKernel(SegUpdateArgs a) {
-  __shared__ TableDesc s_t[EPS_HIP_MAX_TABLES];
-  __shared__ const float* s_grad[EPS_HIP_MAX_FEATURES];
-  __shared__ __align__(16) float s_buf[kLong ? kBlock / kWave : 1][kSlice][kChunkPad];
-#pragma unroll
-  for (uint32_t i = 0; i < EPS_HIP_MAX_TABLES; ++i)
-    if (threadIdx.x == i) s_t[i] = a.t[i];
-#pragma unroll
-  for (uint32_t i = 0; i < EPS_HIP_MAX_FEATURES; ++i)
-    if (threadIdx.x == i) s_grad[i] = a.grad[i];
+// Block-wide copy of a kernel-argument array to LDS, one 32-bit word per
+// thread per step (the arrays are read in place from the argument segment).
+__device__ __forceinline__ void CopyWords(void* dst, const void* src, uint32_t bytes) {
+  const uint32_t* from = static_cast<const uint32_t*>(src);
+  uint32_t* to = static_cast<uint32_t*>(dst);
+  for (uint32_t i = threadIdx.x; i < bytes / 4; i += kBlock) to[i] = from[i];
+}
+
+// Copies the per-launch tables to LDS and decides whether this launch writes;
+// returns false when it has nothing to do (uniform over the block).
+__device__ __forceinline__ bool VecPrologue(const VecArgs& a, TableDesc* s_t, const float** s_grad,
+                                            bool& write) {
+  CopyWords(s_t, a.t, sizeof(a.t));
+  CopyWords(s_grad, a.grad, sizeof(a.grad));
   Control* ctrl = a.ctrl;
   const uint32_t mode = ctrl->mode;
-  bool write;
   if (!a.fallback) {
-    if (mode == kReject) return;
+    if (mode == kReject) return false;
     write = mode == kFused;
   } else {
-    if (mode != kChecked) return;
+    if (mode != kChecked) return false;
     if (ctrl->status & kErrorBits) {
       if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(&ctrl->status, EPS_HIP_STATUS_REJECTED);
-      return;
+      return false;
     }
     write = true;
   }
-  const uint32_t U = ctrl->unique_count, valid = ctrl->valid_count;
+  return true;
+}
+
+// acc + v[0] + v[1] + ... + v[kChunk-1], strictly left to right.  LDS reads
+// go in batches of eight 128-bit loads, the next batch issued before the
+// current one is added, so the adds never wait on a single read.
+__device__ __forceinline__ float ChainSum(float acc, const float* v) {
+  constexpr uint32_t kBatch = 8;
+  const float4* v4 = reinterpret_cast<const float4*>(v);
+  float4 cur[kBatch], nxt[kBatch];
+#pragma unroll
+  for (uint32_t i = 0; i < kBatch; ++i) cur[i] = v4[i];
+#pragma unroll
+  for (uint32_t b = 0; b < kChunk / (4 * kBatch); ++b) {
+    if (b + 1 < kChunk / (4 * kBatch)) {
+#pragma unroll
+      for (uint32_t i = 0; i < kBatch; ++i) nxt[i] = v4[(b + 1) * kBatch + i];
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < kBatch; ++i) {
+      acc = acc + cur[i].x;
+      acc = acc + cur[i].y;
+      acc = acc + cur[i].z;
+      acc = acc + cur[i].w;
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < kBatch; ++i) cur[i] = nxt[i];
+  }
+  return acc;
+}
+
+__global__ void __launch_bounds__(kBlock) HotSliceKernel(VecArgs a) {
+  __shared__ TableDesc s_t[EPS_HIP_MAX_TABLES];
+  __shared__ const float* s_grad[EPS_HIP_MAX_FEATURES];
+  __shared__ __align__(16) float s_buf[kBlock / kWave][kSlice][kChunkPad];
+  bool write = false;
+  if (!VecPrologue(a, s_t, s_grad, write)) return;
+  Control* ctrl = a.ctrl;
+  const uint32_t valid = ctrl->valid_count;
   const uint32_t row_mask = (1u << a.row_bits) - 1;
   const uint32_t lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  float (*buf)[kChunkPad] = s_buf[wave];
   RowStats st;
   __syncthreads();
-
-  if constexpr (kLong) {
-    const uint32_t units = ctrl->long_count * a.slices;
-    const uint32_t q = lane & 3, rr = lane >> 2;  // staging: float4 q of reference rr
-    float (*buf)[kChunkPad] = s_buf[wave];
-    for (uint32_t u = blockIdx.x * (kBlock / kWave) + wave; u < units;
-         u += gridDim.x * (kBlock / kWave)) {
-      const uint32_t s = a.long_list[u / a.slices];
-      const uint32_t col0 = (u % a.slices) * kSlice;
-      const uint32_t start = a.seg_start[s];
-      const uint32_t end = s + 1 < U ? a.seg_start[s + 1] : valid;
-      const uint32_t key = a.keys[start];
-      const TableDesc& T = s_t[key >> a.row_bits];
-      const uint32_t dim = T.dim;
-      if (col0 >= dim) continue;  // wave-uniform
-      float* row = T.state + uint64_t(key & row_mask) * dim * 3;
-      const uint32_t cc = col0 + lane;
-      const bool chain = lane < kSlice && cc < dim;
-      float w = 0.f, m = 0.f, v = 0.f;
-      if (chain) { w = row[cc]; m = row[dim + cc]; v = row[2 * dim + cc]; }
-      const uint32_t sc = col0 + 4 * q;
-      const bool sact = sc < dim;
-      float4 x[kChunk / 16];
-      float scl[kChunk / 16];
-      auto issue = [&](uint32_t cbase) {
-#pragma unroll
-        for (uint32_t k = 0; k < kChunk / 16; ++k) {
-          const uint32_t ref = cbase + 16 * k + rr;
-          x[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-          scl[k] = 0.f;
-          if (ref < end) {
-            const float* src = RefSource(s_grad, a.rs[ref], dim, sc, scl[k]);
-            if (sact) x[k] = Load4(src);
-          }
-        }
-      };
-      issue(start);
-      float acc = 0.f;
-      for (uint32_t cbase = start; cbase < end; cbase += kChunk) {
-#pragma unroll
-        for (uint32_t k = 0; k < kChunk / 16; ++k) {
-          const uint32_t r = 16 * k + rr;
-          buf[4 * q + 0][r] = x[k].x * scl[k];
-          buf[4 * q + 1][r] = x[k].y * scl[k];
-          buf[4 * q + 2][r] = x[k].z * scl[k];
-          buf[4 * q + 3][r] = x[k].w * scl[k];
-        }
-        WaveSync();
-        const uint32_t n = min(kChunk, end - cbase);
-        if (cbase + kChunk < end) issue(cbase + kChunk);
-        if (chain) {
-          const float* mine = buf[lane];
-          if (n == kChunk) {
-#pragma unroll 8
-            for (uint32_t r = 0; r < kChunk; r += 4) {
-              const float4 p = *reinterpret_cast<const float4*>(mine + r);
-              acc = acc + p.x;
-              acc = acc + p.y;
-              acc = acc + p.z;
-              acc = acc + p.w;
-            }
-          } else {
-            for (uint32_t r = 0; r < n; ++r) acc = acc + mine[r];
-          }
-        }
-        WaveSync();
-      }
-      if (chain) {
-        AdamElement(T, acc, w, m, v, st);
-        if (write) {
-          row[cc] = w; row[dim + cc] = m; row[2 * dim + cc] = v;
-          Track(st, w, m, v);
-        }
-      }
-    }
-  }
-
-  // Short segments of this class.
-  constexpr uint32_t G = 1u << kLog2G;
-  constexpr uint32_t ngroups = kBlock / G;
-  uint32_t seg_begin = 0;
-  for (uint32_t c = 0; c < a.cls; ++c) seg_begin += ctrl->seg_class_count[c];
-  const uint32_t seg_end = seg_begin + ctrl->seg_class_count[a.cls];
-  const uint32_t lig = threadIdx.x & (G - 1), gid = threadIdx.x >> kLog2G;
-  const uint32_t c = lig * 4;
-  for (uint32_t s = seg_begin + blockIdx.x * ngroups + gid; s < seg_end; s += gridDim.x * ngroups) {
-    const uint32_t start = a.seg_start[s];
-    const uint32_t end = s + 1 < U ? a.seg_start[s + 1] : valid;
-    const uint32_t len = end - start;
-    if (len > kShortRefs) continue;
+  const uint32_t units = ctrl->long_count * a.slices;
+  for (uint32_t u = blockIdx.x * (kBlock / kWave) + wave; u < units;
+       u += gridDim.x * (kBlock / kWave)) {
+    const uint32_t start = a.hot[u / a.slices];
+    const uint32_t col0 = (u % a.slices) * kSlice;
     const uint32_t key = a.keys[start];
     const TableDesc& T = s_t[key >> a.row_bits];
     const uint32_t dim = T.dim;
-    const bool active = c < dim;
+    if (col0 >= dim) continue;  // wave-uniform
     float* row = T.state + uint64_t(key & row_mask) * dim * 3;
-    float4 w = make_float4(0.f, 0.f, 0.f, 0.f), m = w, v = w;
-    if (active) { w = Load4(row + c); m = Load4(row + dim + c); v = Load4(row + 2 * dim + c); }
-    float4 x[kShortRefs];
-    float scl[kShortRefs];
+    const uint32_t cc = col0 + lane;
+    const bool chain = lane < kSlice;  // dim is a multiple of 4: the whole slice is in the row
+    float w = 0.f, m = 0.f, v = 0.f;
+    if (chain) { w = LoadF(row + cc); m = LoadF(row + dim + cc); v = LoadF(row + 2 * dim + cc); }
+    // The row's references are the positions from `start` whose key is `key`
+    // (keys are sorted, so they form one run).  Lane l stages reference
+    // cbase + kWave*k + l.  Every load is issued unconditionally at an
+    // in-bounds position (clamped to the last valid one) and masked after, so
+    // nothing in the chunk pipeline branches around a load: words and keys of
+    // chunk c+2 and gradient rows of chunk c+1 are in flight during the adds
+    // of chunk c.
+    uint64_t word[kStageLoads];
+    uint32_t kk[kStageLoads];
+    float4 x[kStageLoads];
+    uint32_t match = 0, kk_base = 0;
+    auto load_words = [&](uint32_t cbase) {
+      kk_base = cbase;
 #pragma unroll
-    for (uint32_t k = 0; k < kShortRefs; ++k) {
-      x[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-      scl[k] = 0.f;
-      if (k < len) {
-        const float* src = RefSource(s_grad, a.rs[start + k], dim, c, scl[k]);
-        if (active) x[k] = Load4(src);
+      for (uint32_t k = 0; k < kStageLoads; ++k) {
+        const uint32_t ref = min(cbase + kWave * k + lane, valid - 1);
+        word[k] = a.rs[ref];
+        kk[k] = a.keys[ref];
+      }
+    };
+    auto match_bits = [&]() {
+      uint32_t bits = 0;
+#pragma unroll
+      for (uint32_t k = 0; k < kStageLoads; ++k)
+        bits |= uint32_t(kk[k] == key && kk_base + kWave * k + lane < valid) << k;
+      return bits;
+    };
+    // A position outside the row holds another row's reference, whose
+    // gradient buffer may have another dimension and fewer rows: its address
+    // is formed from the row's own first reference instead (`own`), so every
+    // load stays inside this table's gradient rows; the value is discarded.
+    const uint64_t own = a.rs[start];
+    auto load_rows = [&]() {
+#pragma unroll
+      for (uint32_t k = 0; k < kStageLoads; ++k) {
+        float unused;
+        const uint64_t wk = ((match >> k) & 1u) ? word[k] : own;
+        x[k] = Load4(RefSource(s_grad, wk, dim, col0, unused));
+      }
+    };
+    auto chunk_refs = [&](uint32_t bits) {
+      uint32_t count = 0;
+#pragma unroll
+      for (uint32_t k = 0; k < kStageLoads; ++k)
+        count += uint32_t(__popcll(__ballot((bits >> k) & 1u)));
+      return count;
+    };
+    uint32_t cbase = start;
+    load_words(cbase);
+    match = match_bits();
+    load_rows();
+    uint32_t scale_bits[kStageLoads];
+#pragma unroll
+    for (uint32_t k = 0; k < kStageLoads; ++k) scale_bits[k] = uint32_t(word[k] >> 32);
+    uint32_t n = chunk_refs(match);
+    load_words(cbase + kChunk);
+    float acc = 0.f;
+    // Straight-line body (no loads under a condition): each register set is
+    // consumed before it is reloaded in place, so nothing waits on a load that
+    // was just issued.
+    while (n) {
+      // The product src*scale of each reference, rounded as the reference's
+      // separate multiply (the add happens in the chain below).  Positions of
+      // other rows are staged as -0.0f, the exact identity of IEEE addition
+      // (x + -0 == x for every x, signed zeros included), so the chain always
+      // runs over a whole chunk without changing any bit of the sum.
+#pragma unroll
+      for (uint32_t k = 0; k < kStageLoads; ++k) {
+        const bool in = (match >> k) & 1u;
+        const float sv = __uint_as_float(scale_bits[k]);
+        const uint32_t r = kWave * k + lane;
+        buf[0][r] = in ? x[k].x * sv : -0.f;
+        buf[1][r] = in ? x[k].y * sv : -0.f;
+        buf[2][r] = in ? x[k].z * sv : -0.f;
+        buf[3][r] = in ? x[k].w * sv : -0.f;
+      }
+      WaveSync();
+      // Next chunk: rows from the words already loaded, then words and keys
+      // of the chunk after it.  A chunk that is not full is the row's last.
+      match = n == kChunk ? match_bits() : 0u;
+      load_rows();
+#pragma unroll
+      for (uint32_t k = 0; k < kStageLoads; ++k) scale_bits[k] = uint32_t(word[k] >> 32);
+      const uint32_t n_next = chunk_refs(match);
+      load_words(cbase + 2 * kChunk);
+      if (chain) acc = ChainSum(acc, buf[lane]);
+      WaveSync();
+      n = n_next;
+      cbase += kChunk;
+    }
+    if (chain) {
+      AdamElement(T, acc, w, m, v, st);
+      if (write) {
+        StoreF(row + cc, w); StoreF(row + dim + cc, m); StoreF(row + 2 * dim + cc, v);
+        Track(st, w, m, v);
       }
     }
-    float4 g = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+  FinishBlock(st, ctrl, a.bounds, write);
+}
+
+template <uint32_t kLog2G>
+__global__ void __launch_bounds__(kBlock) RowRunKernel(VecArgs a) {
+  constexpr uint32_t G = 1u << kLog2G;
+  constexpr uint32_t ngroups = kBlock / G;
+  constexpr uint32_t kStaged = kRunPositions + kLongRefs;
+  __shared__ TableDesc s_t[EPS_HIP_MAX_TABLES];
+  __shared__ const float* s_grad[EPS_HIP_MAX_FEATURES];
+  __shared__ uint32_t s_key[kStaged + 1];   // s_key[i + 1] = key at position p0 + i
+  __shared__ const float* s_src[kStaged];   // gradient row of position p0 + i
+  __shared__ float s_scale[kStaged];
+  __shared__ uint32_t s_heads[kRunPositions];
+  __shared__ uint32_t s_wave_heads[kBlock / kWave];
+  bool write = false;
+  if (!VecPrologue(a, s_t, s_grad, write)) return;
+  Control* ctrl = a.ctrl;
+  uint32_t begin = 0;
+  for (uint32_t c = 0; c < a.cls; ++c) begin += ctrl->class_count[c];
+  const uint32_t end = begin + ctrl->class_count[a.cls];
+  const uint32_t row_mask = (1u << a.row_bits) - 1;
+  const uint32_t lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const uint32_t lig = threadIdx.x & (G - 1), gid = threadIdx.x >> kLog2G;
+  const uint32_t c = lig * 4;
+  RowStats st;
+  __syncthreads();
+  for (uint32_t p0 = begin + blockIdx.x * kRunPositions; p0 < end; p0 += gridDim.x * kRunPositions) {
+    const uint32_t p1 = min(p0 + kRunPositions, end);
+    const uint32_t lim = min(p1 + kLongRefs, end);
+    const uint32_t staged = lim - p0;
+    __syncthreads();  // previous iteration's readers are done
+    // Stage keys and, per position, the gradient row it references and its
+    // scale (one coalesced pass; the table and feature lookups happen here
+    // once per position instead of once per lane).
+    if (threadIdx.x == 0) s_key[0] = p0 > begin ? a.keys[p0 - 1] : ~a.keys[p0];
+    for (uint32_t i = threadIdx.x; i < staged; i += kBlock) {
+      const uint32_t key = a.keys[p0 + i];
+      s_key[i + 1] = key;
+      float scale;
+      s_src[i] = RefSource(s_grad, a.rs[p0 + i], s_t[key >> a.row_bits].dim, 0, scale);
+      s_scale[i] = scale;
+    }
+    __syncthreads();
+    const bool head = threadIdx.x < p1 - p0 && s_key[threadIdx.x + 1] != s_key[threadIdx.x];
+    const uint64_t ballot = __ballot(head);
+    if (lane == 0) s_wave_heads[wave] = uint32_t(__popcll(ballot));
+    __syncthreads();
+    uint32_t before = 0;
+    for (uint32_t w = 0; w < wave; ++w) before += s_wave_heads[w];
+    uint32_t nheads = 0;
+    for (uint32_t w = 0; w < kBlock / kWave; ++w) nheads += s_wave_heads[w];
+    if (head) s_heads[before + uint32_t(__popcll(ballot & ((1ull << lane) - 1)))] = threadIdx.x;
+    __syncthreads();
+    for (uint32_t h = gid; h < nheads; h += ngroups) {
+      const uint32_t sb = s_heads[h];
+      const uint32_t key = s_key[sb + 1];
+      // Hot rows (more than kLongRefs references) belong to HotSliceKernel.
+      if (sb + kLongRefs < staged && s_key[sb + kLongRefs + 1] == key) continue;
+      uint32_t se = h + 1 < nheads ? s_heads[h + 1] : p1 - p0;
+      while (se < staged && s_key[se + 1] == key) ++se;
+      const TableDesc& T = s_t[key >> a.row_bits];
+      const uint32_t dim = T.dim;
+      const bool active = c < dim;
+      const uint32_t cl = active ? c : 0;  // inactive lanes read column 0 and drop it
+      float* row = T.state + uint64_t(key & row_mask) * dim * 3;
+      const float4 w0 = Load4(row + cl), m0 = Load4(row + dim + cl), v0 = Load4(row + 2 * dim + cl);
+      float4 g = make_float4(0.f, 0.f, 0.f, 0.f);
+      // Every slot of a batch loads (slots past the row repeat its last
+      // reference, an in-bounds row of the same table); only real references
+      // are added, in order.  The first batch is straight-line code so its
+      // loads go out together with w, m and v; longer rows loop.
+      auto batch = [&](uint32_t j0) {
+        float4 x[kRefBatch];
+        float s[kRefBatch];
 #pragma unroll
-    for (uint32_t k = 0; k < kShortRefs; ++k)
-      if (k < len) Accumulate4(g, x[k], scl[k]);
-    if (!active) continue;
-    AdamElement(T, g.x, w.x, m.x, v.x, st);
-    AdamElement(T, g.y, w.y, m.y, v.y, st);
-    AdamElement(T, g.z, w.z, m.z, v.z, st);
-    AdamElement(T, g.w, w.w, m.w, v.w, st);
-    if (write) {
-      Store4(row + c, w);
-      Store4(row + dim + c, m);
-      Store4(row + 2 * dim + c, v);
-      Track(st, w.x, m.x, v.x); Track(st, w.y, m.y, v.y);
-      Track(st, w.z, m.z, v.z); Track(st, w.w, m.w, v.w);
+        for (uint32_t k = 0; k < kRefBatch; ++k) {
+          const uint32_t j = min(j0 + k, se - 1);
+          s[k] = s_scale[j];
+          x[k] = Load4(s_src[j] + cl);
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kRefBatch; ++k) {
+          float4 t = g;
+          Accumulate4(t, x[k], s[k]);
+          if (j0 + k < se) g = t;
+        }
+      };
+      batch(sb);
+      for (uint32_t j0 = sb + kRefBatch; j0 < se; j0 += kRefBatch) batch(j0);
+      if (!active) continue;
+      float4 w = w0, m = m0, v = v0;
+      AdamElement(T, g.x, w.x, m.x, v.x, st);
+      AdamElement(T, g.y, w.y, m.y, v.y, st);
+      AdamElement(T, g.z, w.z, m.z, v.z, st);
+      AdamElement(T, g.w, w.w, m.w, v.w, st);
+      if (write) {
+        Store4(row + c, w);
+        Store4(row + dim + c, m);
+        Store4(row + 2 * dim + c, v);
+        Track(st, w.x, m.x, v.x); Track(st, w.y, m.y, v.y);
+        Track(st, w.z, m.z, v.z); Track(st, w.w, m.w, v.w);
+      }
     }
   }
   FinishBlock(st, ctrl, a.bounds, write);
@@ -705,28 +841,31 @@ uint64_t SpanBlocks(uint64_t count) {
 }
 
 constexpr int kPrimary = 1, kSecond = 2;
-constexpr uint64_t kSegmentGrid = 2048;  // persistent grid of the segment kernels
+constexpr uint64_t kVectorGrid = 4096;  // persistent grid cap of the vector kernels
 constexpr uint64_t kSecondGrid = 256;
+constexpr uint64_t kHotGrid = 512;      // two LDS-heavy blocks per CU
 
 template <uint32_t kLog2G>
-int LaunchSegmentUpdateG(bool with_long, unsigned grid, const SegUpdateArgs& a, hipStream_t s) {
-  if (with_long)
-    hipLaunchKernelGGL((SegmentUpdateKernel<kLog2G, true>), dim3(grid), dim3(kBlock), 0, s, a);
-  else
-    hipLaunchKernelGGL((SegmentUpdateKernel<kLog2G, false>), dim3(grid), dim3(kBlock), 0, s, a);
-  EPS_HIP_LAUNCHED("segment update");
+int LaunchRowRun(unsigned grid, const VecArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL((RowRunKernel<kLog2G>), dim3(grid), dim3(kBlock), 0, s, a);
+  EPS_HIP_LAUNCHED("row update");
   return EPS_HIP_OK;
 }
 
-int LaunchSegmentUpdate(uint32_t cls, bool with_long, unsigned grid, const SegUpdateArgs& a,
-                        hipStream_t s) {
+// Hot rows (any vector class) when `hot`, else the other rows of class `cls`.
+int LaunchVectorUpdate(uint32_t cls, bool hot, unsigned grid, const VecArgs& a, hipStream_t s) {
+  if (hot) {
+    hipLaunchKernelGGL(HotSliceKernel, dim3(grid), dim3(kBlock), 0, s, a);
+    EPS_HIP_LAUNCHED("hot row update");
+    return EPS_HIP_OK;
+  }
   switch (cls) {
-    case 0: return LaunchSegmentUpdateG<2>(with_long, grid, a, s);
-    case 1: return LaunchSegmentUpdateG<3>(with_long, grid, a, s);
-    case 2: return LaunchSegmentUpdateG<4>(with_long, grid, a, s);
-    case 3: return LaunchSegmentUpdateG<5>(with_long, grid, a, s);
-    case 4: return LaunchSegmentUpdateG<6>(with_long, grid, a, s);
-    default: return Fail(EPS_HIP_INVALID_ARGUMENT, "no segment kernel for this dimension class");
+    case 0: return LaunchRowRun<2>(grid, a, s);
+    case 1: return LaunchRowRun<3>(grid, a, s);
+    case 2: return LaunchRowRun<4>(grid, a, s);
+    case 3: return LaunchRowRun<5>(grid, a, s);
+    case 4: return LaunchRowRun<6>(grid, a, s);
+    default: return Fail(EPS_HIP_INVALID_ARGUMENT, "no vector kernel for this dimension class");
   }
 }
 
@@ -756,41 +895,40 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
   }
   for (uint32_t f = 0; f < feature_count; ++f) a.grad[f] = features[f].gradients;
   if (!reduce) {
-    // Vector classes: the segment-list kernels (long units in the first launch).
-    SegUpdateArgs sa{};
-    for (uint32_t k = 0; k < table_count; ++k) sa.t[k] = a.t[k];
-    for (uint32_t f = 0; f < feature_count; ++f) sa.grad[f] = features[f].gradients;
-    sa.keys = a.keys;
-    sa.rs = a.rs;
-    sa.seg_start = reinterpret_cast<const uint32_t*>(ws + L.seg_start);
-    sa.long_list = reinterpret_cast<const uint32_t*>(ws + L.long_list);
-    sa.ctrl = a.ctrl;
-    sa.bounds = bounds;
-    sa.row_bits = plan.row_bits;
-    sa.slices = 1;
+    // Vector classes: hot rows (sliced) first, then the other rows per class.
+    VecArgs va{};
+    for (uint32_t k = 0; k < table_count; ++k) va.t[k] = a.t[k];
+    for (uint32_t f = 0; f < feature_count; ++f) va.grad[f] = features[f].gradients;
+    va.keys = a.keys;
+    va.rs = a.rs;
+    va.hot = reinterpret_cast<const uint32_t*>(ws + L.long_list);
+    va.ctrl = a.ctrl;
+    va.bounds = bounds;
+    va.row_bits = plan.row_bits;
+    va.slices = 1;
     for (uint32_t t = 0; t < table_count; ++t)
       if (DimClass(tables[t].dim) < kClasses - 1)
-        sa.slices = std::max(sa.slices, (tables[t].dim + kSlice - 1) / kSlice);
+        va.slices = std::max(va.slices, (tables[t].dim + kSlice - 1) / kSlice);
     uint64_t vector_occurrences = 0;
     for (uint32_t cls = 0; cls + 1 < kClasses; ++cls) vector_occurrences += plan.class_occurrences[cls];
-    const uint64_t long_units = (vector_occurrences / (kShortRefs + 1)) * sa.slices;
-    bool first = true;
-    for (uint32_t cls = 0; cls + 1 < kClasses; ++cls) {
-      if (!plan.class_occurrences[cls]) continue;
-      sa.cls = cls;
-      const uint64_t groups = kBlock >> (cls + 2);
-      uint64_t blocks = (plan.class_occurrences[cls] + groups - 1) / groups;
-      if (first) blocks = std::max<uint64_t>(blocks, (long_units + 3) / 4);
-      for (int phase = kPrimary; phase <= kSecond; phase <<= 1) {
-        if (!(phases & phase)) continue;
-        sa.fallback = phase == kSecond;
-        // The checked apply runs only after a validate-only pass; its launch
-        // usually exits at once, so it gets a small grid.
-        const unsigned grid = unsigned(std::max<uint64_t>(1, std::min<uint64_t>(
-            blocks, phase == kSecond ? kSecondGrid : kSegmentGrid)));
-        EPS_HIP_TRY(LaunchSegmentUpdate(cls, first, grid, sa, s));
+    const uint64_t hot_units = (vector_occurrences / (kLongRefs + 1)) * va.slices;
+    for (int phase = kPrimary; phase <= kSecond; phase <<= 1) {
+      if (!(phases & phase)) continue;
+      va.fallback = phase == kSecond;
+      // The checked apply runs only after a validate-only pass; its launches
+      // usually exit at once, so they get small grids.
+      const uint64_t cap = phase == kSecond ? kSecondGrid : kVectorGrid;
+      if (hot_units) {
+        const uint64_t blocks = std::min<uint64_t>((hot_units + 3) / 4, std::min(cap, kHotGrid));
+        EPS_HIP_TRY(LaunchVectorUpdate(0, true, unsigned(blocks), va, s));
       }
-      first = false;
+      for (uint32_t cls = 0; cls + 1 < kClasses; ++cls) {
+        if (!plan.class_occurrences[cls]) continue;
+        va.cls = cls;
+        const uint64_t blocks = std::min<uint64_t>(
+            std::max<uint64_t>(1, (plan.class_occurrences[cls] + kRunPositions - 1) / kRunPositions), cap);
+        EPS_HIP_TRY(LaunchVectorUpdate(cls, false, unsigned(blocks), va, s));
+      }
     }
   }
   for (uint32_t cls = 0; cls < kClasses; ++cls) {

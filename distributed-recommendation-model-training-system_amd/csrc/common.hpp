@@ -20,10 +20,8 @@ constexpr uint32_t kMaxPasses = 4;
 constexpr uint32_t kKeygenItems = 4;      // occurrences per keygen thread
 constexpr uint32_t kClasses = 6;          // 5 vector widths + generic
 constexpr uint32_t kRefRowBits = 27;      // gradient row bits in a reference word
-constexpr uint32_t kShortRefs = 16;       // segments up to this many references: short path
-constexpr uint32_t kSlice = 16;           // columns per long-path work unit
-constexpr uint32_t kSliceLog2 = 4;
-constexpr uint32_t kMaxSlices = 16;       // 256 / kSlice (vector classes have dim <= 256)
+constexpr uint32_t kLongRefs = 128;       // rows with more references take the sliced path
+constexpr uint32_t kSlice = 4;            // columns per sliced-path work unit
 
 // Control block at offset 0 of a push or update workspace (256 bytes).
 struct Control {
@@ -34,12 +32,11 @@ struct Control {
   uint32_t valid_count;     // prepared occurrences that are on this device
   uint32_t mode;            // guard decision of the last push
   uint32_t done_counter;    // last-block detection (self-resetting)
-  uint32_t unique_count;    // segments (unique rows) of the prepared push
+  uint32_t unique_count;
   uint32_t tile_counter[kMaxPasses];
   uint32_t class_count[8];  // prepared occurrences per dimension class
-  uint32_t long_count;      // entries of the long-segment list
-  uint32_t seg_class_count[8];  // segments per dimension class
-  uint32_t pad[35];
+  uint32_t long_count;      // entries of the hot-row list
+  uint32_t pad[43];
 };
 static_assert(sizeof(Control) == 256, "control block is 256 bytes");
 
@@ -52,7 +49,7 @@ struct Bounds { uint32_t v[kBoundSlots][4]; };
 struct PushLayout {
   uint64_t n, tiles;
   uint64_t hist, look, keys_a, keys_b, vals_a, vals_b, refscale, sorted_rs, flags, ranks,
-      block_sums, tile_heads, seg_start, long_list, total;
+      block_sums, long_list, total;
   explicit PushLayout(uint64_t occurrences) {
     n = occurrences;
     tiles = (n + kSortTile - 1) / kSortTile;
@@ -69,9 +66,7 @@ struct PushLayout {
     flags = at; at = align(at + n * 4);
     ranks = at; at = align(at + n * 4);
     block_sums = at; at = align(at + ((n + 1023) / 1024 + 1) * 4);
-    tile_heads = at; at = align(at + (tiles + 1) * 4);
-    seg_start = at; at = align(at + (n + 1) * 4);
-    long_list = at; at = align(at + (n / kShortRefs + 1) * 4);
+    long_list = at; at = align(at + (n / kLongRefs + 1) * 4);
     total = at;
   }
 };
@@ -86,12 +81,23 @@ int Check(hipError_t e, const char* what);
 inline hipStream_t AsStream(void* s) { return static_cast<hipStream_t>(s); }
 
 // ---- device helpers ----
+// Every buffer this library reads or writes is global memory (device memory,
+// or pinned host memory through its mapped address).  Pointers that kernels
+// fetch from LDS tables would otherwise compile to FLAT accesses, which also
+// count against the LDS wait counter, so each LDS wait would stall on every
+// outstanding global load; these accessors name the global address space.
+#define EPS_GLOBAL __attribute__((address_space(1)))
+typedef float EpsF4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float4 Load4(const float* p) {
-  return *reinterpret_cast<const float4*>(p);
+  const EpsF4 v = *(const EPS_GLOBAL EpsF4*)(p);
+  return make_float4(v.x, v.y, v.z, v.w);
 }
 __device__ __forceinline__ void Store4(float* p, float4 v) {
-  *reinterpret_cast<float4*>(p) = v;
+  const EpsF4 x = {v.x, v.y, v.z, v.w};
+  *(EPS_GLOBAL EpsF4*)(p) = x;
 }
+__device__ __forceinline__ float LoadF(const float* p) { return *(const EPS_GLOBAL float*)(p); }
+__device__ __forceinline__ void StoreF(float* p, float v) { *(EPS_GLOBAL float*)(p) = v; }
 __device__ __forceinline__ uint32_t AbsBits(float x) { return __float_as_uint(x) & 0x7fffffffu; }
 __device__ __forceinline__ bool Finite(float x) { return AbsBits(x) < 0x7f800000u; }
 

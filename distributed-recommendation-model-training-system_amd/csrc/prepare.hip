@@ -317,104 +317,28 @@ __global__ void ScanApplyKernel(const uint32_t* flags, const uint32_t* block_sum
   }
 }
 
-// ---- segment list: one entry per unique row, in sorted (key) order ----
-// A tile is kSortTile sorted positions; thread t owns the kSortItems
-// consecutive positions [tile*kSortTile + t*kSortItems, ... + kSortItems), so
-// head positions come out in order after one block scan.
-
-// Head flags (bit k = position base+k starts a segment) of one thread's run.
-__device__ __forceinline__ uint32_t HeadBits(const uint32_t* keys, uint32_t base, uint32_t valid,
-                                             uint32_t* last_key) {
-  uint32_t k[kSortItems];
-  if (base + kSortItems <= valid) {
-    const uint4* v = reinterpret_cast<const uint4*>(keys + base);
-#pragma unroll
-    for (uint32_t i = 0; i < kSortItems / 4; ++i) {
-      const uint4 x = v[i];
-      k[4 * i] = x.x; k[4 * i + 1] = x.y; k[4 * i + 2] = x.z; k[4 * i + 3] = x.w;
-    }
-  } else {
-#pragma unroll
-    for (uint32_t i = 0; i < kSortItems; ++i) k[i] = base + i < valid ? keys[base + i] : 0u;
-  }
-  uint32_t prev = (base > 0 && base <= valid) ? keys[base - 1] : ~k[0];
-  uint32_t bits = 0;
-#pragma unroll
-  for (uint32_t i = 0; i < kSortItems; ++i) {
-    if (base + i < valid && k[i] != prev) bits |= 1u << i;
-    prev = k[i];
-  }
-  if (last_key) *last_key = prev;
-  return bits;
-}
-
-__global__ void __launch_bounds__(kBlock) SegCountKernel(const uint32_t* keys, const Control* ctrl,
-                                                         uint32_t* tile_heads) {
-  __shared__ uint32_t s_wave[4];
-  const uint32_t valid = ctrl->valid_count;
-  const uint32_t base = blockIdx.x * kSortTile + threadIdx.x * kSortItems;
-  uint32_t count = base < valid ? uint32_t(__popc(HeadBits(keys, base, valid, nullptr))) : 0u;
-  for (int o = 32; o > 0; o >>= 1) count += __shfl_xor(count, o);
-  if ((threadIdx.x & (kWave - 1)) == 0) s_wave[threadIdx.x / kWave] = count;
-  __syncthreads();
-  if (threadIdx.x == 0) tile_heads[blockIdx.x] = s_wave[0] + s_wave[1] + s_wave[2] + s_wave[3];
-}
-
-struct SegArgs {
+// ---- hot rows: segments of more than kLongRefs references ----
+// Keys are sorted, so a segment that starts at p has more than kLongRefs
+// references exactly when keys[p + kLongRefs] == keys[p]: one test per
+// position, no scan.  Only vector dimension classes are listed (the generic
+// class keeps its own kernel).  The list order is irrelevant: rows are
+// independent.
+struct HotArgs {
   const uint32_t* keys;
-  const uint32_t* tile_offsets;   // exclusive scan of the per-tile head counts
-  uint32_t* seg_start;
-  uint32_t* long_list;
+  uint32_t* hot;
   Control* ctrl;
-  uint32_t row_bits;
-  uint32_t class_start[kClasses + 1];
+  uint32_t row_bits, vector_keys;  // key indices below vector_keys are vector classes
 };
 
-// Writes seg_start[s] (first sorted position of segment s), counts segments
-// per dimension class and lists the vector-class segments longer than
-// kShortRefs (their order in the list is irrelevant: segments are independent).
-__global__ void __launch_bounds__(kBlock) SegWriteKernel(SegArgs a) {
-  __shared__ uint32_t s_heads[kSortTile];
-  __shared__ uint32_t s_scan[4];
-  __shared__ uint32_t s_class[8];
-  __shared__ uint32_t s_total;
+__global__ void __launch_bounds__(kBlock) HotListKernel(HotArgs a) {
   const uint32_t valid = a.ctrl->valid_count;
-  const uint32_t tile_begin = blockIdx.x * kSortTile;
-  const uint32_t base = tile_begin + threadIdx.x * kSortItems;
-  if (threadIdx.x < 8) s_class[threadIdx.x] = 0;
-  const uint32_t bits = base < valid ? HeadBits(a.keys, base, valid, nullptr) : 0u;
-  const uint32_t count = uint32_t(__popc(bits));
-  const uint32_t before = BlockExclusiveScan(count, s_scan);
-  if (threadIdx.x == kBlock - 1) s_total = before + count;
-  const uint32_t out0 = a.tile_offsets[blockIdx.x];
-  uint32_t h = before;
-#pragma unroll
-  for (uint32_t i = 0; i < kSortItems; ++i) {
-    if (bits & (1u << i)) {
-      s_heads[h] = base + i;
-      a.seg_start[out0 + h] = base + i;
-      ++h;
-    }
-  }
-  __syncthreads();
-  const uint32_t total = s_total;
-  const uint32_t tile_end = min(tile_begin + kSortTile, valid);
-  for (uint32_t i = threadIdx.x; i < total; i += kBlock) {
-    const uint32_t p = s_heads[i];
-    const uint32_t key = a.keys[p];
-    const uint32_t next = i + 1 < total ? s_heads[i + 1] : SegmentEndSearch(a.keys, tile_end, valid, key);
-    const uint32_t k = key >> a.row_bits;
-    uint32_t cls = 0;
-    while (cls + 1 < kClasses && k >= a.class_start[cls + 1]) ++cls;
-    atomicAdd(&s_class[cls], 1u);
-    if (next - p > kShortRefs && cls + 1 < kClasses) {
-      const uint32_t at = atomicAdd(&a.ctrl->long_count, 1u);
-      a.long_list[at] = out0 + i;
-    }
-  }
-  __syncthreads();
-  if (threadIdx.x < kClasses && s_class[threadIdx.x])
-    atomicAdd(&a.ctrl->seg_class_count[threadIdx.x], s_class[threadIdx.x]);
+  const uint32_t p = blockIdx.x * kBlock + threadIdx.x;
+  if (p + kLongRefs >= valid) return;
+  const uint32_t key = a.keys[p];
+  if ((key >> a.row_bits) >= a.vector_keys) return;
+  if (p > 0 && a.keys[p - 1] == key) return;
+  if (a.keys[p + kLongRefs] != key) return;
+  a.hot[atomicAdd(&a.ctrl->long_count, 1u)] = p;
 }
 
 struct UniqueArgs {
@@ -592,25 +516,15 @@ int eps_hip_prepare(const eps_hip_table* tables, uint32_t table_count,
                        &ctrl->tile_counter[p]);
     EPS_HIP_LAUNCHED("radix pass");
   }
-  // Segment list of the sorted keys (unique rows in key order, long segments).
-  const uint32_t* sorted = keys[plan.passes % 2];
-  auto* tile_heads = reinterpret_cast<uint32_t*>(ws + L.tile_heads);
-  hipLaunchKernelGGL(SegCountKernel, dim3(unsigned(L.tiles)), dim3(kBlock), 0, s, sorted, ctrl,
-                     tile_heads);
-  EPS_HIP_LAUNCHED("segment count");
-  hipLaunchKernelGGL(ScanTopKernel, dim3(1), dim3(kBlock), 0, s, tile_heads, uint32_t(L.tiles), ctrl,
-                     static_cast<uint64_t*>(nullptr));
-  EPS_HIP_LAUNCHED("segment scan");
-  SegArgs sa{};
-  sa.keys = sorted;
-  sa.tile_offsets = tile_heads;
-  sa.seg_start = reinterpret_cast<uint32_t*>(ws + L.seg_start);
-  sa.long_list = reinterpret_cast<uint32_t*>(ws + L.long_list);
-  sa.ctrl = ctrl;
-  sa.row_bits = plan.row_bits;
-  for (uint32_t c = 0; c <= kClasses; ++c) sa.class_start[c] = plan.class_start[c];
-  hipLaunchKernelGGL(SegWriteKernel, dim3(unsigned(L.tiles)), dim3(kBlock), 0, s, sa);
-  EPS_HIP_LAUNCHED("segment write");
+  // Hot rows of the sorted keys.
+  HotArgs ha{};
+  ha.keys = keys[plan.passes % 2];
+  ha.hot = reinterpret_cast<uint32_t*>(ws + L.long_list);
+  ha.ctrl = ctrl;
+  ha.row_bits = plan.row_bits;
+  ha.vector_keys = plan.class_start[kClasses - 1];
+  hipLaunchKernelGGL(HotListKernel, dim3(unsigned((n + kBlock - 1) / kBlock)), dim3(kBlock), 0, s, ha);
+  EPS_HIP_LAUNCHED("hot rows");
   return EPS_HIP_OK;
 }
 

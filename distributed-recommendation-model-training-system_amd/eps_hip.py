@@ -12,12 +12,14 @@ from __future__ import annotations
 
 import ctypes as C
 import math
+import os
 import pathlib
 
 import numpy as np
 
 HERE = pathlib.Path(__file__).resolve().parent
-LIB_PATH = HERE / "libeps_hip.so"
+# The in-tree build; EPS_HIP_LIBRARY names another build of the same ABI.
+LIB_PATH = pathlib.Path(os.environ.get("EPS_HIP_LIBRARY", HERE / "libeps_hip.so"))
 
 OK, INVALID_ARGUMENT, UNAVAILABLE, STALE_GENERATION, RETIRED, CAPACITY, RUN_FAILED = range(7)
 SUM, MEAN, SEQUENCE, WEIGHTED_SUM = 0, 1, 2, 3
