@@ -42,10 +42,14 @@ constexpr uint32_t kFallbackGrid = 2048;
 
 // ---------------------------------------------------------------------------
 // Gradient maximum and the guard decision (last block).
+// A guarded input array: gradient values, reference scales, or 64-bit
+// indices that must all be below `limit` (checked before anything is written).
+enum SpanKind : uint32_t { kGradientSpan = 0, kScaleSpan = 1, kIndexSpan = 2 };
 struct Span {
   const float* p;
   uint64_t count;
-  uint32_t block_begin, is_scale;
+  uint32_t block_begin, kind;
+  uint64_t limit;
 };
 struct GuardTable { float beta1, beta2, lr, eps; };
 struct GuardArgs {
@@ -67,7 +71,11 @@ __global__ void __launch_bounds__(kBlock) GradMaxKernel(GuardArgs a) {
   const uint64_t begin = uint64_t(blockIdx.x - sp.block_begin) * per_block;
   const uint64_t end = min(begin + per_block, sp.count);
   uint32_t m = 0;
-  if (reinterpret_cast<uintptr_t>(sp.p) % 16 == 0) {
+  bool out_of_range = false;
+  if (sp.kind == kIndexSpan) {
+    const uint64_t* idx = reinterpret_cast<const uint64_t*>(sp.p);
+    for (uint64_t i = begin + threadIdx.x; i < end; i += kBlock) out_of_range |= idx[i] >= sp.limit;
+  } else if (reinterpret_cast<uintptr_t>(sp.p) % 16 == 0) {
     // All kMaxItems loads of a thread are issued before any is consumed.
     const uint64_t vend = begin + ((end - begin) & ~uint64_t(3));
     float4 x[kMaxItems];
@@ -85,13 +93,14 @@ __global__ void __launch_bounds__(kBlock) GradMaxKernel(GuardArgs a) {
   }
   __shared__ uint32_t s_max[4];
   __shared__ bool s_last;
+  if (out_of_range) atomicOr(&a.ctrl->prep_status, EPS_HIP_STATUS_BAD_INDEX);
   m = WaveMax(m);
   if ((threadIdx.x & (kWave - 1)) == 0) s_max[threadIdx.x / kWave] = m;
   __syncthreads();
   Control* ctrl = a.ctrl;
   if (threadIdx.x == 0) {
     const uint32_t bm = max(max(s_max[0], s_max[1]), max(s_max[2], s_max[3]));
-    if (bm) atomicMax(sp.is_scale ? &ctrl->max_scale_bits : &ctrl->max_src_bits, bm);
+    if (bm) atomicMax(sp.kind == kScaleSpan ? &ctrl->max_scale_bits : &ctrl->max_src_bits, bm);
     __threadfence();
     s_last = atomicAdd(&ctrl->done_counter, 1u) == gridDim.x - 1;
   }
@@ -826,7 +835,7 @@ uint32_t Log2G(uint32_t dim) {
 
 int LaunchGuard(GuardArgs& g, uint64_t blocks, hipStream_t s) {
   if (!blocks) {  // nothing to scan: still decide (one block over an empty span)
-    g.span[0] = Span{nullptr, 0, 0, 0};
+    g.span[0] = Span{nullptr, 0, 0, kGradientSpan, 0};
     g.spans = 1;
     blocks = 1;
   }
@@ -995,7 +1004,7 @@ int eps_hip_push_begin(const eps_hip_table* tables, const eps_hip_optimizer* opt
     const uint64_t rows = in.pooling == EPS_HIP_POOL_SEQUENCE ? in.occurrences : in.bags;
     const uint64_t count = rows * tables[in.table].dim;
     if (!count) continue;
-    g.span[g.spans++] = Span{in.gradients, count, uint32_t(blocks), 0};
+    g.span[g.spans++] = Span{in.gradients, count, uint32_t(blocks), kGradientSpan, 0};
     blocks += SpanBlocks(count);
   }
   for (uint32_t t = 0; t < table_count; ++t) {
@@ -1091,19 +1100,25 @@ static int RunRows(const eps_hip_table* table, const eps_hip_optimizer* optimize
   if (!slots || !src) return Fail(EPS_HIP_INVALID_ARGUMENT, "null update buffers");
   GuardArgs g{};
   uint64_t blocks = 0;
-  if (src_values) {
-    g.span[g.spans++] = Span{src, src_values, 0, 0};
-    blocks += SpanBlocks(src_values);
-  }
-  if (scales && references) {
-    g.span[g.spans++] = Span{scales, references, uint32_t(blocks), 1};
-    blocks += SpanBlocks(references);
+  auto add = [&](const void* p, uint64_t count, SpanKind kind, uint64_t limit) {
+    if (!count) return;
+    g.span[g.spans++] = Span{static_cast<const float*>(p), count, uint32_t(blocks), kind, limit};
+    blocks += SpanBlocks(count);
+  };
+  add(src, src_values, kGradientSpan, 0);
+  if (scales) add(scales, references, kScaleSpan, 0);
+  // Caller-provided indices are range-checked before the update, so a bad
+  // slot or reference rejects it instead of touching memory out of range.
+  add(slots, rows, kIndexSpan, table->rows);
+  if (offsets) {
+    add(offsets, rows + 1, kIndexSpan, references + 1);
+    add(sources, references, kIndexSpan, src_values / table->dim);
   }
   const TableDesc d = MakeTable(*table, *optimizer);
   g.t[0] = GuardTable{optimizer->beta1, optimizer->beta2, d.lr, optimizer->epsilon};
   g.tables = 1;
   g.reset_scale = 1;
-  g.use_prep_status = 0;
+  g.use_prep_status = 1;  // the index checks report there
   g.refs_host = std::max<uint64_t>(1, offsets ? references : 1);
   g.ctrl = ctrl;
   g.bounds = static_cast<const Bounds*>(bounds);

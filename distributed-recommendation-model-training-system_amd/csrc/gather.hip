@@ -187,6 +187,18 @@ __global__ void AddContributionKernel(float* output, const float* source, const 
   }
 }
 
+// NormalizeMean (src/cuda/cache_backend.cu:134-139): output[r, d] /= len[r]
+// for len[r] != 0, an IEEE float divide by the length converted to float.
+__global__ void NormalizeMeanKernel(float* output, const uint64_t* lengths, uint64_t rows,
+                                    uint32_t dim) {
+  const uint64_t values = rows * dim;
+  for (uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < values;
+       i += uint64_t(blockDim.x) * gridDim.x) {
+    const uint64_t len = lengths[i / dim];
+    if (len) output[i] = output[i] / (float)len;
+  }
+}
+
 __global__ void FillKernel(uint32_t* target, uint32_t value, uint64_t count) {
   for (uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < count;
        i += uint64_t(blockDim.x) * gridDim.x)
@@ -452,6 +464,16 @@ int eps_hip_gather(const eps_hip_gather_part* parts, uint32_t count, uint32_t* s
   if (!blocks) return EPS_HIP_OK;
   hipLaunchKernelGGL(GatherKernel, dim3(blocks), dim3(kBlock), 0, AsStream(stream), args);
   EPS_HIP_LAUNCHED("gather");
+  return EPS_HIP_OK;
+}
+
+int eps_hip_normalize_mean(float* output, const uint64_t* lengths, uint64_t rows, uint32_t dim,
+                           void* stream) {
+  if (!rows) return EPS_HIP_OK;
+  if (!output || !lengths || !dim) return Fail(EPS_HIP_INVALID_ARGUMENT, "invalid mean normalisation");
+  hipLaunchKernelGGL(NormalizeMeanKernel, dim3(GridFor(rows * dim)), dim3(kBlock), 0,
+                     AsStream(stream), output, lengths, rows, dim);
+  EPS_HIP_LAUNCHED("normalize mean");
   return EPS_HIP_OK;
 }
 

@@ -75,6 +75,8 @@ SYMBOLS = {
     "eps_hip_gather": (C.c_int, [C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p]),
     "eps_hip_add_contribution": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64,
                                            C.c_uint32, C.c_void_p]),
+    "eps_hip_normalize_mean": (C.c_int, [C.c_void_p, C.c_void_p, C.c_uint64, C.c_uint32,
+                                         C.c_void_p]),
     "eps_hip_push_workspace_bytes": (C.c_uint64, [C.c_uint64]),
     "eps_hip_prepare": (C.c_int, [C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint32, C.c_void_p,
                                   C.c_uint64, C.c_void_p]),

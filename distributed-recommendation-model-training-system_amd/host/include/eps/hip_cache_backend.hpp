@@ -1,0 +1,64 @@
+// eps/hip_cache_backend.hpp -- MI355X (gfx950) implementation of the GPU cache
+// agent.
+//
+// Drop-in for the reference's CudaCacheBackend
+// (include/eps/cuda_cache_backend.hpp:5-37): same operations, options and
+// statistics, same error behaviour, one FIFO worker per backend.  Device work
+// goes through the C ABI of include/eps_hip.h (libeps_hip.so); this class owns
+// the AoS [w | m | v] tables, the slot free lists, the row generations and
+// update counters, pinned staging, one stream and the device-output budget.
+#pragma once
+
+#include <future>
+#include <memory>
+#include <vector>
+
+#include "eps/cache_agent.hpp"
+#include "eps/device_features.hpp"
+
+namespace eps {
+
+// CudaCacheOptions field for field, with MI355X-sized limits: rows_per_table
+// up to 2^31 and transfer_bytes up to 2 GiB (288 GB of HBM per device).
+struct HipCacheOptions {
+  AgentId agent = 0;
+  int device = 0;
+  std::uint64_t state_bytes = 64ULL << 20;
+  std::uint64_t rows_per_table = 4096;
+  std::uint64_t transfer_bytes = 16ULL << 20;
+  std::uint64_t outstanding_output_bytes = 64ULL << 20;
+  std::uint32_t output_alignment = 4;
+};
+
+struct HipMemoryStats {
+  std::uint64_t resident_state_bytes;
+  std::uint64_t staging_device_bytes;
+  std::uint64_t outstanding_output_bytes;
+  std::uint64_t output_allocations;
+  bool operator==(const HipMemoryStats&) const = default;
+};
+
+class HipCacheBackend final : public GpuCacheAgent {
+ public:
+  explicit HipCacheBackend(HipCacheOptions options = {});
+  ~HipCacheBackend() override;
+  std::future<Result<Ack>> Define(TableDefinition) override;
+  std::future<Result<std::uint64_t>> FreeSlots(TableId) override;
+  std::future<Result<std::vector<LocatedRow>>> Load(MigrationPlan, std::vector<RowState>) override;
+  std::future<Result<std::vector<TensorBlock>>> GatherHost(std::vector<AgentWork>,
+                                                           std::vector<FeatureInput>) override;
+  std::future<Result<std::vector<DeviceTensorBlock>>> GatherDevice(
+      std::vector<AgentWork>, std::vector<FeatureInput>) override;
+  std::future<Result<Ack>> ApplyHost(UpdateContext, RowGradients) override;
+  std::future<Result<Ack>> ApplyCompact(UpdateContext, CompactGradients) override;
+  std::future<Result<std::vector<RowState>>> ReadBack(MigrationPlan) override;
+  std::future<Result<Ack>> CommitEviction(MigrationPlan) override;
+  std::future<Result<HipMemoryStats>> MemoryStats();
+  std::future<Result<std::vector<DeviceTensorBlock>>> AssembleFeatures(DeviceAssemblyRequest);
+
+ private:
+  struct Impl;
+  std::unique_ptr<Impl> impl_;
+};
+
+}  // namespace eps

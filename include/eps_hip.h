@@ -152,6 +152,12 @@ int eps_hip_gather(const eps_hip_gather_part* parts, uint32_t count, uint32_t* s
 int eps_hip_add_contribution(float* output, const float* source, const uint64_t* positions,
                              uint64_t values, uint32_t dim, void* stream);
 
+/* In-place mean of assembled pooled sums: output[r*dim + d] /= (float)lengths[r]
+ * where lengths[r] != 0.  Replaces NormalizeMean (:134-139) as used by
+ * AssembleFeatures (:686-692). */
+int eps_hip_normalize_mean(float* output, const uint64_t* lengths, uint64_t rows, uint32_t dim,
+                           void* stream);
+
 /* ---- push: device dedup + duplicate-id aggregation + fused sparse Adam ---- */
 /* Workspace for up to `occurrences` total occurrences over the call's features. */
 uint64_t eps_hip_push_workspace_bytes(uint64_t occurrences);

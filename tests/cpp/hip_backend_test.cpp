@@ -1,0 +1,384 @@
+// hip_backend_test.cpp -- eps::HipCacheBackend against the oracle, on a GPU.
+//
+// Re-expresses the scenarios of the reference's tests/cuda_tests.cpp (device
+// backend vs the protocol reference backend): multi-table pooled gathers with
+// holes, a sequence feature and an empty bag; the transfer_unique route;
+// device results and their lifetime beyond the backend; seven ApplyHost and
+// two ApplyCompact steps on a bounded table (clipping exercised); overflow
+// rejection that leaves every row untouched; slot reclamation and stale
+// generations after reuse; the atomic slot reserve of concurrent loads; plus
+// device feature assembly (tests/device_pull_tests.cpp's ReferenceAssembly).
+// Expected values come from the oracle (oracle/eps_oracle.h, the CPU
+// restatement of the reference shard) and are compared bit for bit.
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <iostream>
+#include <limits>
+#include <map>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "eps/hip_cache_backend.hpp"
+#include "eps_oracle.h"
+
+using namespace eps;
+
+namespace {
+
+int g_checks = 0;
+
+void Check(bool ok, const std::string& why) {
+  ++g_checks;
+  if (!ok) throw std::runtime_error(why);
+}
+
+template <typename T>
+T Take(std::future<Result<T>> f) {
+  auto r = f.get();
+  if (auto e = std::get_if<Error>(&r)) throw std::runtime_error("backend error: " + e->message);
+  return std::get<T>(std::move(r));
+}
+
+template <typename T>
+Error::Code Fails(std::future<Result<T>> f, const std::string& what) {
+  auto r = f.get();
+  Check(std::holds_alternative<Error>(r), what + " was accepted");
+  return std::get<Error>(r).code;
+}
+
+bool SameBits(const std::vector<float>& a, const std::vector<float>& b) {
+  return a.size() == b.size() && (a.empty() || std::memcmp(a.data(), b.data(), a.size() * 4) == 0);
+}
+
+constexpr float kLr = 0.01f, kBeta1 = 0.9f, kBeta2 = 0.999f, kEps = 1e-8f;
+constexpr float kMin = -0.015f, kMax = 0.015f;
+
+TableDefinition Table(TableId id, std::uint32_t dim) {
+  TableDefinition t{id, dim, 1, 1, {kLr, kBeta1, kBeta2, kEps, 0.9f, 0.999f}, -0.1f, 0.1f, 42};
+  if (id == 1) t.optimizer.weight_bounds = WeightBounds{kMin, kMax};
+  return t;
+}
+
+// Deterministic initial rows: table 1 keys 1..4 (dim 128), table 2 keys 1..2 (dim 64).
+std::vector<RowState> States() {
+  std::vector<RowState> rows;
+  for (TableId table : {1u, 2u}) {
+    const std::uint32_t dim = table == 1 ? 128 : 64;
+    for (Key key = 1; key <= (table == 1 ? 4u : 2u); ++key) {
+      RowState r{{table, key}, std::vector<float>(dim), std::vector<float>(dim), std::vector<float>(dim), 3};
+      for (std::uint32_t d = 0; d < dim; ++d) {
+        r.weights[d] = 0.04f * std::cos(float(key * 5 + d * 3 + table));
+        r.first_moment[d] = 0.002f * float((d + key) % 7);
+        r.second_moment[d] = 0.001f * float(1 + (d + 2 * key) % 4);
+      }
+      rows.push_back(std::move(r));
+    }
+  }
+  return rows;
+}
+
+MigrationPlan Plan(const std::vector<RowState>& rows, const std::string& id = "load") {
+  MigrationPlan p{id, 0, {}, Placement::gpu, 0};
+  for (const auto& r : rows) p.rows.push_back({r.row, 0, Placement::loading, 0, 1, 0});
+  return p;
+}
+
+// Mean with a hole (key 999 served elsewhere), a sequence, and a sum with an empty bag.
+std::vector<FeatureInput> Layouts() {
+  return {{1, 0, Pooling::mean, {2, 1, 999, 2, 4}, {0, 3, 5}, {3, 2}},
+          {1, 1, Pooling::sequence, {3, 1, 3}, {0, 2, 3}, {2, 1}},
+          {2, 2, Pooling::sum, {2, 1, 2}, {0, 3, 3}, {3, 0}}};
+}
+
+const LocatedRow& Locate(const std::vector<LocatedRow>& located, TableId table, Key key) {
+  return *std::find_if(located.begin(), located.end(),
+                       [&](const LocatedRow& l) { return l.row == RowKey{table, key}; });
+}
+
+std::vector<AgentWork> Work(const std::vector<LocatedRow>& l) {
+  return {{0, AccessRoute::resident_gpu, 0, {Locate(l, 1, 2), Locate(l, 1, 1), Locate(l, 1, 4)},
+           {0, 1, UINT64_MAX, 0, 2}, {}},
+          {1, AccessRoute::resident_gpu, 0, {Locate(l, 1, 3), Locate(l, 1, 1)}, {0, 1, 0}, {}},
+          {2, AccessRoute::resident_gpu, 0, {Locate(l, 2, 2), Locate(l, 2, 1)}, {0, 1, 0}, {}}};
+}
+
+// Host copy of the rows the backend holds, advanced with the oracle.
+struct Model {
+  std::map<std::pair<TableId, Key>, RowState> rows;
+  const RowState& Get(TableId t, Key k) const { return rows.at({t, k}); }
+};
+
+// GatherHost of one work item: HostCacheBackend semantics via the oracle.
+TensorBlock Expected(const Model& model, const AgentWork& task, const FeatureInput& f, std::uint32_t dim) {
+  eps_or_feature of{f.keys.data(), f.keys.size(), f.offsets.data(), f.valid_lengths.data(), nullptr,
+                    f.valid_lengths.size(), uint32_t(f.pooling), f.feature};
+  std::vector<const float*> unique;
+  for (const auto& loc : task.rows) unique.push_back(model.Get(loc.row.table, loc.row.key).weights.data());
+  const std::uint64_t rows = f.pooling == Pooling::sequence ? f.keys.size() : f.offsets.size() - 1;
+  TensorBlock out{f.feature, {rows, dim}, std::vector<float>(rows * dim)};
+  Check(eps_or_gather_host(&of, dim, task.occurrence_to_unique.data(), task.rows.size(), unique.data(),
+                           out.values.data()) == 0,
+        "oracle gather failed");
+  return out;
+}
+
+void CompareGather(const std::vector<TensorBlock>& got, const Model& model, const std::vector<AgentWork>& work,
+                   const std::vector<FeatureInput>& layouts, const char* what) {
+  Check(got.size() == work.size(), std::string(what) + ": block count");
+  for (std::size_t i = 0; i < work.size(); ++i) {
+    const auto& f = layouts[i];
+    const std::uint32_t dim = f.table == 1 ? 128 : 64;
+    const TensorBlock want = Expected(model, work[i], f, dim);
+    Check(got[i].feature == want.feature && got[i].shape == want.shape, std::string(what) + ": layout");
+    Check(SameBits(got[i].values, want.values), std::string(what) + ": values differ from the oracle");
+  }
+}
+
+void CompareStates(const std::vector<RowState>& got, const Model& model, const char* what) {
+  for (const auto& r : got) {
+    const RowState& want = model.Get(r.row.table, r.row.key);
+    Check(r.row_updates == want.row_updates, std::string(what) + ": update counter");
+    Check(SameBits(r.weights, want.weights) && SameBits(r.first_moment, want.first_moment) &&
+              SameBits(r.second_moment, want.second_moment),
+          std::string(what) + ": state differs from the oracle");
+  }
+}
+
+void ApplyModel(Model& model, TableId table, const std::vector<Key>& keys, const std::vector<float>& g,
+                float b1p, float b2p) {
+  const std::uint32_t dim = table == 1 ? 128 : 64;
+  for (std::size_t i = 0; i < keys.size(); ++i) {
+    auto& r = model.rows.at({table, keys[i]});
+    Check(eps_or_adam_rows_ctx(r.weights.data(), r.first_moment.data(), r.second_moment.data(),
+                               g.data() + i * dim, 1, dim, kBeta1, kBeta2, kEps, kLr, b1p, b2p,
+                               table == 1, kMin, kMax) == 0,
+          "oracle Adam rejected a valid update");
+    ++r.row_updates;
+  }
+}
+
+HipCacheOptions SmallOptions(std::uint64_t rows_per_table) {
+  HipCacheOptions o;
+  o.rows_per_table = rows_per_table;
+  o.state_bytes = 1 << 20;
+  o.transfer_bytes = 1 << 20;
+  o.outstanding_output_bytes = 1 << 20;
+  return o;
+}
+
+// Two loads racing for a slot reserve: the second is refused whole.
+void AtomicReserve() {
+  HipCacheOptions o = SmallOptions(3);
+  o.state_bytes = 96;  // exactly one dim-2 table of 3 rows
+  HipCacheBackend gpu(o);
+  Take(gpu.Define(Table(99, 2)));
+  auto load = [&](Key first, std::size_t count) {
+    std::vector<RowState> states;
+    for (std::size_t n = 0; n < count; ++n) states.push_back({{99, first + n}, {0.1f, 0.2f}, {0, 0}, {0, 0}, 0});
+    auto plan = Plan(states);
+    plan.reserve_slots = 1;
+    return gpu.Load(std::move(plan), std::move(states));
+  };
+  auto first = load(1, 2), second = load(3, 1);
+  Take(std::move(first));
+  Check(Fails(std::move(second), "load into the reserve") == Error::Code::capacity_exceeded,
+        "reserve refusal code");
+  Check(Take(gpu.FreeSlots(99)) == 1, "concurrent load consumed the slot reserve");
+  Check(Fails(gpu.Define(Table(100, 2)), "define beyond the state budget") == Error::Code::capacity_exceeded,
+        "state budget code");
+}
+
+void Assembly(HipCacheBackend& gpu, const std::vector<LocatedRow>& located, const Model& model) {
+  // Device part of a mean feature and of a projected sequence feature, plus
+  // host partial sums; the mean divides once by the original lengths.
+  const std::vector<FeatureInput> layouts = {
+      {2, 7, Pooling::mean, {1, 2, 2}, {0, 2, 3}, {4, 1}},
+      {2, 8, Pooling::sequence, {2, 1}, {0, 2}, {2}}};
+  std::vector<AgentWork> work = {
+      {7, AccessRoute::resident_gpu, 0, {Locate(located, 2, 1), Locate(located, 2, 2)}, {0, 1, 1}, {}},
+      {8, AccessRoute::resident_gpu, 0, {Locate(located, 2, 2), Locate(located, 2, 1)}, {0, 1}, {}}};
+  auto device = Take(gpu.GatherDevice(work, layouts));
+  std::vector<TensorBlock> host = {{7, {2, 64}, std::vector<float>(2 * 64)}, {8, {2, 64}, std::vector<float>(2 * 64)}};
+  for (std::size_t i = 0; i < host[0].values.size(); ++i) host[0].values[i] = 0.001f * float(i % 13);
+  for (std::size_t i = 0; i < host[1].values.size(); ++i) host[1].values[i] = -0.002f * float(i % 5);
+  DeviceAssemblyRequest request;
+  request.host = host;
+  request.layouts = layouts;
+  request.device = {{device[0], {}, false}, {device[1], {}, false}};
+  request.projections = {{8, 5, {1, 3}}};  // sequence rows land at positions 1 and 3 of 5
+  auto assembled = Take(gpu.AssembleFeatures(request));
+  Check(assembled.size() == 2 && assembled[1].shape == std::vector<std::uint64_t>{5, 64}, "assembly layout");
+  // Expected (src/cuda/cache_backend.cu:664-692): a non-projected host part is
+  // copied over the zeroed output, a projected one is added to it; device
+  // parts are added after; the mean divides last.
+  std::vector<float> mean(2 * 64, 0.f), seq(5 * 64, 0.f);
+  const TensorBlock dm = Expected(model, work[0], layouts[0], 64), ds = Expected(model, work[1], layouts[1], 64);
+  for (std::size_t i = 0; i < mean.size(); ++i) {
+    float v = host[0].values[i];
+    v = v + dm.values[i];
+    const std::uint64_t len = layouts[0].valid_lengths[i / 64];
+    mean[i] = len ? v / float(len) : v;
+  }
+  for (std::size_t r = 0; r < 2; ++r) {
+    const std::uint64_t at = request.projections[0].positions[r];
+    for (std::size_t d = 0; d < 64; ++d) {
+      float v = 0.f;
+      v = v + host[1].values[r * 64 + d];
+      v = v + ds.values[r * 64 + d];
+      seq[at * 64 + d] = v;
+    }
+  }
+  assembled[0].tensor->WaitOnStream(nullptr);
+  Check(SameBits(assembled[0].tensor->CopyToHost(), mean), "assembled mean feature");
+  Check(SameBits(assembled[1].tensor->CopyToHost(), seq), "assembled projected sequence feature");
+}
+
+void Main() {
+  AtomicReserve();
+  auto gpu = std::make_shared<HipCacheBackend>(SmallOptions(8));
+  for (const auto& t : {Table(1, 128), Table(2, 64)}) Take(gpu->Define(t));
+  Take(gpu->Define(Table(1, 128)));  // identical redefinition is accepted
+  Check(Fails(gpu->Define(Table(1, 64)), "conflicting redefinition") == Error::Code::invalid_argument,
+        "redefinition code");
+  auto rows = States();
+  Model model;
+  for (const auto& r : rows) model.rows[{r.row.table, r.row.key}] = r;
+  auto plan = Plan(rows);
+  auto located = Take(gpu->Load(plan, rows));
+  Check(located[0].slot == 0 && located[1].slot == 1 && located[0].placement == Placement::gpu,
+        "slots are handed out from the bottom of the free list");
+  Check(Take(gpu->FreeSlots(1)) == 4 && Take(gpu->FreeSlots(2)) == 6, "free slots after load");
+  auto work = Work(located);
+  auto layouts = Layouts();
+  CompareGather(Take(gpu->GatherHost(work, layouts)), model, work, layouts, "resident gather");
+
+  // CPU-owned unique vectors travel with the request and use the same pooling.
+  auto cold = work;
+  for (auto& task : cold) {
+    task.route = AccessRoute::transfer_unique;
+    for (auto& loc : task.rows) {
+      loc.placement = Placement::cpu;
+      const auto& w = model.Get(loc.row.table, loc.row.key).weights;
+      task.transferred_weights.insert(task.transferred_weights.end(), w.begin(), w.end());
+    }
+  }
+  CompareGather(Take(gpu->GatherHost(cold, layouts)), model, work, layouts, "transfer_unique gather");
+  auto poisoned = cold;
+  poisoned[0].transferred_weights[3] = std::numeric_limits<float>::infinity();
+  Check(Fails(gpu->GatherHost(poisoned, layouts), "non-finite transferred weight") == Error::Code::invalid_argument,
+        "transferred weight code");
+
+  auto device = Take(gpu->GatherDevice(work, layouts));
+  std::vector<TensorBlock> before;
+  for (std::size_t i = 0; i < work.size(); ++i)
+    before.push_back(Expected(model, work[i], layouts[i], layouts[i].table == 1 ? 128 : 64));
+  for (std::size_t i = 0; i < device.size(); ++i) {
+    device[i].tensor->WaitOnStream(nullptr);
+    Check(SameBits(device[i].tensor->CopyToHost(), before[i].values), "device gather result");
+  }
+
+  float b1 = 0.9f, b2 = 0.999f;
+  const std::vector<Key> keys = {1, 2, 3, 4};
+  for (std::uint64_t step = 0; step < 7; ++step) {
+    UpdateContext c{{"hip-test", 0, step, Phase::push}, 0, 1, step, kLr, b1, b2};
+    RowGradients g;
+    for (Key key : keys) {
+      g.rows.push_back({1, key});
+      for (int d = 0; d < 128; ++d) g.values.push_back(0.05f * std::sin(float(key * 3 + d + 2 * step)));
+    }
+    Take(gpu->ApplyHost(c, g));
+    ApplyModel(model, 1, keys, g.values, b1, b2);
+    b1 *= 0.9f;
+    b2 *= 0.999f;
+    CompareGather(Take(gpu->GatherHost(work, layouts)), model, work, layouts, "gather after ApplyHost");
+  }
+  CompactGradients compact{{{1, 1}, {1, 2}, {1, 3}, {1, 4}}, 128, {}, {0, 3, 4, 6, 7},
+                           {0, 1, 0, 2, 1, 2, 0}, {1.0f / 3, 0.5f, 1.0f / 3, 1, 0.25f, 0.25f, 1}};
+  for (int source = 0; source < 3; ++source)
+    for (int d = 0; d < 128; ++d) compact.source_values.push_back(0.02f * std::cos(float(source * 7 + d)));
+  for (std::uint64_t step = 7; step < 9; ++step) {
+    UpdateContext c{{"hip-test", 0, step, Phase::push}, 0, 1, step, kLr, b1, b2};
+    Take(gpu->ApplyCompact(c, compact));
+    std::vector<float> g(4 * 128);
+    const std::vector<std::uint64_t> row_keys = {1, 2, 3, 4};
+    Check(eps_or_expand_compact(4, row_keys.data(), 128, compact.source_values.data(),
+                                compact.source_values.size(), compact.row_offsets.data(),
+                                compact.source_rows.data(), compact.scales.data(), compact.source_rows.size(),
+                                g.data()) == 0,
+          "oracle CSR expansion failed");
+    ApplyModel(model, 1, keys, g, b1, b2);
+    b1 *= 0.9f;
+    b2 *= 0.999f;
+  }
+  MigrationPlan readback{"read", 0, located, Placement::cpu, 0};
+  std::reverse(readback.rows.begin(), readback.rows.end());
+  auto original = Take(gpu->ReadBack(readback));
+  CompareStates(original, model, "ReadBack after 7 ApplyHost + 2 ApplyCompact");
+  bool clipped = false;
+  for (const auto& r : original)
+    if (r.row.table == 1)
+      for (float w : r.weights) {
+        Check(w >= kMin && w <= kMax, "bounded weight escaped its interval");
+        clipped = clipped || w == kMin || w == kMax;
+      }
+  Check(clipped, "the updates did not exercise clipping");
+
+  // Updates that would overflow are rejected whole: no row changes.
+  UpdateContext bad{{"hip-test", 0, 9, Phase::push}, 0, 1, 9, kLr, b1, b2};
+  auto overflow_compact = compact;
+  std::fill(overflow_compact.source_values.begin(), overflow_compact.source_values.end(),
+            std::numeric_limits<float>::max());
+  Fails(gpu->ApplyCompact(bad, overflow_compact), "overflowing compact update");
+  CompareStates(Take(gpu->ReadBack(readback)), model, "state after rejected compact update");
+  RowGradients overflow{{{1, 1}, {1, 3}}, std::vector<float>(2 * 128, 1.f)};
+  overflow.values.back() = std::numeric_limits<float>::max();
+  Fails(gpu->ApplyHost(bad, overflow), "overflowing update");
+  CompareStates(Take(gpu->ReadBack(readback)), model, "state after rejected update");
+  RowGradients duplicate{{{1, 1}, {1, 1}}, std::vector<float>(2 * 128, 0.f)};
+  Check(Fails(gpu->ApplyHost(bad, duplicate), "duplicate rows") == Error::Code::invalid_argument, "duplicate code");
+  UpdateContext invalid = bad;
+  invalid.learning_rate = 0.f;
+  Fails(gpu->ApplyHost(invalid, RowGradients{{{1, 2}}, std::vector<float>(128, 0.f)}), "zero learning rate");
+  auto bad_csr = compact;
+  bad_csr.source_rows[2] = 3;  // only three source rows exist
+  Fails(gpu->ApplyCompact(bad, bad_csr), "out-of-range CSR reference");
+  CompareStates(Take(gpu->ReadBack(readback)), model, "state after rejected requests");
+
+  for (std::size_t i = 0; i < device.size(); ++i)
+    Check(SameBits(device[i].tensor->CopyToHost(), before[i].values), "device result changed after updates");
+
+  Assembly(*gpu, located, model);
+  auto stats = Take(gpu->MemoryStats());
+  Check(stats.resident_state_bytes == 8ull * (128 + 64) * 12, "resident state bytes");
+
+  Take(gpu->CommitEviction(readback));
+  Check(Take(gpu->FreeSlots(1)) == 8 && Take(gpu->FreeSlots(2)) == 8, "slots reclaimed by eviction");
+  for (auto& r : rows) r = model.Get(r.row.table, r.row.key);
+  for (auto& loc : plan.rows) loc.generation += 2;
+  auto reloaded = Take(gpu->Load(plan, rows));
+  Check(Fails(gpu->GatherHost(work, layouts), "stale slot") == Error::Code::stale_generation,
+        "stale generation code");
+  auto fresh = Work(reloaded);
+  CompareGather(Take(gpu->GatherHost(fresh, layouts)), model, fresh, layouts, "gather after reload");
+
+  gpu.reset();  // device results own their memory and outlive the backend
+  for (std::size_t i = 0; i < device.size(); ++i)
+    Check(SameBits(device[i].tensor->CopyToHost(), before[i].values), "device result after backend release");
+}
+
+}  // namespace
+
+int main() {
+  try {
+    Main();
+    std::cout << "PASS HIP backend: " << g_checks
+              << " checks (gathers, optimizer states, atomic rejection, slot reuse, assembly, "
+                 "device-result lifetime)\n";
+    return 0;
+  } catch (const std::exception& e) {
+    std::cerr << "FAIL HIP backend: " << e.what() << '\n';
+    return 1;
+  }
+}

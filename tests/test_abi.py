@@ -5,6 +5,7 @@ No compute calls: this runs without a GPU.
 import ctypes
 import pathlib
 import re
+import subprocess
 
 ROOT = pathlib.Path(__file__).resolve().parents[1]
 
@@ -31,6 +32,18 @@ def test_library_exports_every_declared_symbol(pkg):
 
 def test_binding_covers_the_header(pkg):
     assert set(declared("eps_hip.h")) == set(pkg.eps_hip.SYMBOLS)
+
+
+def test_backend_library_loads(pkg):
+    """libeps_hip_backend.so (eps::HipCacheBackend) resolves against
+    libeps_hip.so and the HIP runtime; its C++ entry points are exported."""
+    path = pkg.eps_hip.HERE / "libeps_hip_backend.so"
+    ctypes.CDLL(str(path))
+    names = subprocess.run(["nm", "-DC", "--defined-only", str(path)], capture_output=True,
+                           text=True, check=True).stdout
+    for method in ("Define", "FreeSlots", "Load", "GatherHost", "GatherDevice", "ApplyHost",
+                   "ApplyCompact", "ReadBack", "CommitEviction", "MemoryStats", "AssembleFeatures"):
+        assert f"eps::HipCacheBackend::{method}(" in names, method
 
 
 def test_host_only_queries(pkg):
