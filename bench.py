@@ -218,7 +218,8 @@ def main(argv=None):
         "step_frac_of_hbm_peak": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
         "phases_ms": {"gather": gather_ms, "prepare": prepare_ms, "push": push_ms,
                       "fused_update": fused_ms},
-        "roofline": {"kernel": "SortedUpdateKernel (fused aggregation + Adam)", "bound": "hbm",
+        "roofline": {"kernel": "fused aggregation + sparse Adam (eps_hip_push_apply: "
+                               "HotSliceKernel + RowRunKernel)", "bound": "hbm",
                      "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
                      "algorithmic_bytes_per_launch": mean["fused_bytes"]},
