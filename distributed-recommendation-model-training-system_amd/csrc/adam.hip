@@ -63,10 +63,7 @@ struct GuardArgs {
 constexpr uint32_t kMaxItems = 16;  // float4 per thread per block
 
 __global__ void __launch_bounds__(kBlock) GradMaxKernel(GuardArgs a) {
-  Span sp = a.span[0];
-#pragma unroll
-  for (uint32_t i = 1; i <= EPS_HIP_MAX_FEATURES; ++i)
-    if (i < a.spans && blockIdx.x >= a.span[i].block_begin) sp = a.span[i];
+  const Span sp = a.span[PartOf(a.span, a.spans)];
   const uint64_t per_block = uint64_t(kBlock) * kMaxItems * 4;
   const uint64_t begin = uint64_t(blockIdx.x - sp.block_begin) * per_block;
   const uint64_t end = min(begin + per_block, sp.count);
@@ -157,6 +154,14 @@ struct TableDesc {
 struct RowStats {
   uint32_t err = 0, bw = 0, bm = 0, bv = 0;
 };
+
+// Block-wide copy of a kernel-argument array to LDS, one 32-bit word per
+// thread per step (the arrays are read in place from the argument segment).
+__device__ __forceinline__ void CopyWords(void* dst, const void* src, uint32_t bytes) {
+  const uint32_t* from = static_cast<const uint32_t*>(src);
+  uint32_t* to = static_cast<uint32_t*>(dst);
+  for (uint32_t i = threadIdx.x; i < bytes / 4; i += kBlock) to[i] = from[i];
+}
 
 // One element: Adam in the reference's operation order; returns w (unclamped).
 __device__ __forceinline__ void AdamElement(const TableDesc& T, float g, float& w, float& m,
@@ -263,12 +268,8 @@ __global__ void __launch_bounds__(kBlock) SortedUpdateKernel(FusedArgs a) {
   __shared__ const float* s_grad[EPS_HIP_MAX_FEATURES];
   __shared__ uint32_t s_heads[kBlock];
   __shared__ uint32_t s_wave_heads[4];
-#pragma unroll
-  for (uint32_t i = 0; i < EPS_HIP_MAX_TABLES; ++i)
-    if (threadIdx.x == i) s_t[i] = a.t[i];
-#pragma unroll
-  for (uint32_t i = 0; i < EPS_HIP_MAX_FEATURES; ++i)
-    if (threadIdx.x == i) s_grad[i] = a.grad[i];
+  CopyWords(s_t, a.t, sizeof(a.t));
+  CopyWords(s_grad, a.grad, sizeof(a.grad));
   Control* ctrl = a.ctrl;
   const uint32_t mode = ctrl->mode;
   const uint32_t status = ctrl->status;
@@ -430,14 +431,6 @@ __device__ __forceinline__ const float* RefSource(const float* const* grad, uint
   const uint32_t ref = uint32_t(word);
   scale = __uint_as_float(uint32_t(word >> 32));
   return grad[ref >> kRefRowBits] + uint64_t(ref & ((1u << kRefRowBits) - 1)) * dim + col;
-}
-
-// Block-wide copy of a kernel-argument array to LDS, one 32-bit word per
-// thread per step (the arrays are read in place from the argument segment).
-__device__ __forceinline__ void CopyWords(void* dst, const void* src, uint32_t bytes) {
-  const uint32_t* from = static_cast<const uint32_t*>(src);
-  uint32_t* to = static_cast<uint32_t*>(dst);
-  for (uint32_t i = threadIdx.x; i < bytes / 4; i += kBlock) to[i] = from[i];
 }
 
 // Copies the per-launch tables to LDS and decides whether this launch writes;

@@ -101,6 +101,17 @@ __device__ __forceinline__ void StoreF(float* p, float v) { *(EPS_GLOBAL float*)
 __device__ __forceinline__ uint32_t AbsBits(float x) { return __float_as_uint(x) & 0x7fffffffu; }
 __device__ __forceinline__ bool Finite(float x) { return AbsBits(x) < 0x7f800000u; }
 
+// Part (feature, span) a block belongs to, for launches that cover several
+// parts ordered by their first block: the number of parts starting at or
+// before this block, minus one.  One vector load and a ballot instead of a
+// chain of dependent kernel-argument loads.
+template <typename Part>
+__device__ __forceinline__ uint32_t PartOf(const Part* parts, uint32_t count) {
+  const uint32_t lane = threadIdx.x & (kWave - 1);
+  const uint32_t begin = lane < count ? parts[lane].block_begin : 0xffffffffu;
+  return uint32_t(__popcll(__ballot(begin <= blockIdx.x))) - 1u;
+}
+
 // Maximum over the lanes of a wavefront (DPP/permute lowering by the compiler).
 __device__ __forceinline__ uint32_t WaveMax(uint32_t x) {
 #pragma unroll

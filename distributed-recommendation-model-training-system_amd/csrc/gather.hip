@@ -62,10 +62,7 @@ __device__ __forceinline__ uint64_t ResolveSlot(const GatherDesc& d, uint64_t i,
 }
 
 __global__ void __launch_bounds__(kBlock) GatherKernel(GatherArgs args) {
-  GatherDesc d = args.part[0];
-#pragma unroll
-  for (uint32_t i = 1; i < EPS_HIP_MAX_GATHER_PARTS; ++i)
-    if (i < args.count && blockIdx.x >= args.part[i].block_begin) d = args.part[i];
+  const GatherDesc d = args.part[PartOf(args.part, args.count)];
 
   __shared__ uint64_t s_off[129];
   __shared__ uint64_t s_slot[kIdCap];

@@ -52,23 +52,8 @@ struct PrepArgs {
   uint64_t* refscale;
 };
 
-__device__ __forceinline__ uint64_t BagOf(const uint64_t* offsets, uint64_t bags, uint64_t i) {
-  // Largest b with offsets[b] <= i (upper_bound - 1); empty bags are skipped.
-  uint64_t lo = 0, hi = bags;  // answer in [lo, hi)
-  while (hi - lo > 1) {
-    const uint64_t mid = (lo + hi) >> 1;
-    if (offsets[mid] <= i) lo = mid; else hi = mid;
-  }
-  return lo;
-}
-
 __global__ void __launch_bounds__(kBlock) KeygenKernel(PrepArgs args) {
-  PrepFeature f = args.f[0];
-  uint32_t fi = 0;
-#pragma unroll
-  for (uint32_t i = 1; i < EPS_HIP_MAX_FEATURES; ++i)
-    if (i < args.count && blockIdx.x >= args.f[i].block_begin) { f = args.f[i]; fi = i; }
-  (void)fi;
+  const PrepFeature f = args.f[PartOf(args.f, args.count)];
   __shared__ uint32_t s_hist[kMaxPasses][256];
   __shared__ uint32_t s_class[8];
   __shared__ uint32_t s_misc[2];  // [0] bad, [1] max scale
@@ -82,28 +67,55 @@ __global__ void __launch_bounds__(kBlock) KeygenKernel(PrepArgs args) {
   const uint64_t local0 = uint64_t(blockIdx.x - f.block_begin) * (kBlock * kKeygenItems);
   uint32_t valid = 0, scale_max = 0;
   bool bad = false;
+  // The thread's occurrences are independent: their slot loads and the bag
+  // searches over `offsets` proceed interleaved, so each search step has all
+  // of them in flight instead of one.
+  uint64_t li[kKeygenItems], slot[kKeygenItems], lo[kKeygenItems], hi[kKeygenItems];
+  bool in[kKeygenItems];
+#pragma unroll
   for (uint32_t k = 0; k < kKeygenItems; ++k) {
-    const uint64_t li = local0 + k * kBlock + threadIdx.x;
-    if (li >= f.occurrences) break;
-    const uint64_t gi = f.occ_begin + li;
-    uint64_t slot = f.indices[li];
-    if (slot != kHole && slot >= f.table_rows) { bad = true; slot = kHole; }
+    li[k] = local0 + k * kBlock + threadIdx.x;
+    in[k] = li[k] < f.occurrences;
+    slot[k] = in[k] ? f.indices[li[k]] : kHole;
+    lo[k] = 0;                             // bag of the occurrence: largest b with
+    hi[k] = in[k] ? f.bags : 1;            // offsets[b] <= li, b in [lo, hi)
+  }
+  if (f.pooling != EPS_HIP_POOL_SEQUENCE) {
+    for (;;) {
+      bool more = false;
+#pragma unroll
+      for (uint32_t k = 0; k < kKeygenItems; ++k) {
+        if (hi[k] - lo[k] > 1) {
+          const uint64_t mid = (lo[k] + hi[k]) >> 1;
+          if (f.offsets[mid] <= li[k]) lo[k] = mid; else hi[k] = mid;
+          more |= hi[k] - lo[k] > 1;
+        }
+      }
+      if (!more) break;
+    }
+  }
+#pragma unroll
+  for (uint32_t k = 0; k < kKeygenItems; ++k) {
+    if (!in[k]) continue;
+    const uint64_t gi = f.occ_begin + li[k];
+    uint64_t s = slot[k];
+    if (s != kHole && s >= f.table_rows) { bad = true; s = kHole; }
     uint32_t key = args.sentinel;
-    if (slot != kHole) { key = (f.key_index << args.row_bits) | uint32_t(slot); ++valid; }
+    if (s != kHole) { key = (f.key_index << args.row_bits) | uint32_t(s); ++valid; }
     uint64_t row;
     float scale = 1.0f;
     if (f.pooling == EPS_HIP_POOL_SEQUENCE) {
-      row = li;
+      row = li[k];
     } else {
-      row = BagOf(f.offsets, f.bags, li);
+      row = lo[k];
       if (f.pooling == EPS_HIP_POOL_MEAN) {
         const uint64_t len = f.lengths[row];
         if (len) scale = 1.0f / (float)len;  // batch_access.cpp:79-80
       } else if (f.pooling == EPS_HIP_POOL_WEIGHTED_SUM) {
-        scale = f.weights[li];
+        scale = f.weights[li[k]];
       }
     }
-    if (slot != kHole) scale_max = max(scale_max, AbsBits(scale));
+    if (s != kHole) scale_max = max(scale_max, AbsBits(scale));
     args.keys[gi] = key;
     args.vals[gi] = uint32_t(gi);
     args.refscale[gi] = (uint64_t(__float_as_uint(scale)) << 32) |
@@ -435,6 +447,8 @@ int PlanPush(const eps_hip_table* tables, uint32_t table_count,
     if (f.occurrences && !f.indices) return Fail(EPS_HIP_INVALID_ARGUMENT, "null feature indices");
     if (f.pooling != EPS_HIP_POOL_SEQUENCE && (!f.offsets || (f.pooling == EPS_HIP_POOL_MEAN && !f.valid_lengths)))
       return Fail(EPS_HIP_INVALID_ARGUMENT, "pooled feature needs offsets (and lengths for mean)");
+    if (f.pooling != EPS_HIP_POOL_SEQUENCE && f.occurrences && !f.bags)
+      return Fail(EPS_HIP_INVALID_ARGUMENT, "pooled feature with occurrences but no bags");
     if (f.pooling == EPS_HIP_POOL_WEIGHTED_SUM && f.occurrences && !f.weights)
       return Fail(EPS_HIP_INVALID_ARGUMENT, "weighted feature needs weights");
     const uint64_t rows = f.pooling == EPS_HIP_POOL_SEQUENCE ? f.occurrences : f.bags;
