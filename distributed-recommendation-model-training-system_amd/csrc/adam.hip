@@ -41,7 +41,7 @@ constexpr uint32_t kErrorBits = EPS_HIP_STATUS_BAD_INDEX | EPS_HIP_STATUS_NONFIN
 constexpr uint32_t kFallbackGrid = 2048;
 
 // ---------------------------------------------------------------------------
-// Gradient maximum and the guard decision (last block).
+// Gradient maximum (GradMaxKernel) and the guard decision (GuardDecideKernel).
 // A guarded input array: gradient values, reference scales, or 64-bit
 // indices that must all be below `limit` (checked before anything is written).
 enum SpanKind : uint32_t { kGradientSpan = 0, kScaleSpan = 1, kIndexSpan = 2 };
@@ -89,58 +89,66 @@ __global__ void __launch_bounds__(kBlock) GradMaxKernel(GuardArgs a) {
     for (uint64_t i = begin + threadIdx.x; i < end; i += kBlock) m = max(m, AbsBits(sp.p[i]));
   }
   __shared__ uint32_t s_max[4];
-  __shared__ bool s_last;
   if (out_of_range) atomicOr(&a.ctrl->prep_status, EPS_HIP_STATUS_BAD_INDEX);
   m = WaveMax(m);
   if ((threadIdx.x & (kWave - 1)) == 0) s_max[threadIdx.x / kWave] = m;
   __syncthreads();
-  Control* ctrl = a.ctrl;
   if (threadIdx.x == 0) {
     const uint32_t bm = max(max(s_max[0], s_max[1]), max(s_max[2], s_max[3]));
-    if (bm) atomicMax(sp.kind == kScaleSpan ? &ctrl->max_scale_bits : &ctrl->max_src_bits, bm);
-    __threadfence();
-    s_last = atomicAdd(&ctrl->done_counter, 1u) == gridDim.x - 1;
+    if (bm)
+      atomicMax(sp.kind == kScaleSpan ? &a.ctrl->max_scale_bits
+                                      : &a.ctrl->src_slots[blockIdx.x % kSrcSlots], bm);
   }
-  __syncthreads();
-  if (!s_last || threadIdx.x != 0) return;
-  __threadfence();
-  const uint32_t src_bits = __hip_atomic_load(&ctrl->max_src_bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  const uint32_t scale_bits = __hip_atomic_load(&ctrl->max_scale_bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The guard decision, one wavefront after GradMaxKernel on the same stream
+// (the kernel boundary orders the maxima before it; no cross-block fences).
+__global__ void __launch_bounds__(kWave) GuardDecideKernel(GuardArgs a) {
+  Control* ctrl = a.ctrl;
+  const uint32_t lane = threadIdx.x;
+  // Bounds domain and gradient-maximum slots: one slot per lane, then the
+  // wavefront maxima.  The gradient slots are cleared for the next push.
+  uint32_t wb = 0, mb = 0, vb = 0, gb = 0;
+  for (uint32_t s = lane; s < kBoundSlots; s += kWave) {
+    wb = max(wb, a.bounds->v[s][0]); mb = max(mb, a.bounds->v[s][1]); vb = max(vb, a.bounds->v[s][2]);
+  }
+  for (uint32_t s = lane; s < kSrcSlots; s += kWave) {
+    gb = max(gb, ctrl->src_slots[s]);
+    ctrl->src_slots[s] = 0;
+  }
+  wb = WaveMax(wb); mb = WaveMax(mb); vb = WaveMax(vb); gb = WaveMax(gb);
+  const uint32_t scale_bits = ctrl->max_scale_bits;
   uint32_t status = a.use_prep_status ? ctrl->prep_status : 0u;
   uint32_t mode = kFused;
   if (status & EPS_HIP_STATUS_BAD_INDEX) {
     mode = kReject;
-  } else if (src_bits >= 0x7f800000u) {
+  } else if (gb >= 0x7f800000u) {
     status |= EPS_HIP_STATUS_NONFINITE_GRAD;
     mode = kReject;
   } else {
-    uint32_t wb = 0, mb = 0, vb = 0;
-    for (uint32_t s = 0; s < kBoundSlots; ++s) {
-      wb = max(wb, a.bounds->v[s][0]); mb = max(mb, a.bounds->v[s][1]); vb = max(vb, a.bounds->v[s][2]);
-    }
     const double W = __uint_as_float(wb), M = __uint_as_float(mb), V = __uint_as_float(vb);
     const double refs = double(a.refs_host ? a.refs_host : ctrl->valid_count);
     const double scale = fmax(1.0, double(__uint_as_float(scale_bits)));
-    const double G = double(__uint_as_float(src_bits)) * scale * refs *
+    const double G = double(__uint_as_float(gb)) * scale * refs *
                      exp((refs + 2.0) * 0x1.0p-24) * 1.01;
-    bool safe = G < 1e30;
-    for (uint32_t t = 0; t < a.tables && safe; ++t) {
-      const GuardTable& T = a.t[t];
+    // One table per lane.
+    bool table_safe = true;
+    if (lane < a.tables) {
+      const GuardTable& T = a.t[lane];
       const double b1 = T.beta1, b2 = T.beta2;
       const double mbound = (b1 * M + (1.0 - b1) * G) * 1.01;
       const double vbound = (b2 * V + (1.0 - b2) * G * G) * 1.01;
       const double wbound = (W + double(T.lr) * mbound / double(T.eps)) * 1.01;
-      safe = mbound < 1e30 && vbound < 1e30 && wbound < 1e30 && double(T.eps) > 0.0;
+      table_safe = mbound < 1e30 && vbound < 1e30 && wbound < 1e30 && double(T.eps) > 0.0;
     }
+    const bool safe = G < 1e30 && __ballot(!table_safe) == 0;
     if (!safe) { mode = kChecked; status |= EPS_HIP_STATUS_CHECKED_PATH; }
   }
+  if (lane != 0) return;
   if (mode == kReject) status |= EPS_HIP_STATUS_REJECTED;
   ctrl->mode = mode;
   ctrl->status = status;
-  ctrl->max_src_bits = 0;
   if (a.reset_scale) ctrl->max_scale_bits = 0;
-  ctrl->done_counter = 0;
-  __threadfence();
 }
 
 // ---------------------------------------------------------------------------
@@ -407,6 +415,7 @@ constexpr uint32_t kChunkPad = kChunk + 4;
 constexpr uint32_t kStageLoads = kChunk / kWave;        // staging loads per lane per chunk
 constexpr uint32_t kRunPositions = 128;
 constexpr uint32_t kRefBatch = 8;                       // gradient rows in flight per group
+constexpr uint32_t kXcds = 8;                           // XCDs of an MI355X
 
 struct VecArgs {
   TableDesc t[EPS_HIP_MAX_TABLES];   // by key index
@@ -496,9 +505,15 @@ __global__ void __launch_bounds__(kBlock) HotSliceKernel(VecArgs a) {
   float (*buf)[kChunkPad] = s_buf[wave];
   RowStats st;
   __syncthreads();
-  const uint32_t units = ctrl->long_count * a.slices;
-  for (uint32_t u = blockIdx.x * (kBlock / kWave) + wave; u < units;
-       u += gridDim.x * (kBlock / kWave)) {
+  // Hot rows are cut into kXcds contiguous ranges of the (key-sorted) list,
+  // one per XCD, for the same L2 locality of gradient rows as the row runs.
+  const uint32_t hot_rows = ctrl->long_count;
+  const uint32_t xcd = blockIdx.x % kXcds, per_xcd = gridDim.x / kXcds;
+  const uint32_t hot_span = (hot_rows + kXcds - 1) / kXcds;
+  const uint32_t units_begin = min(xcd * hot_span, hot_rows) * a.slices;
+  const uint32_t units = min((xcd + 1) * hot_span, hot_rows) * a.slices;
+  for (uint32_t u = units_begin + (blockIdx.x / kXcds) * (kBlock / kWave) + wave; u < units;
+       u += per_xcd * (kBlock / kWave)) {
     const uint32_t start = a.hot[u / a.slices];
     const uint32_t col0 = (u % a.slices) * kSlice;
     const uint32_t key = a.keys[start];
@@ -634,9 +649,19 @@ __global__ void __launch_bounds__(kBlock) RowRunKernel(VecArgs a) {
   const uint32_t lig = threadIdx.x & (G - 1), gid = threadIdx.x >> kLog2G;
   const uint32_t c = lig * 4;
   RowStats st;
+  // The class's positions are cut into kXcds contiguous ranges, one per XCD
+  // (the grid is a multiple of kXcds and blocks reach the XCDs round robin):
+  // the gradient rows a range references then come from a few features and
+  // stay in that XCD's L2 for all their references.  Rows that straddle a cut
+  // belong to the range holding their first position.
+  const uint32_t xcd = blockIdx.x % kXcds, per_xcd = gridDim.x / kXcds;
+  const uint32_t span = ((end - begin + kXcds - 1) / kXcds + kRunPositions - 1) / kRunPositions *
+                        kRunPositions;
+  const uint32_t xbegin = min(begin + xcd * span, end), xend = min(xbegin + span, end);
   __syncthreads();
-  for (uint32_t p0 = begin + blockIdx.x * kRunPositions; p0 < end; p0 += gridDim.x * kRunPositions) {
-    const uint32_t p1 = min(p0 + kRunPositions, end);
+  for (uint32_t p0 = xbegin + (blockIdx.x / kXcds) * kRunPositions; p0 < xend;
+       p0 += per_xcd * kRunPositions) {
+    const uint32_t p1 = min(p0 + kRunPositions, xend);
     const uint32_t lim = min(p1 + kLongRefs, end);
     const uint32_t staged = lim - p0;
     __syncthreads();  // previous iteration's readers are done
@@ -834,6 +859,8 @@ int LaunchGuard(GuardArgs& g, uint64_t blocks, hipStream_t s) {
   }
   hipLaunchKernelGGL(GradMaxKernel, dim3(unsigned(blocks)), dim3(kBlock), 0, s, g);
   EPS_HIP_LAUNCHED("gradient guard");
+  hipLaunchKernelGGL(GuardDecideKernel, dim3(1), dim3(kWave), 0, s, g);
+  EPS_HIP_LAUNCHED("guard decision");
   return EPS_HIP_OK;
 }
 
@@ -920,15 +947,17 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
       // The checked apply runs only after a validate-only pass; its launches
       // usually exit at once, so they get small grids.
       const uint64_t cap = phase == kSecond ? kSecondGrid : kVectorGrid;
+      // Grids are multiples of kXcds (the kernels split their work by XCD).
+      auto xcd_grid = [](uint64_t b) { return (b + kXcds - 1) / kXcds * kXcds; };
       if (hot_units) {
-        const uint64_t blocks = std::min<uint64_t>((hot_units + 3) / 4, std::min(cap, kHotGrid));
+        const uint64_t blocks = xcd_grid(std::min<uint64_t>((hot_units + 3) / 4, std::min(cap, kHotGrid)));
         EPS_HIP_TRY(LaunchVectorUpdate(0, true, unsigned(blocks), va, s));
       }
       for (uint32_t cls = 0; cls + 1 < kClasses; ++cls) {
         if (!plan.class_occurrences[cls]) continue;
         va.cls = cls;
-        const uint64_t blocks = std::min<uint64_t>(
-            std::max<uint64_t>(1, (plan.class_occurrences[cls] + kRunPositions - 1) / kRunPositions), cap);
+        const uint64_t blocks = xcd_grid(std::min<uint64_t>(
+            std::max<uint64_t>(1, (plan.class_occurrences[cls] + kRunPositions - 1) / kRunPositions), cap));
         EPS_HIP_TRY(LaunchVectorUpdate(cls, false, unsigned(blocks), va, s));
       }
     }

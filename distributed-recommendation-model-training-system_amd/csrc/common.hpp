@@ -23,22 +23,24 @@ constexpr uint32_t kRefRowBits = 27;      // gradient row bits in a reference wo
 constexpr uint32_t kLongRefs = 128;       // rows with more references take the sliced path
 constexpr uint32_t kSlice = 4;            // columns per sliced-path work unit
 
-// Control block at offset 0 of a push or update workspace (256 bytes).
+constexpr uint32_t kSrcSlots = 64;        // spread of the gradient-maximum atomics
+
+// Control block at offset 0 of a push or update workspace (512 bytes).
 struct Control {
   uint32_t status;          // result of the last push/update (0 = applied)
   uint32_t prep_status;     // prepare-time findings (bad slots)
-  uint32_t max_src_bits;    // max |gradient| as float bits (self-resetting)
+  uint32_t src_slots[kSrcSlots];  // max |gradient| as float bits, per slot (self-resetting)
   uint32_t max_scale_bits;  // max |scale| of the prepared references
   uint32_t valid_count;     // prepared occurrences that are on this device
   uint32_t mode;            // guard decision of the last push
-  uint32_t done_counter;    // last-block detection (self-resetting)
+  uint32_t reserved;
   uint32_t unique_count;
   uint32_t tile_counter[kMaxPasses];
   uint32_t class_count[8];  // prepared occurrences per dimension class
   uint32_t long_count;      // entries of the hot-row list
-  uint32_t pad[43];
+  uint32_t pad[44];
 };
-static_assert(sizeof(Control) == 256, "control block is 256 bytes");
+static_assert(sizeof(Control) == 512, "control block is 512 bytes");
 
 enum Mode : uint32_t { kFused = 0, kChecked = 1, kReject = 2 };
 

@@ -31,6 +31,7 @@ namespace {
 constexpr uint32_t kFlagAggregate = 1u << 30;
 constexpr uint32_t kFlagInclusive = 2u << 30;
 constexpr uint32_t kValueMask = (1u << 30) - 1;
+constexpr uint32_t kLookWindow = 16;  // predecessor tiles read per look-back round
 
 struct PrepFeature {
   const uint64_t* indices;
@@ -67,32 +68,49 @@ __global__ void __launch_bounds__(kBlock) KeygenKernel(PrepArgs args) {
   const uint64_t local0 = uint64_t(blockIdx.x - f.block_begin) * (kBlock * kKeygenItems);
   uint32_t valid = 0, scale_max = 0;
   bool bad = false;
-  // The thread's occurrences are independent: their slot loads and the bag
-  // searches over `offsets` proceed interleaved, so each search step has all
-  // of them in flight instead of one.
-  uint64_t li[kKeygenItems], slot[kKeygenItems], lo[kKeygenItems], hi[kKeygenItems];
+  // The thread's occurrences are independent: their slot loads, bag searches
+  // and scale loads proceed interleaved, so each dependent step has all of
+  // them in flight instead of one.
+  uint64_t li[kKeygenItems], slot[kKeygenItems], lo[kKeygenItems];
   bool in[kKeygenItems];
 #pragma unroll
   for (uint32_t k = 0; k < kKeygenItems; ++k) {
     li[k] = local0 + k * kBlock + threadIdx.x;
     in[k] = li[k] < f.occurrences;
     slot[k] = in[k] ? f.indices[li[k]] : kHole;
-    lo[k] = 0;                             // bag of the occurrence: largest b with
-    hi[k] = in[k] ? f.bags : 1;            // offsets[b] <= li, b in [lo, hi)
+    lo[k] = 0;  // bag of the occurrence: largest b < bags with offsets[b] <= li
   }
   if (f.pooling != EPS_HIP_POOL_SEQUENCE) {
-    for (;;) {
-      bool more = false;
+    // Branch-free binary search with a trip count that is uniform over the
+    // block (every block of a feature sees the same bag count): each step
+    // issues all of the thread's offset loads before it waits on them.  The
+    // probe lo + half stays below lo + len <= bags, inside offsets[0, bags].
+    for (uint64_t len = f.bags; len > 1;) {
+      const uint64_t half = len >> 1;
+      uint64_t probe[kKeygenItems];
 #pragma unroll
-      for (uint32_t k = 0; k < kKeygenItems; ++k) {
-        if (hi[k] - lo[k] > 1) {
-          const uint64_t mid = (lo[k] + hi[k]) >> 1;
-          if (f.offsets[mid] <= li[k]) lo[k] = mid; else hi[k] = mid;
-          more |= hi[k] - lo[k] > 1;
-        }
-      }
-      if (!more) break;
+      for (uint32_t k = 0; k < kKeygenItems; ++k) probe[k] = f.offsets[lo[k] + half];
+#pragma unroll
+      for (uint32_t k = 0; k < kKeygenItems; ++k) lo[k] = probe[k] <= li[k] ? lo[k] + half : lo[k];
+      len -= half;
     }
+  }
+  // Per-occurrence scale, loaded for all items before any is used (the pooling
+  // mode is uniform over the block; indices are clamped into range).
+  float scale[kKeygenItems];
+#pragma unroll
+  for (uint32_t k = 0; k < kKeygenItems; ++k) scale[k] = 1.0f;
+  if (f.pooling == EPS_HIP_POOL_MEAN) {
+    uint64_t len[kKeygenItems];
+#pragma unroll
+    for (uint32_t k = 0; k < kKeygenItems; ++k) len[k] = f.lengths[lo[k]];
+#pragma unroll
+    for (uint32_t k = 0; k < kKeygenItems; ++k)
+      if (len[k]) scale[k] = 1.0f / (float)len[k];  // batch_access.cpp:79-80
+  } else if (f.pooling == EPS_HIP_POOL_WEIGHTED_SUM) {
+#pragma unroll
+    for (uint32_t k = 0; k < kKeygenItems; ++k)
+      scale[k] = f.weights[in[k] ? li[k] : f.occurrences - 1];
   }
 #pragma unroll
   for (uint32_t k = 0; k < kKeygenItems; ++k) {
@@ -102,23 +120,11 @@ __global__ void __launch_bounds__(kBlock) KeygenKernel(PrepArgs args) {
     if (s != kHole && s >= f.table_rows) { bad = true; s = kHole; }
     uint32_t key = args.sentinel;
     if (s != kHole) { key = (f.key_index << args.row_bits) | uint32_t(s); ++valid; }
-    uint64_t row;
-    float scale = 1.0f;
-    if (f.pooling == EPS_HIP_POOL_SEQUENCE) {
-      row = li[k];
-    } else {
-      row = lo[k];
-      if (f.pooling == EPS_HIP_POOL_MEAN) {
-        const uint64_t len = f.lengths[row];
-        if (len) scale = 1.0f / (float)len;  // batch_access.cpp:79-80
-      } else if (f.pooling == EPS_HIP_POOL_WEIGHTED_SUM) {
-        scale = f.weights[li[k]];
-      }
-    }
-    if (s != kHole) scale_max = max(scale_max, AbsBits(scale));
+    const uint64_t row = f.pooling == EPS_HIP_POOL_SEQUENCE ? li[k] : lo[k];
+    if (s != kHole) scale_max = max(scale_max, AbsBits(scale[k]));
     args.keys[gi] = key;
     args.vals[gi] = uint32_t(gi);
-    args.refscale[gi] = (uint64_t(__float_as_uint(scale)) << 32) |
+    args.refscale[gi] = (uint64_t(__float_as_uint(scale[k])) << 32) |
                         (uint64_t(f.feature) << kRefRowBits) | row;
     for (uint32_t p = 0; p < args.passes; ++p)
       atomicAdd(&s_hist[p][(key >> args.shift[p]) & ((1u << args.bits[p]) - 1)], 1u);
@@ -179,6 +185,7 @@ __global__ void __launch_bounds__(kBlock) RadixPassKernel(
   for (uint32_t i = t; i < 4 * 256; i += kBlock) (&s_wcount[0][0])[i] = 0;
   __syncthreads();
   const uint32_t tile = s_tile;
+  const uint32_t digit_count = hist[t];  // global count of digit t, loaded early
   const uint32_t mask = (1u << bits) - 1;
   const uint32_t base = tile * kSortTile + wave * (kSortTile / 4);
   uint32_t key[kSortItems], val[kSortItems], rank[kSortItems];
@@ -224,20 +231,43 @@ __global__ void __launch_bounds__(kBlock) RadixPassKernel(
     __hip_atomic_store(mine, kFlagInclusive | total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   } else {
     __hip_atomic_store(mine, kFlagAggregate | total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    int64_t j = int64_t(tile) - 1;
-    while (j >= 0) {
-      const uint32_t v = __hip_atomic_load(look + uint64_t(j) * 256 + d, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-      const uint32_t flag = v & ~kValueMask;
-      if (flag == 0) continue;  // predecessor tile has not published yet
-      exclusive += v & kValueMask;
-      if (flag == kFlagInclusive) break;
-      --j;
+    // Windowed look-back: each round reads the next kLookWindow predecessors
+    // at once and adds their counts, nearest first, up to the first inclusive
+    // prefix (done) or the first tile that has not published yet (read again
+    // from there).  Tile 0 always publishes an inclusive prefix, so the walk
+    // ends at or before it; reads before tile 0 are never issued.
+    int64_t j = int64_t(tile) - 1;  // nearest predecessor not yet added
+    for (;;) {
+      uint32_t v[kLookWindow];
+#pragma unroll
+      for (uint32_t w = 0; w < kLookWindow; ++w) {
+        const int64_t q = j - int64_t(w);
+        v[w] = q >= 0 ? __hip_atomic_load(look + uint64_t(q) * 256 + d, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT)
+                      : kFlagInclusive;
+      }
+      bool stop = false, done = false;
+      uint32_t taken = 0;
+#pragma unroll
+      for (uint32_t w = 0; w < kLookWindow; ++w) {
+        const uint32_t flag = v[w] & ~kValueMask;
+        if (!stop) {
+          if (flag == 0) {
+            stop = true;  // not published yet
+          } else {
+            exclusive += v[w] & kValueMask;
+            ++taken;
+            if (flag == kFlagInclusive) stop = done = true;
+          }
+        }
+      }
+      if (done) break;
+      j -= int64_t(taken);
     }
     __hip_atomic_store(mine, kFlagInclusive | (exclusive + total), __ATOMIC_RELAXED,
                        __HIP_MEMORY_SCOPE_AGENT);
   }
-  const uint32_t digit_base = BlockExclusiveScan(hist[d], s_scan);
+  const uint32_t digit_base = BlockExclusiveScan(digit_count, s_scan);
   const uint32_t tile_start = BlockExclusiveScan(total, s_scan);
   s_tile_start[d] = tile_start;
   s_global[d] = digit_base + exclusive;
@@ -253,14 +283,32 @@ __global__ void __launch_bounds__(kBlock) RadixPassKernel(
     }
   }
   __syncthreads();
+  // Scatter of the digit-sorted tile: all LDS reads, then (last pass) all
+  // reference-word gathers, then the stores, so no item waits on another's
+  // round trip.  Entries past the tile's end read stale LDS (in bounds) and
+  // are neither gathered nor stored.
   const uint32_t tile_n = min(kSortTile, n - tile * kSortTile);
-  for (uint32_t q = t; q < tile_n; q += kBlock) {
-    const uint32_t k = s_keys[q];
-    const uint32_t digit = (k >> shift) & mask;
-    const uint32_t dest = s_global[digit] + (q - s_tile_start[digit]);
-    keys_out[dest] = k;
-    vals_out[dest] = s_vals[q];
-    if (kLast) sorted_rs[dest] = refscale[s_vals[q]];
+  uint32_t dest[kSortItems];
+#pragma unroll
+  for (uint32_t i = 0; i < kSortItems; ++i) {
+    const uint32_t q = i * kBlock + t;
+    key[i] = s_keys[q];
+    val[i] = s_vals[q];
+    const uint32_t digit = (key[i] >> shift) & mask;
+    dest[i] = s_global[digit] + (q - s_tile_start[digit]);
+  }
+  uint64_t rs[kSortItems];
+  if (kLast) {
+#pragma unroll
+    for (uint32_t i = 0; i < kSortItems; ++i) rs[i] = refscale[i * kBlock + t < tile_n ? val[i] : 0u];
+  }
+#pragma unroll
+  for (uint32_t i = 0; i < kSortItems; ++i) {
+    if (i * kBlock + t < tile_n) {
+      keys_out[dest[i]] = key[i];
+      vals_out[dest[i]] = val[i];
+      if (kLast) sorted_rs[dest[i]] = rs[i];
+    }
   }
 }
 
