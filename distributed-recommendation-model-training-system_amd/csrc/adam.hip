@@ -96,7 +96,7 @@ __global__ void __launch_bounds__(kBlock) GradMaxKernel(GuardArgs a) {
   if (threadIdx.x == 0) {
     const uint32_t bm = max(max(s_max[0], s_max[1]), max(s_max[2], s_max[3]));
     if (bm)
-      atomicMax(sp.kind == kScaleSpan ? &a.ctrl->max_scale_bits
+      atomicMax(sp.kind == kScaleSpan ? &a.ctrl->scale_slots[blockIdx.x % kSrcSlots]
                                       : &a.ctrl->src_slots[blockIdx.x % kSrcSlots], bm);
   }
 }
@@ -108,16 +108,18 @@ __global__ void __launch_bounds__(kWave) GuardDecideKernel(GuardArgs a) {
   const uint32_t lane = threadIdx.x;
   // Bounds domain and gradient-maximum slots: one slot per lane, then the
   // wavefront maxima.  The gradient slots are cleared for the next push.
-  uint32_t wb = 0, mb = 0, vb = 0, gb = 0;
+  uint32_t wb = 0, mb = 0, vb = 0, gb = 0, scale_bits = 0;
   for (uint32_t s = lane; s < kBoundSlots; s += kWave) {
     wb = max(wb, a.bounds->v[s][0]); mb = max(mb, a.bounds->v[s][1]); vb = max(vb, a.bounds->v[s][2]);
   }
   for (uint32_t s = lane; s < kSrcSlots; s += kWave) {
     gb = max(gb, ctrl->src_slots[s]);
+    scale_bits = max(scale_bits, ctrl->scale_slots[s]);
     ctrl->src_slots[s] = 0;
+    if (a.reset_scale) ctrl->scale_slots[s] = 0;
   }
   wb = WaveMax(wb); mb = WaveMax(mb); vb = WaveMax(vb); gb = WaveMax(gb);
-  const uint32_t scale_bits = ctrl->max_scale_bits;
+  scale_bits = WaveMax(scale_bits);
   uint32_t status = a.use_prep_status ? ctrl->prep_status : 0u;
   uint32_t mode = kFused;
   if (status & EPS_HIP_STATUS_BAD_INDEX) {
@@ -148,7 +150,6 @@ __global__ void __launch_bounds__(kWave) GuardDecideKernel(GuardArgs a) {
   if (mode == kReject) status |= EPS_HIP_STATUS_REJECTED;
   ctrl->mode = mode;
   ctrl->status = status;
-  if (a.reset_scale) ctrl->max_scale_bits = 0;
 }
 
 // ---------------------------------------------------------------------------
@@ -295,9 +296,8 @@ __global__ void __launch_bounds__(kBlock) SortedUpdateKernel(FusedArgs a) {
     }
     write = true;
   }
-  uint32_t start = 0;
-  for (uint32_t c = 0; c < a.cls; ++c) start += ctrl->class_count[c];
-  const uint32_t end = start + ctrl->class_count[a.cls];
+  const uint32_t start = ctrl->class_start[a.cls];
+  const uint32_t end = ctrl->class_start[a.cls + 1];
   const uint32_t G = kGeneric ? kWave : (1u << a.log2g);
   const uint32_t lig = threadIdx.x & (G - 1);
   const uint32_t gid = threadIdx.x / G, ngroups = kBlock / G;
@@ -415,7 +415,6 @@ constexpr uint32_t kChunkPad = kChunk + 4;
 constexpr uint32_t kStageLoads = kChunk / kWave;        // staging loads per lane per chunk
 constexpr uint32_t kRunPositions = 128;
 constexpr uint32_t kRefBatch = 8;                       // gradient rows in flight per group
-constexpr uint32_t kXcds = 8;                           // XCDs of an MI355X
 
 struct VecArgs {
   TableDesc t[EPS_HIP_MAX_TABLES];   // by key index
@@ -425,7 +424,7 @@ struct VecArgs {
   const uint32_t* hot;
   Control* ctrl;
   Bounds* bounds;
-  uint32_t row_bits, cls, fallback, slices;
+  uint32_t row_bits, cls, fallback, slices, hot_capacity;
 };
 
 // Orders a wavefront's LDS writes before its later LDS reads (and the reverse).
@@ -505,16 +504,14 @@ __global__ void __launch_bounds__(kBlock) HotSliceKernel(VecArgs a) {
   float (*buf)[kChunkPad] = s_buf[wave];
   RowStats st;
   __syncthreads();
-  // Hot rows are cut into kXcds contiguous ranges of the (key-sorted) list,
-  // one per XCD, for the same L2 locality of gradient rows as the row runs.
-  const uint32_t hot_rows = ctrl->long_count;
+  // XCD x takes hot-row list x: the hot rows of the x-th eighth of the sorted
+  // positions, whose gradient rows the row runs of that XCD also read.
   const uint32_t xcd = blockIdx.x % kXcds, per_xcd = gridDim.x / kXcds;
-  const uint32_t hot_span = (hot_rows + kXcds - 1) / kXcds;
-  const uint32_t units_begin = min(xcd * hot_span, hot_rows) * a.slices;
-  const uint32_t units = min((xcd + 1) * hot_span, hot_rows) * a.slices;
-  for (uint32_t u = units_begin + (blockIdx.x / kXcds) * (kBlock / kWave) + wave; u < units;
+  const uint32_t* hot = a.hot + uint64_t(xcd) * a.hot_capacity;
+  const uint32_t units = ctrl->long_count[xcd] * a.slices;
+  for (uint32_t u = (blockIdx.x / kXcds) * (kBlock / kWave) + wave; u < units;
        u += per_xcd * (kBlock / kWave)) {
-    const uint32_t start = a.hot[u / a.slices];
+    const uint32_t start = hot[u / a.slices];
     const uint32_t col0 = (u % a.slices) * kSlice;
     const uint32_t key = a.keys[start];
     const TableDesc& T = s_t[key >> a.row_bits];
@@ -641,9 +638,7 @@ __global__ void __launch_bounds__(kBlock) RowRunKernel(VecArgs a) {
   bool write = false;
   if (!VecPrologue(a, s_t, s_grad, write)) return;
   Control* ctrl = a.ctrl;
-  uint32_t begin = 0;
-  for (uint32_t c = 0; c < a.cls; ++c) begin += ctrl->class_count[c];
-  const uint32_t end = begin + ctrl->class_count[a.cls];
+  const uint32_t begin = ctrl->class_start[a.cls], end = ctrl->class_start[a.cls + 1];
   const uint32_t row_mask = (1u << a.row_bits) - 1;
   const uint32_t lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   const uint32_t lig = threadIdx.x & (G - 1), gid = threadIdx.x >> kLog2G;
@@ -931,6 +926,7 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
     va.keys = a.keys;
     va.rs = a.rs;
     va.hot = reinterpret_cast<const uint32_t*>(ws + L.long_list);
+    va.hot_capacity = uint32_t(L.HotCapacity());
     va.ctrl = a.ctrl;
     va.bounds = bounds;
     va.row_bits = plan.row_bits;

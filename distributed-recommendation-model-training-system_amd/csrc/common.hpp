@@ -23,24 +23,29 @@ constexpr uint32_t kRefRowBits = 27;      // gradient row bits in a reference wo
 constexpr uint32_t kLongRefs = 128;       // rows with more references take the sliced path
 constexpr uint32_t kSlice = 4;            // columns per sliced-path work unit
 
-constexpr uint32_t kSrcSlots = 64;        // spread of the gradient-maximum atomics
+constexpr uint32_t kSrcSlots = 64;        // spread of the gradient/scale maximum atomics
+constexpr uint32_t kHistCopies = 16;      // spread of the keygen histogram atomics
+constexpr uint32_t kXcds = 8;             // XCDs of an MI355X (one hot-row list each)
 
-// Control block at offset 0 of a push or update workspace (512 bytes).
+// Control block at offset 0 of a push or update workspace (1 KiB).  Values
+// that many blocks update are kept in several copies (slots) written round
+// robin and combined by their reader: atomics that all blocks aim at one
+// address serialise in the memory-side atomic unit.
 struct Control {
   uint32_t status;          // result of the last push/update (0 = applied)
   uint32_t prep_status;     // prepare-time findings (bad slots)
-  uint32_t src_slots[kSrcSlots];  // max |gradient| as float bits, per slot (self-resetting)
-  uint32_t max_scale_bits;  // max |scale| of the prepared references
+  uint32_t src_slots[kSrcSlots];    // max |gradient| as float bits, per slot (self-resetting)
+  uint32_t scale_slots[kSrcSlots];  // max |scale| above 1.0 as float bits, per slot
   uint32_t valid_count;     // prepared occurrences that are on this device
   uint32_t mode;            // guard decision of the last push
   uint32_t reserved;
   uint32_t unique_count;
   uint32_t tile_counter[kMaxPasses];
-  uint32_t class_count[8];  // prepared occurrences per dimension class
-  uint32_t long_count;      // entries of the hot-row list
-  uint32_t pad[44];
+  uint32_t class_start[8];  // first sorted position of each dimension class (+ end)
+  uint32_t long_count[kXcds];  // entries of each hot-row list
+  uint32_t pad[102];
 };
-static_assert(sizeof(Control) == 512, "control block is 512 bytes");
+static_assert(sizeof(Control) == 1024, "control block is 1 KiB");
 
 enum Mode : uint32_t { kFused = 0, kChecked = 1, kReject = 2 };
 
@@ -52,12 +57,14 @@ struct PushLayout {
   uint64_t n, tiles;
   uint64_t hist, look, keys_a, keys_b, vals_a, vals_b, refscale, sorted_rs, flags, ranks,
       block_sums, long_list, total;
+  // Capacity of each of the kXcds hot-row lists (any one may hold them all).
+  uint64_t HotCapacity() const { return n / kLongRefs + 1; }
   explicit PushLayout(uint64_t occurrences) {
     n = occurrences;
     tiles = (n + kSortTile - 1) / kSortTile;
     auto align = [](uint64_t x) { return (x + 255) & ~uint64_t(255); };
     uint64_t at = sizeof(Control);
-    hist = at; at = align(at + kMaxPasses * 256 * 4);
+    hist = at; at = align(at + kHistCopies * kMaxPasses * 256 * 4);
     look = at; at = align(at + kMaxPasses * tiles * 256 * 4);
     keys_a = at; at = align(at + n * 4);
     keys_b = at; at = align(at + n * 4);
@@ -68,7 +75,7 @@ struct PushLayout {
     flags = at; at = align(at + n * 4);
     ranks = at; at = align(at + n * 4);
     block_sums = at; at = align(at + ((n + 1023) / 1024 + 1) * 4);
-    long_list = at; at = align(at + (n / kLongRefs + 1) * 4);
+    long_list = at; at = align(at + kXcds * HotCapacity() * 4);
     total = at;
   }
 };

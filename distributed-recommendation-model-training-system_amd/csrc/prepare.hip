@@ -45,7 +45,6 @@ struct PrepArgs {
   PrepFeature f[EPS_HIP_MAX_FEATURES];
   uint32_t count, row_bits, sentinel, passes;
   uint32_t shift[kMaxPasses], bits[kMaxPasses];
-  uint32_t class_start[kClasses + 1];
   Control* ctrl;
   uint32_t* hist;
   uint32_t* keys;
@@ -56,17 +55,13 @@ struct PrepArgs {
 __global__ void __launch_bounds__(kBlock) KeygenKernel(PrepArgs args) {
   const PrepFeature f = args.f[PartOf(args.f, args.count)];
   __shared__ uint32_t s_hist[kMaxPasses][256];
-  __shared__ uint32_t s_class[8];
   __shared__ uint32_t s_misc[2];  // [0] bad, [1] max scale
   for (uint32_t i = threadIdx.x; i < kMaxPasses * 256; i += kBlock) (&s_hist[0][0])[i] = 0;
-  if (threadIdx.x < 8) s_class[threadIdx.x] = 0;
   if (threadIdx.x < 2) s_misc[threadIdx.x] = 0;
   __syncthreads();
 
-  uint32_t cls = 0;
-  while (cls + 1 < kClasses && f.key_index >= args.class_start[cls + 1]) ++cls;
   const uint64_t local0 = uint64_t(blockIdx.x - f.block_begin) * (kBlock * kKeygenItems);
-  uint32_t valid = 0, scale_max = 0;
+  uint32_t scale_max = 0;
   bool bad = false;
   // The thread's occurrences are independent: their slot loads, bag searches
   // and scale loads proceed interleaved, so each dependent step has all of
@@ -119,7 +114,7 @@ __global__ void __launch_bounds__(kBlock) KeygenKernel(PrepArgs args) {
     uint64_t s = slot[k];
     if (s != kHole && s >= f.table_rows) { bad = true; s = kHole; }
     uint32_t key = args.sentinel;
-    if (s != kHole) { key = (f.key_index << args.row_bits) | uint32_t(s); ++valid; }
+    if (s != kHole) key = (f.key_index << args.row_bits) | uint32_t(s);
     const uint64_t row = f.pooling == EPS_HIP_POOL_SEQUENCE ? li[k] : lo[k];
     if (s != kHole) scale_max = max(scale_max, AbsBits(scale[k]));
     args.keys[gi] = key;
@@ -129,22 +124,22 @@ __global__ void __launch_bounds__(kBlock) KeygenKernel(PrepArgs args) {
     for (uint32_t p = 0; p < args.passes; ++p)
       atomicAdd(&s_hist[p][(key >> args.shift[p]) & ((1u << args.bits[p]) - 1)], 1u);
   }
-  if (valid) atomicAdd(&s_class[cls], valid);
   if (bad) s_misc[0] = 1;
+  // Only scales above 1.0 matter to the guard (it bounds with max(1, |scale|)),
+  // so sum and mean pooling never reach the atomics below.
   scale_max = WaveMax(scale_max);
-  if ((threadIdx.x & (kWave - 1)) == 0 && scale_max) atomicMax(&s_misc[1], scale_max);
+  if ((threadIdx.x & (kWave - 1)) == 0 && scale_max > 0x3f800000u) atomicMax(&s_misc[1], scale_max);
   __syncthreads();
+  // The block's histogram goes to one of kHistCopies copies (round robin);
+  // the radix passes add the copies up.
+  uint32_t* hist = args.hist + (blockIdx.x % kHistCopies) * (kMaxPasses * 256);
   for (uint32_t i = threadIdx.x; i < args.passes * 256; i += kBlock) {
     const uint32_t c = (&s_hist[0][0])[i];
-    if (c) atomicAdd(args.hist + i, c);
-  }
-  if (threadIdx.x < kClasses && s_class[threadIdx.x]) {
-    atomicAdd(&args.ctrl->class_count[threadIdx.x], s_class[threadIdx.x]);
-    atomicAdd(&args.ctrl->valid_count, s_class[threadIdx.x]);
+    if (c) atomicAdd(hist + i, c);
   }
   if (threadIdx.x == 0) {
     if (s_misc[0]) atomicOr(&args.ctrl->prep_status, EPS_HIP_STATUS_BAD_INDEX);
-    if (s_misc[1]) atomicMax(&args.ctrl->max_scale_bits, s_misc[1]);
+    if (s_misc[1]) atomicMax(&args.ctrl->scale_slots[blockIdx.x % kSrcSlots], s_misc[1]);
   }
 }
 
@@ -185,7 +180,9 @@ __global__ void __launch_bounds__(kBlock) RadixPassKernel(
   for (uint32_t i = t; i < 4 * 256; i += kBlock) (&s_wcount[0][0])[i] = 0;
   __syncthreads();
   const uint32_t tile = s_tile;
-  const uint32_t digit_count = hist[t];  // global count of digit t, loaded early
+  uint32_t digit_count = 0;  // global count of digit t (sum of the keygen copies), loaded early
+#pragma unroll
+  for (uint32_t c = 0; c < kHistCopies; ++c) digit_count += hist[c * (kMaxPasses * 256) + t];
   const uint32_t mask = (1u << bits) - 1;
   const uint32_t base = tile * kSortTile + wave * (kSortTile / 4);
   uint32_t key[kSortItems], val[kSortItems], rank[kSortItems];
@@ -387,18 +384,46 @@ struct HotArgs {
   const uint32_t* keys;
   uint32_t* hot;
   Control* ctrl;
-  uint32_t row_bits, vector_keys;  // key indices below vector_keys are vector classes
+  uint32_t n, row_bits, capacity, sentinel;
+  uint32_t class_key[kClasses + 1];  // first table key index of each class (+ table count)
 };
 
+// Dimension class of a sorted key; the sentinel (rows not on this device; it
+// is above every valid key, so it sorts last) is class kClasses.
+__device__ __forceinline__ uint32_t ClassOfKey(const HotArgs& a, uint32_t key) {
+  if (key == a.sentinel) return kClasses;
+  const uint32_t ki = key >> a.row_bits;
+  uint32_t c = 0;
+#pragma unroll
+  for (uint32_t k = 1; k <= kClasses; ++k) c += ki >= a.class_key[k];
+  return c;
+}
+
+// One thread per sorted position p (and one for p == n):
+//  * class boundaries: class_start[c] = first position whose class is >= c,
+//    written by the one position where the class steps over c (the keys are
+//    sorted and key indices are ordered by class); class_start[kClasses] is
+//    the number of valid occurrences;
+//  * hot rows: the first position of a vector-class row with more than
+//    kLongRefs references, appended to the list of the XCD that owns that
+//    eighth of the positions (the update kernels split their work the same way).
 __global__ void __launch_bounds__(kBlock) HotListKernel(HotArgs a) {
-  const uint32_t valid = a.ctrl->valid_count;
   const uint32_t p = blockIdx.x * kBlock + threadIdx.x;
-  if (p + kLongRefs >= valid) return;
-  const uint32_t key = a.keys[p];
-  if ((key >> a.row_bits) >= a.vector_keys) return;
-  if (p > 0 && a.keys[p - 1] == key) return;
-  if (a.keys[p + kLongRefs] != key) return;
-  a.hot[atomicAdd(&a.ctrl->long_count, 1u)] = p;
+  if (p > a.n) return;
+  const uint32_t key = p < a.n ? a.keys[p] : 0u;
+  const uint32_t cls = p < a.n ? ClassOfKey(a, key) : kClasses;
+  const uint32_t pkey = p > 0 ? a.keys[p - 1] : 0u;
+  const bool first = p == 0 || pkey != key;
+  // Classes prev..cls start at p.
+  const uint32_t prev = p == 0 ? 0u : ClassOfKey(a, pkey) + 1u;
+  for (uint32_t c = prev; c <= cls; ++c) {
+    a.ctrl->class_start[c] = p;
+    if (c == kClasses) a.ctrl->valid_count = p;
+  }
+  if (p >= a.n || cls + 1 >= kClasses || !first) return;
+  if (p + kLongRefs >= a.n || a.keys[p + kLongRefs] != key) return;
+  const uint32_t list = uint32_t(uint64_t(p) * kXcds / a.n);
+  a.hot[uint64_t(list) * a.capacity + atomicAdd(&a.ctrl->long_count[list], 1u)] = p;
 }
 
 struct UniqueArgs {
@@ -542,7 +567,6 @@ int eps_hip_prepare(const eps_hip_table* tables, uint32_t table_count,
   args.sentinel = plan.key_bits >= 32 ? 0xffffffffu : ((1u << plan.key_bits) - 1);
   args.passes = plan.passes;
   for (uint32_t p = 0; p < kMaxPasses; ++p) { args.shift[p] = plan.shift[p]; args.bits[p] = plan.bits[p]; }
-  for (uint32_t c = 0; c <= kClasses; ++c) args.class_start[c] = plan.class_start[c];
   args.ctrl = ctrl;
   args.hist = reinterpret_cast<uint32_t*>(ws + L.hist);
   args.keys = reinterpret_cast<uint32_t*>(ws + L.keys_a);
@@ -583,9 +607,13 @@ int eps_hip_prepare(const eps_hip_table* tables, uint32_t table_count,
   ha.keys = keys[plan.passes % 2];
   ha.hot = reinterpret_cast<uint32_t*>(ws + L.long_list);
   ha.ctrl = ctrl;
+  ha.n = n;
   ha.row_bits = plan.row_bits;
-  ha.vector_keys = plan.class_start[kClasses - 1];
-  hipLaunchKernelGGL(HotListKernel, dim3(unsigned((n + kBlock - 1) / kBlock)), dim3(kBlock), 0, s, ha);
+  ha.capacity = uint32_t(L.HotCapacity());
+  ha.sentinel = args.sentinel;
+  for (uint32_t c = 0; c <= kClasses; ++c) ha.class_key[c] = plan.class_start[c];
+  ha.class_key[kClasses] = table_count;
+  hipLaunchKernelGGL(HotListKernel, dim3(unsigned(n / kBlock + 1)), dim3(kBlock), 0, s, ha);
   EPS_HIP_LAUNCHED("hot rows");
   return EPS_HIP_OK;
 }

@@ -50,9 +50,9 @@ def test_host_only_queries(pkg):
     L = pkg.eps_hip.lib()
     assert L.eps_hip_abi_version() == 1
     assert L.eps_hip_bounds_bytes() == 64 * 16
-    assert L.eps_hip_update_workspace_bytes() == 512  # the control block
+    assert L.eps_hip_update_workspace_bytes() == 1024  # the control block
     small, big = L.eps_hip_push_workspace_bytes(1000), L.eps_hip_push_workspace_bytes(10**6)
-    assert 512 < small < big
+    assert 1024 < small < big
     # Validation errors are reported without touching a device.
     rc = L.eps_hip_prepare(None, 0, None, 0, None, 0, None)
     assert rc == pkg.eps_hip.INVALID_ARGUMENT
