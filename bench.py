@@ -5,7 +5,7 @@ Workload: 26 fp32 tables x 1,000,000 rows x dim 64, batch 4096 bags per table,
 bag length U{1..20}, ids Zipf(1.05); tables 0-12 sum pooling, 13-25 mean;
 per-bag gradients N(0, 1e-2); sparse Adam lr 1e-3, betas 0.9/0.999, eps 1e-8.
 One step = pooled pull of every table + device dedup of the lookup (radix sort,
-run concurrently with the pull on a second stream) + fused duplicate-id
+on a second stream, running ahead of the pull and push) + fused duplicate-id
 aggregation and Adam of every unique row.  Inputs (ids,
 offsets, lengths, gradients) are resident in HBM before the timed region;
 several pre-generated batches are cycled.
@@ -144,44 +144,49 @@ def main(argv=None):
     wl = W.Criteo26()
     batches = [wl.batch(i) for i in range(args.batches)]
     stats = [batch_stats(wl, b) for b in batches]
-    shard = H.DeviceShard(torch, wl.tables, max_occurrences=max(s["lookups"] for s in stats))
+    shard = H.DeviceShard(torch, wl.tables, max_occurrences=max(s["lookups"] for s in stats),
+                          workspaces=2)
     shard.init_rows()
     dev = [[H.DeviceFeature(torch, f) for f in b] for b in batches]
     outputs = [torch.empty((wl.batch_size, t.dim), dtype=torch.float32, device="cuda")
                for t in wl.tables]
     stream = torch.cuda.current_stream()
 
-    # The pull's gather (main stream) and the push's preparation (dedup sort and
-    # hot-row list, side stream) read disjoint inputs, so they run concurrently;
-    # the fork waits for the previous step's push (which reads the workspace
-    # the preparation rewrites) and the push waits for both.
+    # Pipeline: the push's preparation (dedup sort and hot-row list) only reads
+    # the batch's ids, so it runs on a side stream ahead of the main stream
+    # (pull, then push).  Two workspaces alternate: the preparation of batch k
+    # waits for the push of batch k-2 (the last reader of its workspace), and
+    # the push of batch k waits for its preparation.
     side = torch.cuda.Stream()
-    forks = [torch.cuda.Event() for _ in range(2)]
-    joins = [torch.cuda.Event() for _ in range(2)]
+    prepared = [torch.cuda.Event() for _ in range(2)]
+    pushed = [torch.cuda.Event() for _ in range(2)]
 
     def step(k, fused=None, phases=None):
         """One step; `fused` = two timing events around the fused update,
-        `phases` = six events for the per-phase breakdown."""
+        `phases` = seven events for the per-phase breakdown."""
         feats = dev[k % len(dev)]
-        fork, join = forks[k % 2], joins[k % 2]
+        slot = k % 2
+        side.wait_event(pushed[slot])
         if phases:
             phases[0].record(stream)
-        fork.record(stream)
-        side.wait_event(fork)
-        shard.prepare(feats, stream=side)
-        join.record(side)
+            phases[5].record(side)
+        shard.prepare(feats, stream=side, slot=slot)
+        prepared[slot].record(side)
+        if phases:
+            phases[6].record(side)
         shard.lookup(feats, outputs, stream=stream)
         if phases:
             phases[1].record(stream)
-            phases[5].record(side)
-        stream.wait_event(join)
+        stream.wait_event(prepared[slot])
         if phases:
             phases[2].record(stream)
-        shard.push(feats, stream=stream, events=fused or (tuple(phases[3:5]) if phases else None))
+        shard.push(feats, stream=stream, slot=slot,
+                   events=fused or (tuple(phases[3:5]) if phases else None))
+        pushed[slot].record(stream)
 
     for k in range(args.warmup):
         step(k)
-        status = shard.status()
+        status = shard.status(slot=k % 2)
         assert status & H.STATUS_ERRORS == 0, f"warm-up push status {status:#x}"
     torch.cuda.synchronize()
     # Timed steps carry only the two events around the fused update (its
@@ -194,11 +199,12 @@ def main(argv=None):
         step(args.warmup + k, fused=fused[k])
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    status = shard.status()
-    assert status & H.STATUS_ERRORS == 0, f"timed push status {status:#x}"
+    for slot in range(2):
+        status = shard.status(slot=slot)
+        assert status & H.STATUS_ERRORS == 0, f"timed push status {status:#x}"
     # Per-phase breakdown on further (untimed) steps.
     breakdown = min(args.steps, 10)
-    events = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(breakdown)]
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(7)] for _ in range(breakdown)]
     for k in range(breakdown):
         step(args.warmup + args.steps + k, phases=events[k])
     torch.cuda.synchronize()
@@ -207,7 +213,8 @@ def main(argv=None):
     used = [stats[(args.warmup + k) % len(stats)] for k in range(args.steps)]
     mean = {key: float(np.mean([u[key] for u in used])) for key in used[0]}
     gather_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in events]))
-    prepare_ms = float(np.mean([e[0].elapsed_time(e[5]) for e in events]))  # side stream
+    prepare_ms = float(np.mean([e[5].elapsed_time(e[6]) for e in events]))  # side stream
+    wait_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in events]))
     fused_ms = float(np.mean([a.elapsed_time(b) for a, b in fused]))
     push_ms = float(np.mean([e[2].elapsed_time(e[4]) for e in events]))
     step_bytes = mean["pull_bytes"] + mean["push_bytes"]
@@ -242,9 +249,11 @@ def main(argv=None):
         "step_algorithmic_bytes": step_bytes,
         "step_algorithmic_GBps": step_bytes / (ms * 1e-3) / 1e9,
         "step_frac_of_hbm_peak": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
-        "phases_ms": {"gather": gather_ms, "prepare": prepare_ms, "push": push_ms,
-                      "fused_update": fused_ms, "note": "gather/prepare/push from untimed "
-                      "steps after the timed ones; fused_update from the timed steps"},
+        "phases_ms": {"gather": gather_ms, "prepare": prepare_ms, "prepare_wait": wait_ms,
+                      "push": push_ms, "fused_update": fused_ms,
+                      "note": "gather/prepare/prepare_wait/push from untimed steps after the "
+                      "timed ones (prepare runs on a side stream, ahead of the pull and push); "
+                      "fused_update from the timed steps"},
         "roofline": {"kernel": "fused aggregation + sparse Adam (eps_hip_push_apply: "
                                "HotSliceKernel + RowRunKernel)", "bound": "hbm",
                      "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",

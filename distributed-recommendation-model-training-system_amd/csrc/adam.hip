@@ -29,6 +29,8 @@
 
 #include <cfloat>
 #include <cmath>
+#include <map>
+#include <mutex>
 
 namespace eps_hip {
 
@@ -694,7 +696,8 @@ __global__ void __launch_bounds__(kBlock) RowRunKernel(VecArgs a) {
       const bool active = c < dim;
       const uint32_t cl = active ? c : 0;  // inactive lanes read column 0 and drop it
       float* row = T.state + uint64_t(key & row_mask) * dim * 3;
-      const float4 w0 = Load4(row + cl), m0 = Load4(row + dim + cl), v0 = Load4(row + 2 * dim + cl);
+      const float4 w0 = Load4Stream(row + cl), m0 = Load4Stream(row + dim + cl),
+                   v0 = Load4Stream(row + 2 * dim + cl);
       float4 g = make_float4(0.f, 0.f, 0.f, 0.f);
       // Every slot of a batch loads (slots past the row repeat its last
       // reference, an in-bounds row of the same table); only real references
@@ -725,9 +728,9 @@ __global__ void __launch_bounds__(kBlock) RowRunKernel(VecArgs a) {
       AdamElement(T, g.z, w.z, m.z, v.z, st);
       AdamElement(T, g.w, w.w, m.w, v.w, st);
       if (write) {
-        Store4(row + c, w);
-        Store4(row + dim + c, m);
-        Store4(row + 2 * dim + c, v);
+        Store4Stream(row + c, w);
+        Store4Stream(row + dim + c, m);
+        Store4Stream(row + 2 * dim + c, v);
         Track(st, w.x, m.x, v.x); Track(st, w.y, m.y, v.y);
         Track(st, w.z, m.z, v.z); Track(st, w.w, m.w, v.w);
       }
@@ -893,6 +896,36 @@ int LaunchVectorUpdate(uint32_t cls, bool hot, unsigned grid, const VecArgs& a, 
   }
 }
 
+// A second stream on each device for the row runs of a push.  Hot rows and
+// the other rows are disjoint, and the hot-row kernel is bound by its serial
+// reference chains rather than by HBM, so the two run side by side: the row
+// runs are forked from the caller's stream after the guard and joined back
+// before the push's later work.  Streams and events are created once per device and kept until
+// the process ends; `mu` keeps one push's fork, launch and join together.
+struct SideLane {
+  hipStream_t stream = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+  std::mutex mu;
+};
+
+int GetSideLane(SideLane*& lane) {
+  static std::mutex table_mu;
+  static auto* lanes = new std::map<int, SideLane*>();
+  int device = 0;
+  EPS_HIP_TRY(Check(hipGetDevice(&device), "hipGetDevice"));
+  std::lock_guard<std::mutex> lock(table_mu);
+  SideLane*& l = (*lanes)[device];
+  if (!l) {
+    auto* created = new SideLane();
+    EPS_HIP_TRY(Check(hipStreamCreateWithFlags(&created->stream, hipStreamNonBlocking), "hipStreamCreate"));
+    EPS_HIP_TRY(Check(hipEventCreateWithFlags(&created->fork, hipEventDisableTiming), "hipEventCreate"));
+    EPS_HIP_TRY(Check(hipEventCreateWithFlags(&created->join, hipEventDisableTiming), "hipEventCreate"));
+    l = created;
+  }
+  lane = l;
+  return EPS_HIP_OK;
+}
+
 int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, uint32_t table_count,
               const eps_hip_push_feature* features, uint32_t feature_count, const PushPlan& plan,
               const PushLayout& L, uint8_t* ws, bool reduce, const uint64_t* occ2u, float* out,
@@ -945,6 +978,20 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
       const uint64_t cap = phase == kSecond ? kSecondGrid : kVectorGrid;
       // Grids are multiples of kXcds (the kernels split their work by XCD).
       auto xcd_grid = [](uint64_t b) { return (b + kXcds - 1) / kXcds * kXcds; };
+      // The primary pass runs the hot rows on `s` and forks the row runs onto
+      // the device's second stream, so the hot-row blocks (few, long-lived)
+      // are resident first and the row runs fill the rest of the chip.  The
+      // checked apply (whose launches usually exit at once) stays on `s`.
+      SideLane* lane = nullptr;
+      std::unique_lock<std::mutex> lane_lock;
+      hipStream_t rows_stream = s;
+      if (hot_units && phase == kPrimary) {
+        EPS_HIP_TRY(GetSideLane(lane));
+        lane_lock = std::unique_lock<std::mutex>(lane->mu);
+        EPS_HIP_TRY(Check(hipEventRecord(lane->fork, s), "hipEventRecord"));
+        EPS_HIP_TRY(Check(hipStreamWaitEvent(lane->stream, lane->fork, 0), "hipStreamWaitEvent"));
+        rows_stream = lane->stream;
+      }
       if (hot_units) {
         const uint64_t blocks = xcd_grid(std::min<uint64_t>((hot_units + 3) / 4, std::min(cap, kHotGrid)));
         EPS_HIP_TRY(LaunchVectorUpdate(0, true, unsigned(blocks), va, s));
@@ -954,7 +1001,11 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
         va.cls = cls;
         const uint64_t blocks = xcd_grid(std::min<uint64_t>(
             std::max<uint64_t>(1, (plan.class_occurrences[cls] + kRunPositions - 1) / kRunPositions), cap));
-        EPS_HIP_TRY(LaunchVectorUpdate(cls, false, unsigned(blocks), va, s));
+        EPS_HIP_TRY(LaunchVectorUpdate(cls, false, unsigned(blocks), va, rows_stream));
+      }
+      if (lane) {
+        EPS_HIP_TRY(Check(hipEventRecord(lane->join, lane->stream), "hipEventRecord"));
+        EPS_HIP_TRY(Check(hipStreamWaitEvent(s, lane->join, 0), "hipStreamWaitEvent"));
       }
     }
   }

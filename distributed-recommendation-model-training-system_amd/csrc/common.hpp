@@ -105,6 +105,17 @@ __device__ __forceinline__ void Store4(float* p, float4 v) {
   const EpsF4 x = {v.x, v.y, v.z, v.w};
   *(EPS_GLOBAL EpsF4*)(p) = x;
 }
+// Streaming forms for table state rows, which a push reads once and writes
+// once: the nontemporal hint lets L2 evict them first, so the reused lines
+// (gradient rows, sorted keys) stay resident while the state streams through.
+__device__ __forceinline__ float4 Load4Stream(const float* p) {
+  const EpsF4 v = __builtin_nontemporal_load((const EPS_GLOBAL EpsF4*)(p));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void Store4Stream(float* p, float4 v) {
+  const EpsF4 x = {v.x, v.y, v.z, v.w};
+  __builtin_nontemporal_store(x, (EPS_GLOBAL EpsF4*)(p));
+}
 __device__ __forceinline__ float LoadF(const float* p) { return *(const EPS_GLOBAL float*)(p); }
 __device__ __forceinline__ void StoreF(float* p, float v) { *(EPS_GLOBAL float*)(p) = v; }
 __device__ __forceinline__ uint32_t AbsBits(float x) { return __float_as_uint(x) & 0x7fffffffu; }

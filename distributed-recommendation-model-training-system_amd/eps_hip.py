@@ -177,7 +177,7 @@ class DeviceFeature:
 class DeviceShard:
     """Every row of each table resident in HBM as AoS [w|m|v] (slot == key)."""
 
-    def __init__(self, torch, specs, max_occurrences=0, device="cuda"):
+    def __init__(self, torch, specs, max_occurrences=0, device="cuda", workspaces=1):
         self.torch = torch
         self.specs = list(specs)
         self.device = device
@@ -189,17 +189,24 @@ class DeviceShard:
         self.bounds = torch.zeros(L.eps_hip_bounds_bytes() // 4, dtype=torch.int32, device=device)
         self.update_ws = torch.zeros(L.eps_hip_update_workspace_bytes() // 4, dtype=torch.int32,
                                      device=device)
-        self.ws = None
+        # Push workspaces: a caller that prepares the next batch while the
+        # current one is pushed alternates between two of them (`slot`).
+        self.wss = [None] * workspaces
         self.ws_bytes = 0
         self.reserve(max_occurrences)
         self.tables = (Table * len(self.specs))(*[
             Table(_ptr(st), s.rows, s.dim, s.id) for st, s in zip(self.state, self.specs)])
 
     # ---- workspace ----
+    @property
+    def ws(self):
+        return self.wss[0]
+
     def reserve(self, occurrences):
         need = lib().eps_hip_push_workspace_bytes(int(occurrences))
         if need > self.ws_bytes:
-            self.ws = self.torch.zeros((need + 3) // 4, dtype=self.torch.int32, device=self.device)
+            self.wss = [self.torch.zeros((need + 3) // 4, dtype=self.torch.int32, device=self.device)
+                        for _ in self.wss]
             self.ws_bytes = need
 
     # ---- state ----
@@ -269,19 +276,20 @@ class DeviceShard:
         arr = (PushFeature * len(feats))(*[f.push_struct() for f in feats])
         return arr
 
-    def prepare(self, feats, stream=None):
+    def prepare(self, feats, stream=None, slot=0):
         self.reserve(sum(f.occurrences for f in feats))
         arr = self._push_args(feats)
-        check(lib().eps_hip_prepare(self.tables, len(self.specs), arr, len(feats), _ptr(self.ws),
-                                    self.ws_bytes, _stream(self.torch, stream)))
+        check(lib().eps_hip_prepare(self.tables, len(self.specs), arr, len(feats),
+                                    _ptr(self.wss[slot]), self.ws_bytes, _stream(self.torch, stream)))
 
-    def push(self, feats, stream=None, advance=True, events=None):
+    def push(self, feats, stream=None, advance=True, events=None, slot=0):
         """Fused aggregation + Adam of a prepared push (asynchronous).  Powers are
         advanced optimistically; check status() after the stream drains.
-        `events` = (start, end) torch events recorded around the fused pass."""
+        `events` = (start, end) torch events recorded around the fused pass;
+        `slot` = the workspace the batch was prepared in."""
         arr = self._push_args(feats)
         opts = (Optimizer * len(self.specs))(*[self.optimizer(t) for t in range(len(self.specs))])
-        args = (self.tables, opts, len(self.specs), arr, len(feats), _ptr(self.ws), self.ws_bytes,
+        args = (self.tables, opts, len(self.specs), arr, len(feats), _ptr(self.wss[slot]), self.ws_bytes,
                 _ptr(self.bounds), _stream(self.torch, stream))
         L = lib()
         check(L.eps_hip_push_begin(*args))
@@ -294,9 +302,9 @@ class DeviceShard:
         if advance:
             self.advance_powers([f.table for f in feats])
 
-    def status(self, stream=None, workspace=None):
+    def status(self, stream=None, workspace=None, slot=0):
         out = C.c_uint32()
-        ws = self.ws if workspace is None else workspace
+        ws = self.wss[slot] if workspace is None else workspace
         check(lib().eps_hip_read_status(_ptr(ws), C.byref(out), _stream(self.torch, stream)))
         return out.value
 
