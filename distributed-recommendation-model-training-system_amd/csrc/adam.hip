@@ -399,13 +399,13 @@ __global__ void __launch_bounds__(kBlock) SortedUpdateKernel(FusedArgs a) {
 // Vector-class update (dim % 4 == 0, dim <= 256).  Two kernels:
 //
 //  * HotSliceKernel: rows with more than kLongRefs references (listed at
-//    prepare time).  Work unit = (hot row, 8-column slice), one wavefront.
-//    The wave stages products src*scale of kChunk references into its own LDS
-//    tile ([column][reference]); 8 lanes (one per column) then add them in
-//    reference order.  The next chunk's gradient loads and the chunk after
-//    that's reference words are in flight during the adds.  Adam is
-//    elementwise, so the slices of one row are independent and a hot row's
-//    serial chain is spread over dim/8 wavefronts.
+//    prepare time).  Work unit = (hot row, kSlice-column slice), one
+//    wavefront.  The wave stages products src*scale of kChunk references into
+//    its own LDS tile ([column][reference]); kSlice lanes (one per column)
+//    then add them in reference order.  The next chunk's gradient loads and
+//    the chunk after that's reference words are in flight during the adds.
+//    Adam is elementwise, so the slices of one row are independent and a hot
+//    row's serial chain is spread over dim/kSlice wavefronts.
 //  * RowRunKernel: every other row.  A block owns kRunPositions sorted
 //    positions; it stages their keys and reference words (plus kLongRefs
 //    positions of look-ahead) in LDS with coalesced loads, finds the segment
@@ -416,7 +416,7 @@ constexpr uint32_t kChunk = 512;
 constexpr uint32_t kChunkPad = kChunk + 4;
 constexpr uint32_t kStageLoads = kChunk / kWave;        // staging loads per lane per chunk
 constexpr uint32_t kRunPositions = 128;
-constexpr uint32_t kRefBatch = 8;                       // gradient rows in flight per group
+constexpr uint32_t kRefBatch = 4;                       // gradient rows in flight per group
 
 struct VecArgs {
   TableDesc t[EPS_HIP_MAX_TABLES];   // by key index
