@@ -29,8 +29,6 @@
 
 #include <cfloat>
 #include <cmath>
-#include <map>
-#include <mutex>
 
 namespace eps_hip {
 
@@ -412,7 +410,7 @@ __global__ void __launch_bounds__(kBlock) SortedUpdateKernel(FusedArgs a) {
 //    heads with a ballot, and a group of G = dim/4 lanes per row (lane = 4
 //    columns) loads the row's w, m, v together with its gradient rows, sums
 //    them in order and applies Adam.
-constexpr uint32_t kChunk = 512;
+constexpr uint32_t kChunk = kHotChunk;
 constexpr uint32_t kChunkPad = kChunk + 4;
 constexpr uint32_t kStageLoads = kChunk / kWave;        // staging loads per lane per chunk
 constexpr uint32_t kRunPositions = 128;
@@ -506,15 +504,33 @@ __global__ void __launch_bounds__(kBlock) HotSliceKernel(VecArgs a) {
   float (*buf)[kChunkPad] = s_buf[wave];
   RowStats st;
   __syncthreads();
-  // XCD x takes hot-row list x: the hot rows of the x-th eighth of the sorted
-  // positions, whose gradient rows the row runs of that XCD also read.
-  const uint32_t xcd = blockIdx.x % kXcds, per_xcd = gridDim.x / kXcds;
-  const uint32_t* hot = a.hot + uint64_t(xcd) * a.hot_capacity;
-  const uint32_t units = ctrl->long_count[xcd] * a.slices;
-  for (uint32_t u = (blockIdx.x / kXcds) * (kBlock / kWave) + wave; u < units;
-       u += per_xcd * (kBlock / kWave)) {
-    const uint32_t start = hot[u / a.slices];
-    const uint32_t col0 = (u % a.slices) * kSlice;
+  // XCD x takes its hot-row lists: the hot rows of the x-th eighth of the
+  // sorted positions, whose gradient rows the row runs of that XCD also read.
+  // Work units are (row, slice) in list order, longest rows first, dealt to
+  // the XCD's wavefronts in snake order (round r goes left to right when r is
+  // even, right to left when odd), so each wave gets at most one of the
+  // longest units and the per-wave totals stay close.
+  const uint32_t xcd = blockIdx.x % kXcds;
+  const uint32_t xcd_waves = gridDim.x / kXcds * (kBlock / kWave);
+  const uint32_t me = (blockIdx.x / kXcds) * (kBlock / kWave) + wave;
+  uint32_t bucket_end[kHotBuckets];
+  uint32_t units = 0;
+#pragma unroll
+  for (uint32_t b = 0; b < kHotBuckets; ++b) {
+    units += ctrl->long_count[xcd * kHotBuckets + b] * a.slices;
+    bucket_end[b] = units;
+  }
+  for (uint32_t round = 0;; ++round) {
+    // Unit indices grow with the round, so the first one past the end ends the loop.
+    const uint32_t u = round * xcd_waves + ((round & 1) ? xcd_waves - 1 - me : me);
+    if (u >= units) break;
+    uint32_t b = 0;
+#pragma unroll
+    for (uint32_t k = 0; k + 1 < kHotBuckets; ++k) b += u >= bucket_end[k];
+    const uint32_t local = u - (b ? bucket_end[b - 1] : 0u);
+    const uint32_t start =
+        a.hot[uint64_t(xcd * kHotBuckets + b) * a.hot_capacity + local / a.slices];
+    const uint32_t col0 = (local % a.slices) * kSlice;
     const uint32_t key = a.keys[start];
     const TableDesc& T = s_t[key >> a.row_bits];
     const uint32_t dim = T.dim;
@@ -896,36 +912,6 @@ int LaunchVectorUpdate(uint32_t cls, bool hot, unsigned grid, const VecArgs& a, 
   }
 }
 
-// A second stream on each device for the row runs of a push.  Hot rows and
-// the other rows are disjoint, and the hot-row kernel is bound by its serial
-// reference chains rather than by HBM, so the two run side by side: the row
-// runs are forked from the caller's stream after the guard and joined back
-// before the push's later work.  Streams and events are created once per device and kept until
-// the process ends; `mu` keeps one push's fork, launch and join together.
-struct SideLane {
-  hipStream_t stream = nullptr;
-  hipEvent_t fork = nullptr, join = nullptr;
-  std::mutex mu;
-};
-
-int GetSideLane(SideLane*& lane) {
-  static std::mutex table_mu;
-  static auto* lanes = new std::map<int, SideLane*>();
-  int device = 0;
-  EPS_HIP_TRY(Check(hipGetDevice(&device), "hipGetDevice"));
-  std::lock_guard<std::mutex> lock(table_mu);
-  SideLane*& l = (*lanes)[device];
-  if (!l) {
-    auto* created = new SideLane();
-    EPS_HIP_TRY(Check(hipStreamCreateWithFlags(&created->stream, hipStreamNonBlocking), "hipStreamCreate"));
-    EPS_HIP_TRY(Check(hipEventCreateWithFlags(&created->fork, hipEventDisableTiming), "hipEventCreate"));
-    EPS_HIP_TRY(Check(hipEventCreateWithFlags(&created->join, hipEventDisableTiming), "hipEventCreate"));
-    l = created;
-  }
-  lane = l;
-  return EPS_HIP_OK;
-}
-
 int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, uint32_t table_count,
               const eps_hip_push_feature* features, uint32_t feature_count, const PushPlan& plan,
               const PushLayout& L, uint8_t* ws, bool reduce, const uint64_t* occ2u, float* out,
@@ -978,20 +964,9 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
       const uint64_t cap = phase == kSecond ? kSecondGrid : kVectorGrid;
       // Grids are multiples of kXcds (the kernels split their work by XCD).
       auto xcd_grid = [](uint64_t b) { return (b + kXcds - 1) / kXcds * kXcds; };
-      // The primary pass runs the hot rows on `s` and forks the row runs onto
-      // the device's second stream, so the hot-row blocks (few, long-lived)
-      // are resident first and the row runs fill the rest of the chip.  The
-      // checked apply (whose launches usually exit at once) stays on `s`.
-      SideLane* lane = nullptr;
-      std::unique_lock<std::mutex> lane_lock;
-      hipStream_t rows_stream = s;
-      if (hot_units && phase == kPrimary) {
-        EPS_HIP_TRY(GetSideLane(lane));
-        lane_lock = std::unique_lock<std::mutex>(lane->mu);
-        EPS_HIP_TRY(Check(hipEventRecord(lane->fork, s), "hipEventRecord"));
-        EPS_HIP_TRY(Check(hipStreamWaitEvent(lane->stream, lane->fork, 0), "hipStreamWaitEvent"));
-        rows_stream = lane->stream;
-      }
+      // Hot rows first, then the row runs of each class, in stream order: the
+      // two run at full occupancy one after the other (side by side they
+      // compete for the same registers and bandwidth and finish later).
       if (hot_units) {
         const uint64_t blocks = xcd_grid(std::min<uint64_t>((hot_units + 3) / 4, std::min(cap, kHotGrid)));
         EPS_HIP_TRY(LaunchVectorUpdate(0, true, unsigned(blocks), va, s));
@@ -1001,11 +976,7 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
         va.cls = cls;
         const uint64_t blocks = xcd_grid(std::min<uint64_t>(
             std::max<uint64_t>(1, (plan.class_occurrences[cls] + kRunPositions - 1) / kRunPositions), cap));
-        EPS_HIP_TRY(LaunchVectorUpdate(cls, false, unsigned(blocks), va, rows_stream));
-      }
-      if (lane) {
-        EPS_HIP_TRY(Check(hipEventRecord(lane->join, lane->stream), "hipEventRecord"));
-        EPS_HIP_TRY(Check(hipStreamWaitEvent(s, lane->join, 0), "hipStreamWaitEvent"));
+        EPS_HIP_TRY(LaunchVectorUpdate(cls, false, unsigned(blocks), va, s));
       }
     }
   }

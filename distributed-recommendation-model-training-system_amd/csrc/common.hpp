@@ -25,7 +25,9 @@ constexpr uint32_t kSlice = 4;            // columns per sliced-path work unit
 
 constexpr uint32_t kSrcSlots = 64;        // spread of the gradient/scale maximum atomics
 constexpr uint32_t kHistCopies = 16;      // spread of the keygen histogram atomics
-constexpr uint32_t kXcds = 8;             // XCDs of an MI355X (one hot-row list each)
+constexpr uint32_t kXcds = 8;             // XCDs of an MI355X
+constexpr uint32_t kHotBuckets = 4;       // hot-row lists per XCD, by length (longest first)
+constexpr uint32_t kHotChunk = 512;       // references per chunk of the hot-row kernel
 
 // Control block at offset 0 of a push or update workspace (1 KiB).  Values
 // that many blocks update are kept in several copies (slots) written round
@@ -42,8 +44,8 @@ struct Control {
   uint32_t unique_count;
   uint32_t tile_counter[kMaxPasses];
   uint32_t class_start[8];  // first sorted position of each dimension class (+ end)
-  uint32_t long_count[kXcds];  // entries of each hot-row list
-  uint32_t pad[102];
+  uint32_t long_count[kXcds * kHotBuckets];  // entries of each hot-row list
+  uint32_t pad[78];
 };
 static_assert(sizeof(Control) == 1024, "control block is 1 KiB");
 
@@ -57,7 +59,7 @@ struct PushLayout {
   uint64_t n, tiles;
   uint64_t hist, look, keys_a, keys_b, vals_a, vals_b, refscale, sorted_rs, flags, ranks,
       block_sums, long_list, total;
-  // Capacity of each of the kXcds hot-row lists (any one may hold them all).
+  // Capacity of each hot-row list (any one may hold every hot row).
   uint64_t HotCapacity() const { return n / kLongRefs + 1; }
   explicit PushLayout(uint64_t occurrences) {
     n = occurrences;
@@ -75,7 +77,7 @@ struct PushLayout {
     flags = at; at = align(at + n * 4);
     ranks = at; at = align(at + n * 4);
     block_sums = at; at = align(at + ((n + 1023) / 1024 + 1) * 4);
-    long_list = at; at = align(at + kXcds * HotCapacity() * 4);
+    long_list = at; at = align(at + kXcds * kHotBuckets * HotCapacity() * 4);
     total = at;
   }
 };
