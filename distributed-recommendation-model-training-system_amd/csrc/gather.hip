@@ -30,6 +30,7 @@ int Check(hipError_t e, const char* what) {
 namespace {
 
 constexpr uint32_t kIdCap = 2048;     // occurrences staged in LDS per tile
+constexpr uint32_t kGatherBatch = 8;  // source rows in flight per lane group
 constexpr uint32_t kGenericLog2 = 0xff;
 
 struct GatherDesc {
@@ -48,6 +49,7 @@ struct GatherArgs {
   uint32_t count;
   uint32_t* status;
 };
+static_assert(sizeof(GatherArgs) <= 4096, "gather arguments fit the kernel-argument segment");
 
 // Slot of occurrence `i` (or kHole); range failures are reported and skipped.
 __device__ __forceinline__ uint64_t ResolveSlot(const GatherDesc& d, uint64_t i, bool& bad) {
@@ -105,36 +107,67 @@ __global__ void __launch_bounds__(kBlock) GatherKernel(GatherArgs args) {
       const uint64_t beg = seq ? row0 + r : s_off[r];
       const uint64_t end = none ? beg : (seq ? row0 + r + 1 : s_off[r + 1]);
       float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-      for (uint64_t pos = beg; pos < end; pos += 4) {
-        float4 v[4];
-        float a[4];
-        bool ok[4];
+      if (staged && d.source_rows) {
+        // Staged slots: every load of a batch is issued before any is added,
+        // with no branch around a load (a hole or a position past the bag
+        // reads row 0, column 0 and is dropped; row 0 exists).
+        const uint32_t cl = active ? c : 0;
+        for (uint64_t pos = beg; pos < end; pos += kGatherBatch) {
+          float4 v[kGatherBatch];
+          float a[kGatherBatch];
+          bool ok[kGatherBatch];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const uint64_t i = pos + u;
-          uint64_t slot = kHole;
-          a[u] = 1.f;
-          if (i < end) {
-            if (staged) {
-              slot = s_slot[i - occ_begin];
-              if (weighted) a[u] = s_weight[i - occ_begin];
+          for (uint32_t u = 0; u < kGatherBatch; ++u) {
+            const uint64_t i = pos + u;
+            const uint32_t at = uint32_t(min(i, end - 1) - occ_begin);
+            const uint64_t slot = s_slot[at];
+            ok[u] = i < end && slot != kHole;
+            a[u] = weighted ? s_weight[at] : 1.f;
+            v[u] = Load4(d.source + (ok[u] ? slot : 0) * d.stride + cl);
+          }
+#pragma unroll
+          for (uint32_t u = 0; u < kGatherBatch; ++u) {
+            if (!ok[u]) continue;
+            if (weighted) {
+              acc.x += v[u].x * a[u]; acc.y += v[u].y * a[u];
+              acc.z += v[u].z * a[u]; acc.w += v[u].w * a[u];
             } else {
-              slot = ResolveSlot(d, i, bad);
-              if (weighted) a[u] = d.weights[i];
+              acc.x += v[u].x; acc.y += v[u].y; acc.z += v[u].z; acc.w += v[u].w;
             }
           }
-          ok[u] = slot != kHole;
-          v[u] = (ok[u] && active) ? Load4(d.source + slot * d.stride + c)
-                                   : make_float4(0.f, 0.f, 0.f, 0.f);
         }
+      } else {
+        for (uint64_t pos = beg; pos < end; pos += 4) {
+          float4 v[4];
+          float a[4];
+          bool ok[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          if (!ok[u]) continue;
-          if (weighted) {
-            acc.x += v[u].x * a[u]; acc.y += v[u].y * a[u];
-            acc.z += v[u].z * a[u]; acc.w += v[u].w * a[u];
-          } else {
-            acc.x += v[u].x; acc.y += v[u].y; acc.z += v[u].z; acc.w += v[u].w;
+          for (int u = 0; u < 4; ++u) {
+            const uint64_t i = pos + u;
+            uint64_t slot = kHole;
+            a[u] = 1.f;
+            if (i < end) {
+              if (staged) {
+                slot = s_slot[i - occ_begin];
+                if (weighted) a[u] = s_weight[i - occ_begin];
+              } else {
+                slot = ResolveSlot(d, i, bad);
+                if (weighted) a[u] = d.weights[i];
+              }
+            }
+            ok[u] = slot != kHole;
+            v[u] = (ok[u] && active) ? Load4(d.source + slot * d.stride + c)
+                                     : make_float4(0.f, 0.f, 0.f, 0.f);
+          }
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            if (!ok[u]) continue;
+            if (weighted) {
+              acc.x += v[u].x * a[u]; acc.y += v[u].y * a[u];
+              acc.z += v[u].z * a[u]; acc.w += v[u].w * a[u];
+            } else {
+              acc.x += v[u].x; acc.y += v[u].y; acc.z += v[u].z; acc.w += v[u].w;
+            }
           }
         }
       }
@@ -447,7 +480,7 @@ int eps_hip_gather(const eps_hip_gather_part* parts, uint32_t count, uint32_t* s
       uint32_t log2g = 2;
       while ((1u << log2g) < in.dim / 4) ++log2g;
       d.log2g = log2g;
-      d.rows_per_block = 2 * (kBlock >> log2g);
+      d.rows_per_block = kBlock >> log2g;  // one bag per lane group
     } else {
       d.log2g = kGenericLog2;
       d.rows_per_block = 8;

@@ -32,7 +32,7 @@ STATUS_CHECKED_PATH = 0x100
 STATUS_ERRORS = 0xF
 MAX_FEATURES = 32
 MAX_TABLES = 32
-MAX_GATHER_PARTS = 16
+MAX_GATHER_PARTS = 32
 HOLE = -1  # UINT64_MAX as int64
 
 

@@ -58,7 +58,7 @@ extern "C" {
 /* Per-launch limits (descriptors travel as kernel arguments). */
 #define EPS_HIP_MAX_FEATURES 32
 #define EPS_HIP_MAX_TABLES 32
-#define EPS_HIP_MAX_GATHER_PARTS 16
+#define EPS_HIP_MAX_GATHER_PARTS 32
 
 typedef struct eps_hip_table {
   float* state;       /* rows * 3 * dim floats */

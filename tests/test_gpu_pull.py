@@ -57,15 +57,15 @@ def test_gather_matches_oracle(torch_gpu, pkg, dim, pooling):
 
 
 def test_gather_many_parts_one_call(torch_gpu, pkg):
-    """Up to 16 features of different tables/dims in one launch, 20 -> two calls."""
+    """Up to 32 features of different tables/dims in one launch, 40 -> two calls."""
     torch, W, H = torch_gpu, pkg.workloads, pkg.eps_hip
     rng = np.random.default_rng(1)
     dims = [4, 8, 16, 64, 96, 128, 256, 6, 300, 32]
     specs = [W.TableSpec(i, d, 2000 + 100 * i, seed=10 + i) for i, d in enumerate(dims)]
     feats = []
-    for i in range(20):
+    for i in range(40):
         t = i % len(specs)
-        f = random_feature(W, rng, specs[t], [0, 1, 2, 3][i % 4], bags=50 + 7 * i)
+        f = random_feature(W, rng, specs[t], [0, 1, 2, 3][i % 4], bags=50 + 7 * (i % 20))
         f.table = t
         feats.append(f)
     shard = H.DeviceShard(torch, specs)
