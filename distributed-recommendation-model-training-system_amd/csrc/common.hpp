@@ -17,6 +17,10 @@ constexpr uint32_t kBoundSlots = 64;      // spread of the bound atomics
 constexpr uint32_t kSortTile = 4096;      // keys per radix-sort tile (256 x 16)
 constexpr uint32_t kSortItems = 16;
 constexpr uint32_t kMaxPasses = 4;
+constexpr uint32_t kRadixBits = 9;        // largest radix digit
+constexpr uint32_t kDigits = 1u << kRadixBits;
+constexpr uint32_t kDigitsPerThread = kDigits / kBlock;  // the sort kernels assume two
+static_assert(kDigitsPerThread == 2, "radix digits per thread");
 constexpr uint32_t kKeygenItems = 4;      // occurrences per keygen thread
 constexpr uint32_t kClasses = 6;          // 5 vector widths + generic
 constexpr uint32_t kRefRowBits = 27;      // gradient row bits in a reference word
@@ -66,8 +70,8 @@ struct PushLayout {
     tiles = (n + kSortTile - 1) / kSortTile;
     auto align = [](uint64_t x) { return (x + 255) & ~uint64_t(255); };
     uint64_t at = sizeof(Control);
-    hist = at; at = align(at + kHistCopies * kMaxPasses * 256 * 4);
-    look = at; at = align(at + kMaxPasses * tiles * 256 * 4);
+    hist = at; at = align(at + kHistCopies * kMaxPasses * kDigits * 4);
+    look = at; at = align(at + kMaxPasses * tiles * kDigits * 4);
     keys_a = at; at = align(at + n * 4);
     keys_b = at; at = align(at + n * 4);
     vals_a = at; at = align(at + n * 4);

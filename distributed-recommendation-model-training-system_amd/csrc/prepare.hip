@@ -32,6 +32,7 @@ constexpr uint32_t kFlagAggregate = 1u << 30;
 constexpr uint32_t kFlagInclusive = 2u << 30;
 constexpr uint32_t kValueMask = (1u << 30) - 1;
 constexpr uint32_t kLookWindow = 16;  // predecessor tiles read per look-back round
+constexpr uint32_t kStageBags = 2048;   // bag offsets a keygen block stages in LDS
 
 struct PrepFeature {
   const uint64_t* indices;
@@ -54,11 +55,12 @@ struct PrepArgs {
 
 __global__ void __launch_bounds__(kBlock) KeygenKernel(PrepArgs args) {
   const PrepFeature f = args.f[PartOf(args.f, args.count)];
-  __shared__ uint32_t s_hist[kMaxPasses][256];
+  __shared__ uint32_t s_hist[kMaxPasses][kDigits];
   __shared__ uint32_t s_misc[2];  // [0] bad, [1] max scale
-  for (uint32_t i = threadIdx.x; i < kMaxPasses * 256; i += kBlock) (&s_hist[0][0])[i] = 0;
+  __shared__ uint64_t s_off[kStageBags];  // offsets[b0 .. b0 + staged)
+  __shared__ uint64_t s_b0;
+  for (uint32_t i = threadIdx.x; i < kMaxPasses * kDigits; i += kBlock) (&s_hist[0][0])[i] = 0;
   if (threadIdx.x < 2) s_misc[threadIdx.x] = 0;
-  __syncthreads();
 
   const uint64_t local0 = uint64_t(blockIdx.x - f.block_begin) * (kBlock * kKeygenItems);
   uint32_t scale_max = 0;
@@ -76,19 +78,64 @@ __global__ void __launch_bounds__(kBlock) KeygenKernel(PrepArgs args) {
     lo[k] = 0;  // bag of the occurrence: largest b < bags with offsets[b] <= li
   }
   if (f.pooling != EPS_HIP_POOL_SEQUENCE) {
-    // Branch-free binary search with a trip count that is uniform over the
-    // block (every block of a feature sees the same bag count): each step
-    // issues all of the thread's offset loads before it waits on them.  The
-    // probe lo + half stays below lo + len <= bags, inside offsets[0, bags].
-    for (uint64_t len = f.bags; len > 1;) {
-      const uint64_t half = len >> 1;
-      uint64_t probe[kKeygenItems];
-#pragma unroll
-      for (uint32_t k = 0; k < kKeygenItems; ++k) probe[k] = f.offsets[lo[k] + half];
-#pragma unroll
-      for (uint32_t k = 0; k < kKeygenItems; ++k) lo[k] = probe[k] <= li[k] ? lo[k] + half : lo[k];
-      len -= half;
+    // Bag of each occurrence: the largest b < bags with offsets[b] <= li.
+    // The block's occurrences are consecutive, so wavefront 0 first finds the
+    // bag b0 of the block's first occurrence with a 64-way search (each round
+    // probes 64 evenly spaced offsets at once and keeps the segment the ballot
+    // points at: two rounds for 4096 bags), the block then stages
+    // offsets[b0 ..] in LDS, and each occurrence is searched there.
+    const uint64_t first = local0, last = min(local0 + kBlock * kKeygenItems, f.occurrences) - 1;
+    if (threadIdx.x < kWave) {
+      const uint32_t lane = threadIdx.x;
+      uint64_t base = 0, len = f.bags;  // answer in [base, base + len); offsets[base] <= first or base == 0
+      while (len > 1) {
+        const uint64_t step = (len + kWave - 1) / kWave;
+        const uint64_t q = uint64_t(lane) * step;
+        const bool probe = q < len && f.offsets[base + q] <= first;
+        const uint32_t count = uint32_t(__popcll(__ballot(probe)));
+        const uint64_t keep = count ? count - 1 : 0;
+        base += keep * step;
+        len = min(step, len - keep * step);
+      }
+      if (lane == 0) s_b0 = base;
     }
+    __syncthreads();
+    const uint64_t b0 = s_b0;
+    const uint32_t staged = uint32_t(min<uint64_t>(kStageBags, f.bags + 1 - b0));
+    for (uint32_t i = threadIdx.x; i < staged; i += kBlock) s_off[i] = f.offsets[b0 + i];
+    __syncthreads();
+    // Covered when the staged offsets reach past the block's last occurrence
+    // (or reach offsets[bags], which is past every occurrence); else (runs of
+    // empty bags longer than the stage) fall back to searching global memory.
+    if (b0 + staged == f.bags + 1 || s_off[staged - 1] > last) {
+      uint32_t r[kKeygenItems];
+#pragma unroll
+      for (uint32_t k = 0; k < kKeygenItems; ++k) r[k] = 0;
+      // Answer in [0, staged - 1): offsets[b0 + staged - 1] > last unless it is offsets[bags].
+      for (uint32_t len = staged - 1; len > 1;) {
+        const uint32_t half = len >> 1;
+#pragma unroll
+        for (uint32_t k = 0; k < kKeygenItems; ++k) r[k] = s_off[r[k] + half] <= li[k] ? r[k] + half : r[k];
+        len -= half;
+      }
+#pragma unroll
+      for (uint32_t k = 0; k < kKeygenItems; ++k) lo[k] = b0 + r[k];
+    } else {
+      // Branch-free binary search with a trip count that is uniform over the
+      // block: each step issues all of the thread's offset loads before it
+      // waits on them.  The probe lo + half stays below lo + len <= bags.
+      for (uint64_t len = f.bags; len > 1;) {
+        const uint64_t half = len >> 1;
+        uint64_t probe[kKeygenItems];
+#pragma unroll
+        for (uint32_t k = 0; k < kKeygenItems; ++k) probe[k] = f.offsets[lo[k] + half];
+#pragma unroll
+        for (uint32_t k = 0; k < kKeygenItems; ++k) lo[k] = probe[k] <= li[k] ? lo[k] + half : lo[k];
+        len -= half;
+      }
+    }
+  } else {
+    __syncthreads();
   }
   // Per-occurrence scale, loaded for all items before any is used (the pooling
   // mode is uniform over the block; indices are clamped into range).
@@ -132,8 +179,8 @@ __global__ void __launch_bounds__(kBlock) KeygenKernel(PrepArgs args) {
   __syncthreads();
   // The block's histogram goes to one of kHistCopies copies (round robin);
   // the radix passes add the copies up.
-  uint32_t* hist = args.hist + (blockIdx.x % kHistCopies) * (kMaxPasses * 256);
-  for (uint32_t i = threadIdx.x; i < args.passes * 256; i += kBlock) {
+  uint32_t* hist = args.hist + (blockIdx.x % kHistCopies) * (kMaxPasses * kDigits);
+  for (uint32_t i = threadIdx.x; i < args.passes * kDigits; i += kBlock) {
     const uint32_t c = (&s_hist[0][0])[i];
     if (c) atomicAdd(hist + i, c);
   }
@@ -168,21 +215,26 @@ __global__ void __launch_bounds__(kBlock) RadixPassKernel(
     uint32_t shift, uint32_t bits, const uint32_t* __restrict__ hist, uint32_t* look,
     uint32_t* tile_counter) {
   __shared__ uint32_t s_tile;
-  __shared__ uint32_t s_wcount[4][256];
-  __shared__ uint32_t s_tile_start[256];
-  __shared__ uint32_t s_global[256];
+  __shared__ uint32_t s_wcount[4][kDigits];
+  __shared__ uint32_t s_tile_start[kDigits];
+  __shared__ uint32_t s_global[kDigits];
   __shared__ uint32_t s_scan[4];
   __shared__ uint32_t s_keys[kSortTile];
   __shared__ uint32_t s_vals[kSortTile];
 
   const uint32_t t = threadIdx.x, lane = t & (kWave - 1), wave = t / kWave;
   if (t == 0) s_tile = atomicAdd(tile_counter, 1u);
-  for (uint32_t i = t; i < 4 * 256; i += kBlock) (&s_wcount[0][0])[i] = 0;
+  for (uint32_t i = t; i < 4 * kDigits; i += kBlock) (&s_wcount[0][0])[i] = 0;
   __syncthreads();
   const uint32_t tile = s_tile;
-  uint32_t digit_count = 0;  // global count of digit t (sum of the keygen copies), loaded early
+  // This thread's digits are 2t and 2t+1; their global counts (the sum of
+  // the keygen copies) are loaded early.
+  uint32_t digit_count[kDigitsPerThread] = {0, 0};
 #pragma unroll
-  for (uint32_t c = 0; c < kHistCopies; ++c) digit_count += hist[c * (kMaxPasses * 256) + t];
+  for (uint32_t c = 0; c < kHistCopies; ++c)
+#pragma unroll
+    for (uint32_t j = 0; j < kDigitsPerThread; ++j)
+      digit_count[j] += hist[c * (kMaxPasses * kDigits) + kDigitsPerThread * t + j];
   const uint32_t mask = (1u << bits) - 1;
   const uint32_t base = tile * kSortTile + wave * (kSortTile / 4);
   uint32_t key[kSortItems], val[kSortItems], rank[kSortItems];
@@ -213,61 +265,84 @@ __global__ void __launch_bounds__(kBlock) RadixPassKernel(
     }
   }
   __syncthreads();
-  // Per digit (one per thread): wave prefixes, tile total, look-back.
-  const uint32_t d = t;
-  uint32_t total = 0;
+  // Per digit (two per thread): wave prefixes, tile total, look-back.
+  uint32_t total[kDigitsPerThread], exclusive[kDigitsPerThread];
 #pragma unroll
-  for (uint32_t w = 0; w < 4; ++w) {
-    const uint32_t c = s_wcount[w][d];
-    s_wcount[w][d] = total;
-    total += c;
+  for (uint32_t j = 0; j < kDigitsPerThread; ++j) {
+    const uint32_t d = kDigitsPerThread * t + j;
+    total[j] = 0;
+    exclusive[j] = 0;
+#pragma unroll
+    for (uint32_t w = 0; w < 4; ++w) {
+      const uint32_t c = s_wcount[w][d];
+      s_wcount[w][d] = total[j];
+      total[j] += c;
+    }
   }
-  uint32_t* mine = look + uint64_t(tile) * 256 + d;
-  uint32_t exclusive = 0;
+  uint32_t* mine = look + uint64_t(tile) * kDigits + kDigitsPerThread * t;
   if (tile == 0) {
-    __hip_atomic_store(mine, kFlagInclusive | total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (uint32_t j = 0; j < kDigitsPerThread; ++j)
+      __hip_atomic_store(mine + j, kFlagInclusive | total[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   } else {
-    __hip_atomic_store(mine, kFlagAggregate | total, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // Windowed look-back: each round reads the next kLookWindow predecessors
-    // at once and adds their counts, nearest first, up to the first inclusive
-    // prefix (done) or the first tile that has not published yet (read again
-    // from there).  Tile 0 always publishes an inclusive prefix, so the walk
-    // ends at or before it; reads before tile 0 are never issued.
-    int64_t j = int64_t(tile) - 1;  // nearest predecessor not yet added
-    for (;;) {
-      uint32_t v[kLookWindow];
 #pragma unroll
-      for (uint32_t w = 0; w < kLookWindow; ++w) {
-        const int64_t q = j - int64_t(w);
-        v[w] = q >= 0 ? __hip_atomic_load(look + uint64_t(q) * 256 + d, __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT)
-                      : kFlagInclusive;
-      }
-      bool stop = false, done = false;
-      uint32_t taken = 0;
+    for (uint32_t j = 0; j < kDigitsPerThread; ++j)
+      __hip_atomic_store(mine + j, kFlagAggregate | total[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // Windowed look-back, both digits together: each round reads the next
+    // kLookWindow predecessors of every unfinished digit at once and adds
+    // their counts, nearest first, up to the first inclusive prefix (done) or
+    // the first tile that has not published yet (read again from there).
+    // Tile 0 always publishes inclusive prefixes, so each walk ends at or
+    // before it; reads before tile 0 are never issued.
+    int64_t next[kDigitsPerThread];
+    bool done[kDigitsPerThread];
 #pragma unroll
-      for (uint32_t w = 0; w < kLookWindow; ++w) {
-        const uint32_t flag = v[w] & ~kValueMask;
-        if (!stop) {
-          if (flag == 0) {
-            stop = true;  // not published yet
-          } else {
-            exclusive += v[w] & kValueMask;
-            ++taken;
-            if (flag == kFlagInclusive) stop = done = true;
+    for (uint32_t j = 0; j < kDigitsPerThread; ++j) { next[j] = int64_t(tile) - 1; done[j] = false; }
+    while (!done[0] || !done[1]) {
+      uint32_t v[kDigitsPerThread][kLookWindow];
+#pragma unroll
+      for (uint32_t j = 0; j < kDigitsPerThread; ++j)
+#pragma unroll
+        for (uint32_t w = 0; w < kLookWindow; ++w) {
+          const int64_t q = next[j] - int64_t(w);
+          v[j][w] = (!done[j] && q >= 0)
+                        ? __hip_atomic_load(look + uint64_t(q) * kDigits + kDigitsPerThread * t + j,
+                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                        : kFlagInclusive;
+        }
+#pragma unroll
+      for (uint32_t j = 0; j < kDigitsPerThread; ++j) {
+        if (done[j]) continue;
+        bool stop = false;
+        uint32_t taken = 0;
+#pragma unroll
+        for (uint32_t w = 0; w < kLookWindow; ++w) {
+          const uint32_t flag = v[j][w] & ~kValueMask;
+          if (!stop) {
+            if (flag == 0) {
+              stop = true;  // not published yet
+            } else {
+              exclusive[j] += v[j][w] & kValueMask;
+              ++taken;
+              if (flag == kFlagInclusive) stop = done[j] = true;
+            }
           }
         }
+        next[j] -= int64_t(taken);
       }
-      if (done) break;
-      j -= int64_t(taken);
     }
-    __hip_atomic_store(mine, kFlagInclusive | (exclusive + total), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (uint32_t j = 0; j < kDigitsPerThread; ++j)
+      __hip_atomic_store(mine + j, kFlagInclusive | (exclusive[j] + total[j]), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
   }
-  const uint32_t digit_base = BlockExclusiveScan(digit_count, s_scan);
-  const uint32_t tile_start = BlockExclusiveScan(total, s_scan);
-  s_tile_start[d] = tile_start;
-  s_global[d] = digit_base + exclusive;
+  // Exclusive scans in digit order: thread t's pair (2t, 2t+1) is one scan item.
+  const uint32_t digit_base = BlockExclusiveScan(digit_count[0] + digit_count[1], s_scan);
+  const uint32_t tile_start = BlockExclusiveScan(total[0] + total[1], s_scan);
+  s_tile_start[2 * t] = tile_start;
+  s_tile_start[2 * t + 1] = tile_start + total[0];
+  s_global[2 * t] = digit_base + exclusive[0];
+  s_global[2 * t + 1] = digit_base + digit_count[0] + exclusive[1];
   __syncthreads();
 #pragma unroll
   for (uint32_t i = 0; i < kSortItems; ++i) {
@@ -508,7 +583,7 @@ int PlanPush(const eps_hip_table* tables, uint32_t table_count,
   const uint64_t max_valid = (uint64_t(table_count - 1) << plan.row_bits) | (max_rows - 1);
   plan.key_bits = BitLength(max_valid + 1);
   if (plan.key_bits > 32) return Fail(EPS_HIP_CAPACITY_EXCEEDED, "table rows exceed 32-bit sort keys");
-  plan.passes = (plan.key_bits + 7) / 8;
+  plan.passes = (plan.key_bits + kRadixBits - 1) / kRadixBits;
   uint32_t at = 0;
   for (uint32_t p = 0; p < plan.passes; ++p) {
     const uint32_t remaining = plan.key_bits - at, left = plan.passes - p;
@@ -603,7 +678,7 @@ int eps_hip_prepare(const eps_hip_table* tables, uint32_t table_count,
                        keys[(p + 1) % 2], vals[(p + 1) % 2],
                        reinterpret_cast<const uint64_t*>(ws + L.refscale),
                        reinterpret_cast<uint64_t*>(ws + L.sorted_rs), n, plan.shift[p], plan.bits[p],
-                       args.hist + p * 256, look + uint64_t(p) * L.tiles * 256,
+                       args.hist + p * kDigits, look + uint64_t(p) * L.tiles * kDigits,
                        &ctrl->tile_counter[p]);
     EPS_HIP_LAUNCHED("radix pass");
   }

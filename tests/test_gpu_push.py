@@ -116,6 +116,41 @@ def test_push_steps_match_oracle(torch_gpu, pkg, dims):
             assert tuple(shard.powers[t]) == stores[t].powers()[:2] or not any(f.table == t for f in feats)
 
 
+@pytest.mark.parametrize("pooling", [0, 1, 3])
+def test_push_with_long_runs_of_empty_bags(torch_gpu, pkg, pooling):
+    """Thousands of bags and a run of 3000 empty ones: several preparation
+    blocks per feature, one of which spans the empty run (its bag search
+    cannot stage the run and takes the global search)."""
+    torch, W, H = torch_gpu, pkg.workloads, pkg.eps_hip
+    rng = np.random.default_rng(7 + pooling)
+    specs = [W.TableSpec(0, 32, 3000, seed=41)]
+    bags = 6000
+    lengths = rng.integers(1, 9, bags)
+    lengths[1500:4500] = 0
+    offsets = np.concatenate([[0], np.cumsum(lengths)]).astype(np.uint64)
+    n = int(offsets[-1])
+    keys = (rng.zipf(1.1, n) % specs[0].rows).astype(np.uint64)
+    valid = lengths.astype(np.uint64)
+    weights = rng.random(n).astype(F32) if pooling == W.WEIGHTED_SUM else None
+    grad = rng.normal(0, 1e-2, (bags, 32)).astype(F32)
+    feats = [W.Feature(0, 0, pooling, keys, offsets, valid, weights, grad)]
+    print(f"case: pooling={pooling} occurrences={n}", flush=True)
+    shard = H.DeviceShard(torch, specs)
+    shard.init_rows()
+    dev = [H.DeviceFeature(torch, f) for f in feats]
+    shard.prepare(dev)
+    shard.push(dev)
+    status = shard.status()
+    assert status & H.STATUS_ERRORS == 0, f"status {status:#x}"
+    store = oracle_store(specs[0])
+    store.prepare(feats[0])
+    assert oracle.push([store], feats, [0], [grad]) == 0
+    keys_done = store.keys()
+    want, _ = store.read_many(keys_done)
+    got = shard.read_rows(0, torch.from_numpy(keys_done.view(np.int64)).cuda()).cpu().numpy()
+    assert_close(got.reshape(want.shape), want, "state after push", strict_ulp=0)
+
+
 def test_overflow_rejects_whole_push(torch_gpu, pkg):
     """core_tests.cpp:214-222 / cuda_tests.cpp:131-139: an overflowing update
     leaves every row untouched; non-finite gradients and bad slots likewise."""
