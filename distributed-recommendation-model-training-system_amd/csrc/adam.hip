@@ -467,7 +467,7 @@ __device__ __forceinline__ bool VecPrologue(const VecArgs& a, TableDesc* s_t, co
 // go in batches of eight 128-bit loads, the next batch issued before the
 // current one is added, so the adds never wait on a single read.
 __device__ __forceinline__ float ChainSum(float acc, const float* v) {
-  constexpr uint32_t kBatch = 8;
+  constexpr uint32_t kBatch = 4;
   const float4* v4 = reinterpret_cast<const float4*>(v);
   float4 cur[kBatch], nxt[kBatch];
 #pragma unroll
@@ -491,7 +491,7 @@ __device__ __forceinline__ float ChainSum(float acc, const float* v) {
   return acc;
 }
 
-__global__ void __launch_bounds__(kBlock) HotSliceKernel(VecArgs a) {
+__global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) HotSliceKernel(VecArgs a) {
   __shared__ TableDesc s_t[EPS_HIP_MAX_TABLES];
   __shared__ const float* s_grad[EPS_HIP_MAX_FEATURES];
   __shared__ __align__(16) float s_buf[kBlock / kWave][kSlice][kChunkPad];
@@ -886,7 +886,7 @@ uint64_t SpanBlocks(uint64_t count) {
 constexpr int kPrimary = 1, kSecond = 2;
 constexpr uint64_t kVectorGrid = 4096;  // persistent grid cap of the vector kernels
 constexpr uint64_t kSecondGrid = 256;
-constexpr uint64_t kHotGrid = 512;      // two LDS-heavy blocks per CU
+constexpr uint64_t kHotGrid = 1024;     // four blocks per CU (four waves per SIMD)
 
 template <uint32_t kLog2G>
 int LaunchRowRun(unsigned grid, const VecArgs& a, hipStream_t s) {

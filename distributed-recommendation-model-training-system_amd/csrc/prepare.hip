@@ -482,8 +482,8 @@ __device__ __forceinline__ uint32_t ClassOfKey(const HotArgs& a, uint32_t key) {
 //  * hot rows: the first position of a vector-class row with more than
 //    kLongRefs references, appended to one of the lists of the XCD that owns
 //    that eighth of the positions (the update kernels split their work the
-//    same way); the row's length picks the list (>= 8 chunks of kHotChunk
-//    references, 4-7, 2-3, 1), so the hot-row kernel can deal the longest
+//    same way); the row's length picks the list (>= 2048 references,
+//    1024-2047, 512-1023, fewer), so the hot-row kernel can deal the longest
 //    rows out first.
 __global__ void __launch_bounds__(kBlock) HotListKernel(HotArgs a) {
   const uint32_t p = blockIdx.x * kBlock + threadIdx.x;
@@ -500,8 +500,8 @@ __global__ void __launch_bounds__(kBlock) HotListKernel(HotArgs a) {
   }
   if (p >= a.n || cls + 1 >= kClasses || !first) return;
   if (p + kLongRefs >= a.n || a.keys[p + kLongRefs] != key) return;
-  const uint32_t chunks = (SegmentEndSearch(a.keys, p + kLongRefs, a.n, key) - p + kHotChunk - 1) / kHotChunk;
-  const uint32_t bucket = chunks >= 8 ? 0u : chunks >= 4 ? 1u : chunks >= 2 ? 2u : 3u;
+  const uint32_t refs = SegmentEndSearch(a.keys, p + kLongRefs, a.n, key) - p;
+  const uint32_t bucket = refs >= 2048 ? 0u : refs >= 1024 ? 1u : refs >= 512 ? 2u : 3u;
   const uint32_t list = uint32_t(uint64_t(p) * kXcds / a.n) * kHotBuckets + bucket;
   a.hot[uint64_t(list) * a.capacity + atomicAdd(&a.ctrl->long_count[list], 1u)] = p;
 }
