@@ -168,10 +168,19 @@ class DeviceFeature:
         if with_gradient and feature.gradient is not None:
             self.gradient = torch.from_numpy(np.ascontiguousarray(feature.gradient, np.float32)).to(device)
 
+    def __setattr__(self, name, value):
+        # Any change of the feature's arrays or fields drops the cached struct.
+        object.__setattr__(self, name, value)
+        object.__setattr__(self, "_struct", None)
+
     def push_struct(self, table_index=None):
-        return PushFeature(_ptr(self.indices), _ptr(self.offsets), _ptr(self.valid_lengths),
-                           _ptr(self.weights), _ptr(self.gradient), self.occurrences, self.bags,
-                           self.table if table_index is None else table_index, self.pooling)
+        if table_index is not None:
+            return PushFeature(_ptr(self.indices), _ptr(self.offsets), _ptr(self.valid_lengths),
+                               _ptr(self.weights), _ptr(self.gradient), self.occurrences, self.bags,
+                               table_index, self.pooling)
+        if self._struct is None:
+            object.__setattr__(self, "_struct", self.push_struct(self.table))
+        return self._struct
 
 
 class DeviceShard:
@@ -185,7 +194,15 @@ class DeviceShard:
         check(L.eps_hip_device_check(torch.device(device).index or 0))
         self.state = [torch.empty(s.rows * 3 * s.dim, dtype=torch.float32, device=device)
                       for s in self.specs]
-        self.powers = [[np.float32(s.b1p), np.float32(s.b2p)] for s in self.specs]
+        # Optimizer powers (beta1^t, beta2^t) per table, advanced in fp32.
+        self.powers = np.array([[s.b1p, s.b2p] for s in self.specs], dtype=np.float32)
+        self._betas = np.array([[s.beta1, s.beta2] for s in self.specs], dtype=np.float32)
+        # One persistent optimizer array for the push calls; only its powers
+        # change between pushes (written through a numpy view).
+        self._opts = (Optimizer * len(self.specs))(*[self.optimizer(t) for t in range(len(self.specs))])
+        self._opts_view = np.frombuffer(self._opts, dtype=np.dtype(
+            [(name, np.float32 if ctype is C.c_float else np.int32) for name, ctype in Optimizer._fields_]))
+        self._args_cache = {}
         self.bounds = torch.zeros(L.eps_hip_bounds_bytes() // 4, dtype=torch.int32, device=device)
         self.update_ws = torch.zeros(L.eps_hip_update_workspace_bytes() // 4, dtype=torch.int32,
                                      device=device)
@@ -240,10 +257,8 @@ class DeviceShard:
                          1 if s.bounds else 0, lo, hi)
 
     def advance_powers(self, tables):
-        for t in set(tables):
-            s = self.specs[t]
-            self.powers[t][0] = np.float32(self.powers[t][0] * np.float32(s.beta1))
-            self.powers[t][1] = np.float32(self.powers[t][1] * np.float32(s.beta2))
+        sel = list(set(tables))
+        self.powers[sel] = self.powers[sel] * self._betas[sel]  # fp32 products, as the reference
 
     # ---- pull ----
     def gather_parts(self, feats, outputs, mean_divide=True):
@@ -262,19 +277,36 @@ class DeviceShard:
         if outputs is None:
             outputs = [self.torch.empty((f.rows, self.specs[f.table].dim), dtype=self.torch.float32,
                                         device=self.device) for f in feats]
-        parts = self.gather_parts(feats, outputs, mean_divide)
-        for i in range(0, len(parts), MAX_GATHER_PARTS):
-            chunk = parts[i:i + MAX_GATHER_PARTS]
-            arr = (GatherPart * len(chunk))(*chunk)
-            check(lib().eps_hip_gather(arr, len(chunk), _ptr(status), _stream(self.torch, stream)))
+        def build():
+            parts = self.gather_parts(feats, outputs, mean_divide)
+            return [((GatherPart * len(parts[i:i + MAX_GATHER_PARTS]))(*parts[i:i + MAX_GATHER_PARTS]),
+                     len(parts[i:i + MAX_GATHER_PARTS])) for i in range(0, len(parts), MAX_GATHER_PARTS)]
+        chunks = self._cached("gather", list(feats) + list(outputs), build,
+                              (mean_divide, tuple(o.data_ptr() for o in outputs)))
+        for arr, count in chunks:
+            check(lib().eps_hip_gather(arr, count, _ptr(status), _stream(self.torch, stream)))
         return outputs
 
     # ---- push ----
+    def _cached(self, kind, objs, build, extra=()):
+        """ctypes argument array for these objects, kept for the last few object
+        lists seen (an entry holds its objects, so their ids stay unique while it
+        lives) and rebuilt when a feature's struct or `extra` has changed."""
+        key = (kind, tuple(map(id, objs)))
+        hit = self._args_cache.get(key)
+        if hit is not None and hit[1] == extra and all(
+                getattr(a, "_struct", None) is c for a, c in zip(hit[0], hit[2])):
+            return hit[3]
+        arr = build()
+        if len(self._args_cache) >= 16:
+            self._args_cache.pop(next(iter(self._args_cache)))
+        self._args_cache[key] = (list(objs), extra, [getattr(o, "_struct", None) for o in objs], arr)
+        return arr
+
     def _push_args(self, feats):
         if len(feats) > MAX_FEATURES:
             raise ValueError("too many features for one push")
-        arr = (PushFeature * len(feats))(*[f.push_struct() for f in feats])
-        return arr
+        return self._cached("push", feats, lambda: (PushFeature * len(feats))(*[f.push_struct() for f in feats]))
 
     def prepare(self, feats, stream=None, slot=0):
         self.reserve(sum(f.occurrences for f in feats))
@@ -288,8 +320,9 @@ class DeviceShard:
         `events` = (start, end) torch events recorded around the fused pass;
         `slot` = the workspace the batch was prepared in."""
         arr = self._push_args(feats)
-        opts = (Optimizer * len(self.specs))(*[self.optimizer(t) for t in range(len(self.specs))])
-        args = (self.tables, opts, len(self.specs), arr, len(feats), _ptr(self.wss[slot]), self.ws_bytes,
+        self._opts_view["beta1_power"] = self.powers[:, 0]
+        self._opts_view["beta2_power"] = self.powers[:, 1]
+        args = (self.tables, self._opts, len(self.specs), arr, len(feats), _ptr(self.wss[slot]), self.ws_bytes,
                 _ptr(self.bounds), _stream(self.torch, stream))
         L = lib()
         check(L.eps_hip_push_begin(*args))
