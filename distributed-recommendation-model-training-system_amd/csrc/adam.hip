@@ -421,7 +421,7 @@ struct VecArgs {
   const float* grad[EPS_HIP_MAX_FEATURES];
   const uint32_t* keys;
   const uint64_t* rs;
-  const uint32_t* hot;
+  const HotEntry* hot;
   Control* ctrl;
   Bounds* bounds;
   uint32_t row_bits, cls, fallback, slices, hot_capacity;
@@ -491,6 +491,14 @@ __device__ __forceinline__ float ChainSum(float acc, const float* v) {
   return acc;
 }
 
+// One chunk of a hot work unit: positions [cbase, cbase + kChunk) of the row
+// whose references are the sorted positions [start, end), for the kSlice
+// columns from col0.  `ok` is false past the wavefront's last unit.
+struct HotSlot {
+  uint32_t start, end, key, col0, cbase;
+  bool ok;
+};
+
 __global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) HotSliceKernel(VecArgs a) {
   __shared__ TableDesc s_t[EPS_HIP_MAX_TABLES];
   __shared__ const float* s_grad[EPS_HIP_MAX_FEATURES];
@@ -498,10 +506,10 @@ __global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))
   bool write = false;
   if (!VecPrologue(a, s_t, s_grad, write)) return;
   Control* ctrl = a.ctrl;
-  const uint32_t valid = ctrl->valid_count;
   const uint32_t row_mask = (1u << a.row_bits) - 1;
   const uint32_t lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   float (*buf)[kChunkPad] = s_buf[wave];
+  const bool chain = lane < kSlice;  // dim is a multiple of 4: a slice inside the row is whole
   RowStats st;
   __syncthreads();
   // XCD x takes its hot-row lists: the hot rows of the x-th eighth of the
@@ -520,123 +528,129 @@ __global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))
     units += ctrl->long_count[xcd * kHotBuckets + b] * a.slices;
     bucket_end[b] = units;
   }
-  for (uint32_t round = 0;; ++round) {
-    // Unit indices grow with the round, so the first one past the end ends the loop.
+  // The wave's units form one stream of chunks, processed in a three-stage
+  // pipeline that runs across unit boundaries: while chunk i is staged and
+  // added, the gradient rows of chunk i+1 and the reference words of chunk
+  // i+2 are in flight, whichever units they belong to.  A unit's w, m, v are
+  // loaded when its first chunk's rows are, and Adam runs after its last chunk.
+  uint32_t round = 0;
+  HotEntry next_entry{0, 0, 0, 0};
+  uint32_t next_col0 = 0;
+  bool next_ok = false;
+  auto fetch = [&]() {  // header of the wave's next unit (its load completes later)
     const uint32_t u = round * xcd_waves + ((round & 1) ? xcd_waves - 1 - me : me);
-    if (u >= units) break;
+    ++round;
+    next_ok = u < units;  // unit indices grow with the round: past the end stays past
+    if (!next_ok) return;
     uint32_t b = 0;
 #pragma unroll
     for (uint32_t k = 0; k + 1 < kHotBuckets; ++k) b += u >= bucket_end[k];
     const uint32_t local = u - (b ? bucket_end[b - 1] : 0u);
-    const uint32_t start =
-        a.hot[uint64_t(xcd * kHotBuckets + b) * a.hot_capacity + local / a.slices];
-    const uint32_t col0 = (local % a.slices) * kSlice;
-    const uint32_t key = a.keys[start];
-    const TableDesc& T = s_t[key >> a.row_bits];
-    const uint32_t dim = T.dim;
-    if (col0 >= dim) continue;  // wave-uniform
-    float* row = T.state + uint64_t(key & row_mask) * dim * 3;
-    const uint32_t cc = col0 + lane;
-    const bool chain = lane < kSlice;  // dim is a multiple of 4: the whole slice is in the row
-    float w = 0.f, m = 0.f, v = 0.f;
-    if (chain) { w = LoadF(row + cc); m = LoadF(row + dim + cc); v = LoadF(row + 2 * dim + cc); }
-    // The row's references are the positions from `start` whose key is `key`
-    // (keys are sorted, so they form one run).  Lane l stages reference
-    // cbase + kWave*k + l.  Every load is issued unconditionally at an
-    // in-bounds position (clamped to the last valid one) and masked after, so
-    // nothing in the chunk pipeline branches around a load: words and keys of
-    // chunk c+2 and gradient rows of chunk c+1 are in flight during the adds
-    // of chunk c.
-    uint64_t word[kStageLoads];
-    uint32_t kk[kStageLoads];
-    float4 x[kStageLoads];
-    uint32_t match = 0, kk_base = 0;
-    auto load_words = [&](uint32_t cbase) {
-      kk_base = cbase;
-#pragma unroll
-      for (uint32_t k = 0; k < kStageLoads; ++k) {
-        const uint32_t ref = min(cbase + kWave * k + lane, valid - 1);
-        word[k] = a.rs[ref];
-        kk[k] = a.keys[ref];
-      }
-    };
-    auto match_bits = [&]() {
-      uint32_t bits = 0;
-#pragma unroll
-      for (uint32_t k = 0; k < kStageLoads; ++k)
-        bits |= uint32_t(kk[k] == key && kk_base + kWave * k + lane < valid) << k;
-      return bits;
-    };
-    // A position outside the row holds another row's reference, whose
-    // gradient buffer may have another dimension and fewer rows: its address
-    // is formed from the row's own first reference instead (`own`), so every
-    // load stays inside this table's gradient rows; the value is discarded.
-    const uint64_t own = a.rs[start];
-    auto load_rows = [&]() {
-#pragma unroll
-      for (uint32_t k = 0; k < kStageLoads; ++k) {
-        float unused;
-        const uint64_t wk = ((match >> k) & 1u) ? word[k] : own;
-        x[k] = Load4(RefSource(s_grad, wk, dim, col0, unused));
-      }
-    };
-    auto chunk_refs = [&](uint32_t bits) {
-      uint32_t count = 0;
-#pragma unroll
-      for (uint32_t k = 0; k < kStageLoads; ++k)
-        count += uint32_t(__popcll(__ballot((bits >> k) & 1u)));
-      return count;
-    };
-    uint32_t cbase = start;
-    load_words(cbase);
-    match = match_bits();
-    load_rows();
-    uint32_t scale_bits[kStageLoads];
-#pragma unroll
-    for (uint32_t k = 0; k < kStageLoads; ++k) scale_bits[k] = uint32_t(word[k] >> 32);
-    uint32_t n = chunk_refs(match);
-    load_words(cbase + kChunk);
-    float acc = 0.f;
-    // Straight-line body (no loads under a condition): each register set is
-    // consumed before it is reloaded in place, so nothing waits on a load that
-    // was just issued.
-    while (n) {
-      // The product src*scale of each reference, rounded as the reference's
-      // separate multiply (the add happens in the chain below).  Positions of
-      // other rows are staged as -0.0f, the exact identity of IEEE addition
-      // (x + -0 == x for every x, signed zeros included), so the chain always
-      // runs over a whole chunk without changing any bit of the sum.
-#pragma unroll
-      for (uint32_t k = 0; k < kStageLoads; ++k) {
-        const bool in = (match >> k) & 1u;
-        const float sv = __uint_as_float(scale_bits[k]);
-        const uint32_t r = kWave * k + lane;
-        buf[0][r] = in ? x[k].x * sv : -0.f;
-        buf[1][r] = in ? x[k].y * sv : -0.f;
-        buf[2][r] = in ? x[k].z * sv : -0.f;
-        buf[3][r] = in ? x[k].w * sv : -0.f;
-      }
-      WaveSync();
-      // Next chunk: rows from the words already loaded, then words and keys
-      // of the chunk after it.  A chunk that is not full is the row's last.
-      match = n == kChunk ? match_bits() : 0u;
-      load_rows();
-#pragma unroll
-      for (uint32_t k = 0; k < kStageLoads; ++k) scale_bits[k] = uint32_t(word[k] >> 32);
-      const uint32_t n_next = chunk_refs(match);
-      load_words(cbase + 2 * kChunk);
-      if (chain) acc = ChainSum(acc, buf[lane]);
-      WaveSync();
-      n = n_next;
-      cbase += kChunk;
+    // The entry is the same for the whole wave: keep it in scalar registers.
+    const HotEntry e = a.hot[uint64_t(xcd * kHotBuckets + b) * a.hot_capacity + local / a.slices];
+    next_entry = HotEntry{uint32_t(__builtin_amdgcn_readfirstlane(int(e.start))),
+                          uint32_t(__builtin_amdgcn_readfirstlane(int(e.end))),
+                          uint32_t(__builtin_amdgcn_readfirstlane(int(e.key))), 0u};
+    next_col0 = (local % a.slices) * kSlice;
+  };
+  auto take = [&]() {  // the next unit's first chunk; slices past a row's dimension are skipped
+    for (;;) {
+      HotSlot t{next_entry.start, next_entry.end, next_entry.key, next_col0, next_entry.start, next_ok};
+      const bool usable = !next_ok || next_col0 < s_t[next_entry.key >> a.row_bits].dim;
+      fetch();
+      if (usable) return t;
     }
-    if (chain) {
-      AdamElement(T, acc, w, m, v, st);
-      if (write) {
-        StoreF(row + cc, w); StoreF(row + dim + cc, m); StoreF(row + 2 * dim + cc, v);
-        Track(st, w, m, v);
-      }
+  };
+  auto after = [&](const HotSlot& c) {  // the chunk that follows c in the stream
+    if (c.ok && c.cbase + kChunk < c.end) {
+      HotSlot t = c;
+      t.cbase += kChunk;
+      return t;
     }
+    return take();
+  };
+  // Loads of one stage.  A lane past the row's end reads the row's last
+  // reference (so every address lies in this table's gradient rows) and its
+  // product is masked to -0.0f, the exact identity of IEEE addition.
+  uint64_t word[kStageLoads];
+  float4 x[kStageLoads];
+  auto load_words = [&](const HotSlot& c) {
+    if (!c.ok) return;
+#pragma unroll
+    for (uint32_t k = 0; k < kStageLoads; ++k) word[k] = a.rs[min(c.cbase + kWave * k + lane, c.end - 1)];
+  };
+  auto load_rows = [&](const HotSlot& c, uint32_t& in_bits, uint32_t* scale_bits) {
+    in_bits = 0;
+    if (!c.ok) return;
+    const uint32_t dim = s_t[c.key >> a.row_bits].dim;
+#pragma unroll
+    for (uint32_t k = 0; k < kStageLoads; ++k) {
+      float unused;
+      in_bits |= uint32_t(c.cbase + kWave * k + lane < c.end) << k;
+      scale_bits[k] = uint32_t(word[k] >> 32);
+      x[k] = Load4(RefSource(s_grad, word[k], dim, c.col0, unused));
+    }
+  };
+  float wmv_r[3] = {0.f, 0.f, 0.f}, wmv_p[3] = {0.f, 0.f, 0.f};
+  auto load_state = [&](const HotSlot& c, float* wmv) {
+    if (!c.ok || !chain) return;
+    const TableDesc& T = s_t[c.key >> a.row_bits];
+    const float* row = T.state + uint64_t(c.key & row_mask) * T.dim * 3 + c.col0 + lane;
+    wmv[0] = LoadF(row); wmv[1] = LoadF(row + T.dim); wmv[2] = LoadF(row + 2 * T.dim);
+  };
+
+  // Fill the pipeline: chunk 0's rows (and its row's state), chunk 1's words.
+  fetch();
+  HotSlot cp = take();  // chunk being staged and added
+  uint32_t in_p = 0, sc_p[kStageLoads];
+  load_words(cp);
+  load_rows(cp, in_p, sc_p);
+  load_state(cp, wmv_p);
+  HotSlot cr = after(cp);  // chunk whose rows load next
+  load_words(cr);
+  float acc = 0.f;
+  while (cp.ok) {
+    const HotSlot cw = after(cr);  // chunk whose words load next
+#pragma unroll
+    for (uint32_t k = 0; k < kStageLoads; ++k) {
+      const bool in = (in_p >> k) & 1u;
+      const float sv = __uint_as_float(sc_p[k]);
+      const uint32_t r = kWave * k + lane;
+      buf[0][r] = in ? x[k].x * sv : -0.f;
+      buf[1][r] = in ? x[k].y * sv : -0.f;
+      buf[2][r] = in ? x[k].z * sv : -0.f;
+      buf[3][r] = in ? x[k].w * sv : -0.f;
+    }
+    WaveSync();
+    const bool r_first = cr.ok && cr.cbase == cr.start;
+    uint32_t in_r = 0, sc_r[kStageLoads];
+    load_rows(cr, in_r, sc_r);
+    if (r_first) load_state(cr, wmv_r);
+    load_words(cw);
+    if (chain) acc = ChainSum(acc, buf[lane]);
+    WaveSync();
+    if (cp.cbase + kChunk >= cp.end) {  // cp was its unit's last chunk
+      if (chain) {
+        const TableDesc& T = s_t[cp.key >> a.row_bits];
+        float w = wmv_p[0], m = wmv_p[1], v = wmv_p[2];
+        AdamElement(T, acc, w, m, v, st);
+        if (write) {
+          float* row = T.state + uint64_t(cp.key & row_mask) * T.dim * 3 + cp.col0 + lane;
+          StoreF(row, w); StoreF(row + T.dim, m); StoreF(row + 2 * T.dim, v);
+          Track(st, w, m, v);
+        }
+      }
+      acc = 0.f;
+    }
+    if (r_first) {
+#pragma unroll
+      for (uint32_t k = 0; k < 3; ++k) wmv_p[k] = wmv_r[k];
+    }
+    cp = cr;
+    cr = cw;
+    in_p = in_r;
+#pragma unroll
+    for (uint32_t k = 0; k < kStageLoads; ++k) sc_p[k] = sc_r[k];
   }
   FinishBlock(st, ctrl, a.bounds, write);
 }
@@ -944,7 +958,7 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
     for (uint32_t f = 0; f < feature_count; ++f) va.grad[f] = features[f].gradients;
     va.keys = a.keys;
     va.rs = a.rs;
-    va.hot = reinterpret_cast<const uint32_t*>(ws + L.long_list);
+    va.hot = reinterpret_cast<const HotEntry*>(ws + L.long_list);
     va.hot_capacity = uint32_t(L.HotCapacity());
     va.ctrl = a.ctrl;
     va.bounds = bounds;

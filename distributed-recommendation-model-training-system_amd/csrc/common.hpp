@@ -58,6 +58,9 @@ enum Mode : uint32_t { kFused = 0, kChecked = 1, kReject = 2 };
 // Bounds domain: kBoundSlots x {W, M, V, unused} as non-negative float bits.
 struct Bounds { uint32_t v[kBoundSlots][4]; };
 
+// A hot row: its sorted positions [start, end) and its key.
+struct HotEntry { uint32_t start, end, key, pad; };
+
 // Workspace layout of a push, for `n` occurrences.
 struct PushLayout {
   uint64_t n, tiles;
@@ -81,7 +84,7 @@ struct PushLayout {
     flags = at; at = align(at + n * 4);
     ranks = at; at = align(at + n * 4);
     block_sums = at; at = align(at + ((n + 1023) / 1024 + 1) * 4);
-    long_list = at; at = align(at + kXcds * kHotBuckets * HotCapacity() * 4);
+    long_list = at; at = align(at + kXcds * kHotBuckets * HotCapacity() * sizeof(HotEntry));
     total = at;
   }
 };

@@ -457,7 +457,7 @@ __global__ void ScanApplyKernel(const uint32_t* flags, const uint32_t* block_sum
 // independent.
 struct HotArgs {
   const uint32_t* keys;
-  uint32_t* hot;
+  HotEntry* hot;
   Control* ctrl;
   uint32_t n, row_bits, capacity, sentinel;
   uint32_t class_key[kClasses + 1];  // first table key index of each class (+ table count)
@@ -479,12 +479,12 @@ __device__ __forceinline__ uint32_t ClassOfKey(const HotArgs& a, uint32_t key) {
 //    written by the one position where the class steps over c (the keys are
 //    sorted and key indices are ordered by class); class_start[kClasses] is
 //    the number of valid occurrences;
-//  * hot rows: the first position of a vector-class row with more than
-//    kLongRefs references, appended to one of the lists of the XCD that owns
-//    that eighth of the positions (the update kernels split their work the
-//    same way); the row's length picks the list (>= 2048 references,
-//    1024-2047, 512-1023, fewer), so the hot-row kernel can deal the longest
-//    rows out first.
+//  * hot rows: a vector-class row with more than kLongRefs references (its
+//    positions and key) is appended, by the thread at its first position, to
+//    one of the lists of the XCD that owns that eighth of the positions (the
+//    update kernels split their work the same way); the row's length picks
+//    the list (>= 2048 references, 1024-2047, 512-1023, fewer), so the
+//    hot-row kernel can deal the longest rows out first.
 __global__ void __launch_bounds__(kBlock) HotListKernel(HotArgs a) {
   const uint32_t p = blockIdx.x * kBlock + threadIdx.x;
   if (p > a.n) return;
@@ -500,10 +500,10 @@ __global__ void __launch_bounds__(kBlock) HotListKernel(HotArgs a) {
   }
   if (p >= a.n || cls + 1 >= kClasses || !first) return;
   if (p + kLongRefs >= a.n || a.keys[p + kLongRefs] != key) return;
-  const uint32_t refs = SegmentEndSearch(a.keys, p + kLongRefs, a.n, key) - p;
+  const uint32_t end = SegmentEndSearch(a.keys, p + kLongRefs, a.n, key), refs = end - p;
   const uint32_t bucket = refs >= 2048 ? 0u : refs >= 1024 ? 1u : refs >= 512 ? 2u : 3u;
   const uint32_t list = uint32_t(uint64_t(p) * kXcds / a.n) * kHotBuckets + bucket;
-  a.hot[uint64_t(list) * a.capacity + atomicAdd(&a.ctrl->long_count[list], 1u)] = p;
+  a.hot[uint64_t(list) * a.capacity + atomicAdd(&a.ctrl->long_count[list], 1u)] = HotEntry{p, end, key, 0u};
 }
 
 struct UniqueArgs {
@@ -685,7 +685,7 @@ int eps_hip_prepare(const eps_hip_table* tables, uint32_t table_count,
   // Hot rows of the sorted keys.
   HotArgs ha{};
   ha.keys = keys[plan.passes % 2];
-  ha.hot = reinterpret_cast<uint32_t*>(ws + L.long_list);
+  ha.hot = reinterpret_cast<HotEntry*>(ws + L.long_list);
   ha.ctrl = ctrl;
   ha.n = n;
   ha.row_bits = plan.row_bits;

@@ -85,3 +85,63 @@ def test_ragged8_weighted_steps(torch_gpu, pkg):
     """8 ragged tables (dims 16..256, 100k..5M rows), weighted sum, Poisson(8) bags."""
     W, H = pkg.workloads, pkg.eps_hip
     run(torch_gpu, W, H, W.Ragged8(), 2)
+
+
+def sub_feature(f, bags=None, keep_keys=None):
+    """The feature restricted to some bags (pull check) or to the occurrences of
+    some keys in every bag (push check).  Bag lengths for the mean stay the
+    original ones, so each kept term has the scale it has in the full batch."""
+    starts, ends = f.offsets[:-1].astype(np.int64), f.offsets[1:].astype(np.int64)
+    if bags is not None:
+        parts = [f.keys[starts[b]:ends[b]] for b in bags]
+        offsets = np.concatenate([[0], np.cumsum([len(p) for p in parts])]).astype(np.uint64)
+        return type(f)(f.table, f.feature, f.pooling, np.concatenate(parts).astype(np.uint64), offsets,
+                       f.valid_lengths[bags], None, f.gradient[bags])
+    keep = np.isin(f.keys, keep_keys)
+    kept_before = np.concatenate([[0], np.cumsum(keep)])
+    offsets = kept_before[np.concatenate([starts[:1], ends])].astype(np.uint64)
+    return type(f)(f.table, f.feature, f.pooling, f.keys[keep], offsets, f.valid_lengths, None,
+                   f.gradient)
+
+
+def test_large4_full_size_sampled(torch_gpu, pkg):
+    """4 x 12,500,000 x 128 (77 GB of state), 262,144 bags x 32 per table, Zipf(1.1), mean.
+    The whole step runs at full size on the device; the oracle checks 1,024 sampled bags
+    of the pull and, after the push, the 16 hottest and 240 random touched rows of each
+    table (their reduced gradients take every occurrence of those keys, in order)."""
+    torch, W, H = torch_gpu, pkg.workloads, pkg.eps_hip
+    t0 = time.time()
+    wl = W.Large4()
+    feats = wl.batch(0)
+    print(f"large4 batch generated ({time.time() - t0:.1f}s)", flush=True)
+    shard = H.DeviceShard(torch, wl.tables, max_occurrences=sum(len(f.keys) for f in feats))
+    shard.init_rows()
+    dev = [H.DeviceFeature(torch, f) for f in feats]
+    pulled = shard.lookup(dev)
+    shard.prepare(dev)
+    shard.push(dev)
+    status = shard.status()
+    assert status & H.STATUS_ERRORS == 0, f"status {status:#x}"
+    print(f"large4 device step done ({time.time() - t0:.1f}s)", flush=True)
+    rng = np.random.default_rng(44)
+    for f, out in zip(feats, pulled):
+        spec = wl.tables[f.table]
+        bags = np.sort(rng.choice(len(f.valid_lengths), 1024, replace=False))
+        sub = sub_feature(f, bags=bags)
+        want = expected_pull(oracle_store(spec), sub)
+        assert_close(out[torch.from_numpy(bags).cuda()].cpu().numpy(), want,
+                     f"large4 pull table {f.table}", strict_ulp=0)
+        uniq, counts = np.unique(f.keys, return_counts=True)
+        hottest = uniq[np.argsort(-counts)[:16]]
+        sample = np.union1d(hottest, rng.choice(uniq, 240, replace=False)).astype(np.uint64)
+        part = sub_feature(f, keep_keys=sample)
+        store = oracle_store(spec)
+        store.prepare(part)
+        assert oracle.push([store], [part], [0], [part.gradient]) == 0, oracle.last_error()
+        keys = store.keys()
+        assert len(keys) == len(sample)
+        want, _ = store.read_many(keys)
+        got = shard.read_rows(f.table, torch.from_numpy(keys.view(np.int64)).cuda()).cpu().numpy()
+        assert_close(got.reshape(want.shape), want, f"large4 state table {f.table}", strict_ulp=0)
+        assert tuple(shard.powers[f.table]) == store.powers()[:2]
+        print(f"large4 table {f.table} ok ({time.time() - t0:.1f}s)", flush=True)
