@@ -166,10 +166,11 @@ struct RowStats {
 
 // Block-wide copy of a kernel-argument array to LDS, one 32-bit word per
 // thread per step (the arrays are read in place from the argument segment).
+template <uint32_t kThreads = kBlock>
 __device__ __forceinline__ void CopyWords(void* dst, const void* src, uint32_t bytes) {
   const uint32_t* from = static_cast<const uint32_t*>(src);
   uint32_t* to = static_cast<uint32_t*>(dst);
-  for (uint32_t i = threadIdx.x; i < bytes / 4; i += kBlock) to[i] = from[i];
+  for (uint32_t i = threadIdx.x; i < bytes / 4; i += kThreads) to[i] = from[i];
 }
 
 // One element: Adam in the reference's operation order; returns w (unclamped).
@@ -229,8 +230,9 @@ __device__ __forceinline__ void Accumulate4(float4& acc, float4 x, float s) {
 
 // Block-level fold of the per-lane statistics: error bits to the status word,
 // written maxima to one slot of the bounds domain.
+template <uint32_t kWaves = kBlock / kWave>
 __device__ void FinishBlock(const RowStats& st, Control* ctrl, Bounds* bounds, bool wrote) {
-  __shared__ uint32_t s_red[4][4];
+  __shared__ uint32_t s_red[kWaves][4];
   uint32_t e = st.err;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) e |= uint32_t(__shfl_xor(int(e), o));
@@ -242,7 +244,7 @@ __device__ void FinishBlock(const RowStats& st, Control* ctrl, Bounds* bounds, b
   __syncthreads();
   if (threadIdx.x == 0) {
     uint32_t E = 0, W = 0, M = 0, V = 0;
-    for (int i = 0; i < 4; ++i) {
+    for (uint32_t i = 0; i < kWaves; ++i) {
       E |= s_red[i][0]; W = max(W, s_red[i][1]); M = max(M, s_red[i][2]); V = max(V, s_red[i][3]);
     }
     if (E) atomicOr(&ctrl->status, E);
@@ -397,22 +399,32 @@ __global__ void __launch_bounds__(kBlock) SortedUpdateKernel(FusedArgs a) {
 // Vector-class update (dim % 4 == 0, dim <= 256).  Two kernels:
 //
 //  * HotSliceKernel: rows with more than kLongRefs references (listed at
-//    prepare time).  Work unit = (hot row, kSlice-column slice), one
-//    wavefront.  The wave stages products src*scale of kChunk references into
-//    its own LDS tile ([column][reference]); kSlice lanes (one per column)
-//    then add them in reference order.  The next chunk's gradient loads and
-//    the chunk after that's reference words are in flight during the adds.
-//    Adam is elementwise, so the slices of one row are independent and a hot
-//    row's serial chain is spread over dim/kSlice wavefronts.
+//    prepare time).  Work unit = (hot row, kSlice-column slice); a block
+//    works through a stream of units chunk by chunk (kHotChunk references).
+//    Wave 0 adds: lane c owns column col0 + c, adds the chunk's products in
+//    reference order (one dependent add per reference) and applies Adam
+//    after the unit's last chunk.  Waves 1..kProducers produce: producer p
+//    loads the gradient rows of every kProducers-th chunk (16 contiguous
+//    bytes per lane), multiplies them by their scales and stores the products
+//    into one of kHotRing LDS tiles [column][reference], with the unit's
+//    w, m, v when the chunk is its last.  Tiles change hands through two LDS
+//    counters per tile (staged / added), so the waves never meet at a block
+//    barrier, and each producer keeps two chunks of rows in flight: the
+//    adding wave's serial chain is the critical path.
 //  * RowRunKernel: every other row.  A block owns kRunPositions sorted
 //    positions; it stages their keys and reference words (plus kLongRefs
 //    positions of look-ahead) in LDS with coalesced loads, finds the segment
 //    heads with a ballot, and a group of G = dim/4 lanes per row (lane = 4
 //    columns) loads the row's w, m, v together with its gradient rows, sums
 //    them in order and applies Adam.
-constexpr uint32_t kChunk = kHotChunk;
-constexpr uint32_t kChunkPad = kChunk + 4;
-constexpr uint32_t kStageLoads = kChunk / kWave;        // staging loads per lane per chunk
+constexpr uint32_t kHotBlock = 256;                       // threads of a hot-row block
+constexpr uint32_t kHotRing = 4;                          // chunks staged in LDS per block
+constexpr uint32_t kHotPitch = kHotChunk + 4;             // floats per tile row (one column)
+constexpr uint32_t kHotQuads = kSlice / 4;                // lanes per reference in a row load
+constexpr uint32_t kHotRefsPerLoad = kWave / kHotQuads;   // references per row load
+constexpr uint32_t kHotLoads = kHotChunk / kHotRefsPerLoad;  // row loads per producer lane per chunk
+constexpr uint32_t kProducers = kHotBlock / kWave - 1;
+static_assert(kSlice == kWave && kHotChunk == kWave && kHotQuads == 16, "hot-row tile shape");
 constexpr uint32_t kRunPositions = 128;
 constexpr uint32_t kRefBatch = 4;                       // gradient rows in flight per group
 
@@ -424,14 +436,15 @@ struct VecArgs {
   const HotEntry* hot;
   Control* ctrl;
   Bounds* bounds;
-  uint32_t row_bits, cls, fallback, slices, hot_capacity;
+  uint32_t row_bits, cls, fallback, slice_bits, hot_capacity;
 };
 
-// Orders a wavefront's LDS writes before its later LDS reads (and the reverse).
-__device__ __forceinline__ void WaveSync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+// Position of (column c, reference r) in a hot-row tile.  Groups of four
+// references are rotated by the column's quarter (XOR), so the four stores of
+// a producer's row load hit 64 distinct banks, and the adding wave's 16-byte
+// reads of four consecutive references stay aligned.
+__device__ __forceinline__ uint32_t TileAt(uint32_t c, uint32_t r) {
+  return c * kHotPitch + 4u * ((r >> 2) ^ (c >> 4)) + (r & 3u);
 }
 
 __device__ __forceinline__ const float* RefSource(const float* const* grad, uint64_t word,
@@ -443,10 +456,11 @@ __device__ __forceinline__ const float* RefSource(const float* const* grad, uint
 
 // Copies the per-launch tables to LDS and decides whether this launch writes;
 // returns false when it has nothing to do (uniform over the block).
+template <uint32_t kThreads = kBlock>
 __device__ __forceinline__ bool VecPrologue(const VecArgs& a, TableDesc* s_t, const float** s_grad,
                                             bool& write) {
-  CopyWords(s_t, a.t, sizeof(a.t));
-  CopyWords(s_grad, a.grad, sizeof(a.grad));
+  CopyWords<kThreads>(s_t, a.t, sizeof(a.t));
+  CopyWords<kThreads>(s_grad, a.grad, sizeof(a.grad));
   Control* ctrl = a.ctrl;
   const uint32_t mode = ctrl->mode;
   if (!a.fallback) {
@@ -463,82 +477,115 @@ __device__ __forceinline__ bool VecPrologue(const VecArgs& a, TableDesc* s_t, co
   return true;
 }
 
-// acc + v[0] + v[1] + ... + v[kChunk-1], strictly left to right.  LDS reads
-// go in batches of eight 128-bit loads, the next batch issued before the
-// current one is added, so the adds never wait on a single read.
-__device__ __forceinline__ float ChainSum(float acc, const float* v) {
-  constexpr uint32_t kBatch = 4;
-  const float4* v4 = reinterpret_cast<const float4*>(v);
-  float4 cur[kBatch], nxt[kBatch];
-#pragma unroll
-  for (uint32_t i = 0; i < kBatch; ++i) cur[i] = v4[i];
-#pragma unroll
-  for (uint32_t b = 0; b < kChunk / (4 * kBatch); ++b) {
-    if (b + 1 < kChunk / (4 * kBatch)) {
-#pragma unroll
-      for (uint32_t i = 0; i < kBatch; ++i) nxt[i] = v4[(b + 1) * kBatch + i];
-    }
-#pragma unroll
-    for (uint32_t i = 0; i < kBatch; ++i) {
-      acc = acc + cur[i].x;
-      acc = acc + cur[i].y;
-      acc = acc + cur[i].z;
-      acc = acc + cur[i].w;
-    }
-#pragma unroll
-    for (uint32_t i = 0; i < kBatch; ++i) cur[i] = nxt[i];
-  }
-  return acc;
-}
-
-// One chunk of a hot work unit: positions [cbase, cbase + kChunk) of the row
-// whose references are the sorted positions [start, end), for the kSlice
-// columns from col0.  `ok` is false past the wavefront's last unit.
+// One chunk of a hot work unit: positions [cbase, cbase + kHotChunk) of the
+// row whose references are the sorted positions [start, end), for the kSlice
+// columns from col0.  `ok` is false past the stream's last unit.  Every field
+// is the same in all lanes of a wavefront.
 struct HotSlot {
   uint32_t start, end, key, col0, cbase;
   bool ok;
 };
 
-__global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))) HotSliceKernel(VecArgs a) {
+// A producer's loads of one chunk in flight.  Row load k brings columns
+// 4*quad .. 4*quad+3 of reference kHotRefsPerLoad*k + sub, with its scale;
+// wmv is lane l's column of the unit's w, m, v (used when the chunk ends its
+// unit).
+struct HotRows {
+  HotSlot c;
+  float4 x[kHotLoads];
+  float s[kHotLoads];
+  float wmv[3];
+};
+
+// A producer's row pointers and scales of one chunk, staged in LDS in the
+// order the row loads use them: entry [sub][k] is reference
+// kHotRefsPerLoad*k + sub, so a lane reads its kHotLoads pointers and scales
+// with a few 16-byte reads.
+struct HotRefs {
+  const float* src[kHotRefsPerLoad][kHotLoads];
+  float scale[kHotRefsPerLoad][kHotLoads];
+};
+
+// s_waitcnt operand that waits for LDS (and scalar memory) accesses only:
+// vmcnt and expcnt at their maxima, lgkmcnt 0.
+constexpr int kLgkmZero = 0xC07F;
+
+// Spin limit of the hand-over waits: a wait that has not been satisfied after
+// this many polls marks the push failed and stops waiting, so a block always
+// finishes.
+constexpr uint32_t kHotSpinLimit = 1u << 22;
+
+// Waits until the LDS counter reaches `target` (all lanes read the same word).
+// Returns false on a timeout.
+__device__ __forceinline__ bool WaitCounter(const uint32_t* counter, uint32_t target, uint32_t sleep) {
+  for (uint32_t spins = 0;; ++spins) {
+    const uint32_t v = uint32_t(__builtin_amdgcn_readfirstlane(
+        int(__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP))));
+    if (v >= target) break;
+    if (spins >= kHotSpinLimit) return false;
+    if (sleep) __builtin_amdgcn_s_sleep(1);
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+  return true;
+}
+
+// Publishes `value` after this wave's earlier LDS accesses.
+__device__ __forceinline__ void PostCounter(uint32_t* counter, uint32_t value) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  if ((threadIdx.x & (kWave - 1)) == 0)
+    __hip_atomic_store(counter, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+__global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
   __shared__ TableDesc s_t[EPS_HIP_MAX_TABLES];
   __shared__ const float* s_grad[EPS_HIP_MAX_FEATURES];
-  __shared__ __align__(16) float s_buf[kBlock / kWave][kSlice][kChunkPad];
+  __shared__ __align__(16) float s_tile[kHotRing][kSlice * kHotPitch];
+  __shared__ float s_wmv[kHotRing][3][kSlice];
+  __shared__ __align__(16) HotRefs s_ref[kProducers];
+  // ready[t]: chunks staged in tile t so far; used[t]: chunks added from it.
+  __shared__ uint32_t s_ready[kHotRing], s_used[kHotRing];
   bool write = false;
-  if (!VecPrologue(a, s_t, s_grad, write)) return;
+  if (!VecPrologue<kHotBlock>(a, s_t, s_grad, write)) return;
+  if (threadIdx.x < kHotRing) {
+    s_ready[threadIdx.x] = 0;
+    s_used[threadIdx.x] = 0;
+  }
   Control* ctrl = a.ctrl;
   const uint32_t row_mask = (1u << a.row_bits) - 1;
-  const uint32_t lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
-  float (*buf)[kChunkPad] = s_buf[wave];
-  const bool chain = lane < kSlice;  // dim is a multiple of 4: a slice inside the row is whole
+  const uint32_t lane = threadIdx.x & (kWave - 1);
+  const uint32_t wave = uint32_t(__builtin_amdgcn_readfirstlane(int(threadIdx.x / kWave)));
   RowStats st;
   __syncthreads();
   // XCD x takes its hot-row lists: the hot rows of the x-th eighth of the
   // sorted positions, whose gradient rows the row runs of that XCD also read.
   // Work units are (row, slice) in list order, longest rows first, dealt to
-  // the XCD's wavefronts in snake order (round r goes left to right when r is
-  // even, right to left when odd), so each wave gets at most one of the
-  // longest units and the per-wave totals stay close.
+  // the XCD's blocks in snake order (round r goes left to right when r is
+  // even, right to left when odd), so each block gets at most one of the
+  // longest units and the per-block totals stay close.
   const uint32_t xcd = blockIdx.x % kXcds;
-  const uint32_t xcd_waves = gridDim.x / kXcds * (kBlock / kWave);
-  const uint32_t me = (blockIdx.x / kXcds) * (kBlock / kWave) + wave;
+  const uint32_t xcd_blocks = gridDim.x / kXcds;
+  const uint32_t me = blockIdx.x / kXcds;
+  const uint32_t slice_mask = (1u << a.slice_bits) - 1;
   uint32_t bucket_end[kHotBuckets];
   uint32_t units = 0;
 #pragma unroll
   for (uint32_t b = 0; b < kHotBuckets; ++b) {
-    units += ctrl->long_count[xcd * kHotBuckets + b] * a.slices;
+    units += uint32_t(__builtin_amdgcn_readfirstlane(int(ctrl->long_count[xcd * kHotBuckets + b])))
+             << a.slice_bits;
     bucket_end[b] = units;
   }
-  // The wave's units form one stream of chunks, processed in a three-stage
-  // pipeline that runs across unit boundaries: while chunk i is staged and
-  // added, the gradient rows of chunk i+1 and the reference words of chunk
-  // i+2 are in flight, whichever units they belong to.  A unit's w, m, v are
-  // loaded when its first chunk's rows are, and Adam runs after its last chunk.
+  // Hot-row entries are read through the scalar cache (the lists are written
+  // before this kernel and only read here): a scalar load's wait does not
+  // wait for the vector loads in flight.
+  const auto* hot = reinterpret_cast<const __attribute__((address_space(4))) HotEntry*>(
+      reinterpret_cast<uintptr_t>(a.hot));
+  // The block's stream of chunks; every wave walks it the same way.
   uint32_t round = 0;
   HotEntry next_entry{0, 0, 0, 0};
   uint32_t next_col0 = 0;
   bool next_ok = false;
-  auto fetch = [&]() {  // header of the wave's next unit (its load completes later)
-    const uint32_t u = round * xcd_waves + ((round & 1) ? xcd_waves - 1 - me : me);
+  auto fetch = [&]() {  // header of the block's next unit
+    const uint32_t u = round * xcd_blocks + ((round & 1) ? xcd_blocks - 1 - me : me);
     ++round;
     next_ok = u < units;  // unit indices grow with the round: past the end stays past
     if (!next_ok) return;
@@ -546,113 +593,246 @@ __global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(4))
 #pragma unroll
     for (uint32_t k = 0; k + 1 < kHotBuckets; ++k) b += u >= bucket_end[k];
     const uint32_t local = u - (b ? bucket_end[b - 1] : 0u);
-    // The entry is the same for the whole wave: keep it in scalar registers.
-    const HotEntry e = a.hot[uint64_t(xcd * kHotBuckets + b) * a.hot_capacity + local / a.slices];
-    next_entry = HotEntry{uint32_t(__builtin_amdgcn_readfirstlane(int(e.start))),
-                          uint32_t(__builtin_amdgcn_readfirstlane(int(e.end))),
-                          uint32_t(__builtin_amdgcn_readfirstlane(int(e.key))), 0u};
-    next_col0 = (local % a.slices) * kSlice;
+    const auto& e = hot[uint64_t(xcd * kHotBuckets + b) * a.hot_capacity + (local >> a.slice_bits)];
+    next_entry = HotEntry{e.start, e.end, e.key, 0u};
+    next_col0 = (local & slice_mask) * kSlice;
   };
   auto take = [&]() {  // the next unit's first chunk; slices past a row's dimension are skipped
     for (;;) {
       HotSlot t{next_entry.start, next_entry.end, next_entry.key, next_col0, next_entry.start, next_ok};
-      const bool usable = !next_ok || next_col0 < s_t[next_entry.key >> a.row_bits].dim;
+      const uint32_t dim = uint32_t(__builtin_amdgcn_readfirstlane(int(s_t[next_entry.key >> a.row_bits].dim)));
+      const bool usable = !next_ok || next_col0 < dim;
       fetch();
       if (usable) return t;
     }
   };
   auto after = [&](const HotSlot& c) {  // the chunk that follows c in the stream
-    if (c.ok && c.cbase + kChunk < c.end) {
+    if (c.ok && c.cbase + kHotChunk < c.end) {
       HotSlot t = c;
-      t.cbase += kChunk;
+      t.cbase += kHotChunk;
       return t;
     }
     return take();
   };
-  // Loads of one stage.  A lane past the row's end reads the row's last
-  // reference (so every address lies in this table's gradient rows) and its
-  // product is masked to -0.0f, the exact identity of IEEE addition.
-  uint64_t word[kStageLoads];
-  float4 x[kStageLoads];
-  auto load_words = [&](const HotSlot& c) {
-    if (!c.ok) return;
-#pragma unroll
-    for (uint32_t k = 0; k < kStageLoads; ++k) word[k] = a.rs[min(c.cbase + kWave * k + lane, c.end - 1)];
-  };
-  auto load_rows = [&](const HotSlot& c, uint32_t& in_bits, uint32_t* scale_bits) {
-    in_bits = 0;
-    if (!c.ok) return;
-    const uint32_t dim = s_t[c.key >> a.row_bits].dim;
-#pragma unroll
-    for (uint32_t k = 0; k < kStageLoads; ++k) {
-      float unused;
-      in_bits |= uint32_t(c.cbase + kWave * k + lane < c.end) << k;
-      scale_bits[k] = uint32_t(word[k] >> 32);
-      x[k] = Load4(RefSource(s_grad, word[k], dim, c.col0, unused));
-    }
-  };
-  float wmv_r[3] = {0.f, 0.f, 0.f}, wmv_p[3] = {0.f, 0.f, 0.f};
-  auto load_state = [&](const HotSlot& c, float* wmv) {
-    if (!c.ok || !chain) return;
-    const TableDesc& T = s_t[c.key >> a.row_bits];
-    const float* row = T.state + uint64_t(c.key & row_mask) * T.dim * 3 + c.col0 + lane;
-    wmv[0] = LoadF(row); wmv[1] = LoadF(row + T.dim); wmv[2] = LoadF(row + 2 * T.dim);
-  };
+  bool stalled = false;  // a hand-over wait timed out: stop waiting, report failure
 
-  // Fill the pipeline: chunk 0's rows (and its row's state), chunk 1's words.
-  fetch();
-  HotSlot cp = take();  // chunk being staged and added
-  uint32_t in_p = 0, sc_p[kStageLoads];
-  load_words(cp);
-  load_rows(cp, in_p, sc_p);
-  load_state(cp, wmv_p);
-  HotSlot cr = after(cp);  // chunk whose rows load next
-  load_words(cr);
-  float acc = 0.f;
-  while (cp.ok) {
-    const HotSlot cw = after(cr);  // chunk whose words load next
+  if (wave == 0) {
+    // The adding wave: chunk j is the (j / kHotRing)-th use of tile j % kHotRing.
+    // Chunk j + 1's tile is read while chunk j is added, and the readiness
+    // of chunk j + 2 is polled at the same time; scheduling barriers keep the
+    // compiler from moving those LDS accesses (or their waits) before the adds.
+    __builtin_amdgcn_s_setprio(2);
+    fetch();
+    HotSlot c = take();          // chunk j
+    HotSlot cn = after(c);       // chunk j + 1
+    HotSlot cnn = after(cn);     // chunk j + 2
+    float acc = 0.f;
+    auto read_tile = [&](uint32_t j, float4* x) {
+      const float* tile = s_tile[j % kHotRing];
 #pragma unroll
-    for (uint32_t k = 0; k < kStageLoads; ++k) {
-      const bool in = (in_p >> k) & 1u;
-      const float sv = __uint_as_float(sc_p[k]);
-      const uint32_t r = kWave * k + lane;
-      buf[0][r] = in ? x[k].x * sv : -0.f;
-      buf[1][r] = in ? x[k].y * sv : -0.f;
-      buf[2][r] = in ? x[k].z * sv : -0.f;
-      buf[3][r] = in ? x[k].w * sv : -0.f;
+      for (uint32_t g = 0; g < kHotChunk / 4; ++g)
+        x[g] = *reinterpret_cast<const float4*>(tile + TileAt(lane, 4 * g));
+    };
+    auto ready = [&](uint32_t j) {
+      if (!stalled && !WaitCounter(&s_ready[j % kHotRing], j / kHotRing + 1, 0)) stalled = true;
+    };
+    // Adds chunk j (values in x, chunk c); reads chunk j + 1 into y.
+    auto add = [&](uint32_t j, const float4* x, float4* y) {
+      // x arrived during the previous adds.  Wait for it here, before more
+      // reads are issued: the LDS counter tracks at most 15 accesses, so a
+      // wait placed after the next tile's 16 reads would wait for those too.
+      __builtin_amdgcn_s_waitcnt(kLgkmZero);
+      __builtin_amdgcn_sched_barrier(0);
+      const uint32_t t = j % kHotRing;
+      float w = s_wmv[t][0][lane], m = s_wmv[t][1][lane], v = s_wmv[t][2][lane];
+      const uint32_t peek = __hip_atomic_load(&s_ready[(j + 2) % kHotRing], __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_WORKGROUP);
+      if (cn.ok) read_tile(j + 1, y);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (uint32_t g = 0; g < kHotChunk / 4; ++g) {
+        acc = acc + x[g].x;
+        acc = acc + x[g].y;
+        acc = acc + x[g].z;
+        acc = acc + x[g].w;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      // Tile t is free once chunk j's values and w, m, v are read: they were
+      // read before tile j + 1's reads, and a wavefront's LDS accesses are
+      // performed in order, so the counter store needs no wait for the reads
+      // still in flight (the wavefront-scope fence keeps the compiler from
+      // moving the reads after it).
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+      if (lane == 0)
+        __hip_atomic_store(&s_used[t], j / kHotRing + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      __builtin_amdgcn_sched_barrier(0);
+      if (c.cbase + kHotChunk >= c.end) {  // the unit's last chunk
+        const TableDesc& T = s_t[c.key >> a.row_bits];
+        if (c.col0 + lane < T.dim) {
+          AdamElement(T, acc, w, m, v, st);
+          if (write) {
+            float* row = T.state + uint64_t(c.key & row_mask) * T.dim * 3 + c.col0 + lane;
+            StoreF(row, w); StoreF(row + T.dim, m); StoreF(row + 2 * T.dim, v);
+            Track(st, w, m, v);
+          }
+        }
+        acc = 0.f;
+      }
+      // Chunk j + 2 (if any) must be staged before the next call reads it.
+      if (cnn.ok && uint32_t(__builtin_amdgcn_readfirstlane(int(peek))) < (j + 2) / kHotRing + 1)
+        ready(j + 2);
+      else
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+      c = cn;
+      cn = cnn;
+      cnn = after(cnn);
+    };
+    float4 xa[kHotChunk / 4], xb[kHotChunk / 4];
+    if (c.ok) {
+      ready(0);
+      read_tile(0, xa);
+      if (cn.ok) ready(1);
     }
-    WaveSync();
-    const bool r_first = cr.ok && cr.cbase == cr.start;
-    uint32_t in_r = 0, sc_r[kStageLoads];
-    load_rows(cr, in_r, sc_r);
-    if (r_first) load_state(cr, wmv_r);
-    load_words(cw);
-    if (chain) acc = ChainSum(acc, buf[lane]);
-    WaveSync();
-    if (cp.cbase + kChunk >= cp.end) {  // cp was its unit's last chunk
-      if (chain) {
-        const TableDesc& T = s_t[cp.key >> a.row_bits];
-        float w = wmv_p[0], m = wmv_p[1], v = wmv_p[2];
-        AdamElement(T, acc, w, m, v, st);
-        if (write) {
-          float* row = T.state + uint64_t(cp.key & row_mask) * T.dim * 3 + cp.col0 + lane;
-          StoreF(row, w); StoreF(row + T.dim, m); StoreF(row + 2 * T.dim, v);
-          Track(st, w, m, v);
+    for (uint32_t j = 0; c.ok; j += 2) {
+      add(j, xa, xb);
+      if (!c.ok) break;
+      add(j + 1, xb, xa);
+    }
+  } else {
+    // Producer p stages chunks p, p + kProducers, ... (its own chunks, counted
+    // by o).  At own chunk o it stages rows(o), decodes the words of o + 2
+    // into its LDS reference slots, loads the words of o + 3 and then the
+    // rows of o + 2.  Loads complete in issue order, so each wait waits only
+    // for what it needs: the words loaded now are decoded one own chunk
+    // later, before the rows loaded now are staged.  Every chunk issues the
+    // same loads, also past the stream's end (then from the start of the
+    // reference words, never used), so the number of loads between any two
+    // points is fixed.
+    const uint32_t p = wave - 1;
+    const uint32_t quad = lane % kHotQuads, sub = lane / kHotQuads;
+    const float* idle = reinterpret_cast<const float*>(a.rs);
+    HotRefs& slots = s_ref[p];
+    fetch();
+    HotSlot cur = take();  // cursor over the stream, at chunk jc
+    uint32_t jc = 0, total = cur.ok ? ~0u : 0u;
+    auto advance = [&](uint32_t by) {
+      for (uint32_t i = 0; i < by; ++i) {
+        cur = after(cur);
+        ++jc;
+        if (!cur.ok && total == ~0u) total = jc;
+      }
+    };
+    HotSlot wc{};  // chunk whose words are in `word`
+    HotSlot dc{};  // chunk whose references are in the LDS slots
+    uint64_t word = 0;
+    auto load_words = [&]() {
+      wc = cur;
+      const uint32_t pos = cur.ok ? min(cur.cbase + lane, cur.end - 1) : 0u;
+      word = a.rs[pos];
+    };
+    // Lane l decodes the word of reference l: its gradient row (from the
+    // slice's first column) and scale.
+    auto decode = [&]() {
+      dc = wc;
+      const TableDesc& T = s_t[wc.key >> a.row_bits];
+      float scale;
+      const float* src = RefSource(s_grad, word, T.dim, wc.col0, scale);
+      slots.src[lane % kHotRefsPerLoad][lane / kHotRefsPerLoad] = wc.ok ? src : idle;
+      slots.scale[lane % kHotRefsPerLoad][lane / kHotRefsPerLoad] = scale;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+    };
+    // Lanes whose columns lie past the row's dimension read the slice's first
+    // columns; their products are never stored by the adding wave.
+    auto load_rows = [&](HotRows& r) {
+      r.c = dc;
+      const TableDesc& T = s_t[dc.key >> a.row_bits];
+      const uint32_t dim = T.dim;
+      const uint32_t off = dc.col0 + 4 * quad < dim ? 4 * quad : 0u;
+      const uint32_t step = dc.ok ? off : 0u;
+      const float* src[kHotLoads];
+#pragma unroll
+      for (uint32_t k = 0; k < kHotLoads; k += 2) {
+        const uint4 two = *reinterpret_cast<const uint4*>(&slots.src[sub][k]);
+        src[k] = reinterpret_cast<const float*>(uint64_t(two.x) | (uint64_t(two.y) << 32));
+        src[k + 1] = reinterpret_cast<const float*>(uint64_t(two.z) | (uint64_t(two.w) << 32));
+      }
+#pragma unroll
+      for (uint32_t k = 0; k < kHotLoads; k += 4) {
+        const float4 four = *reinterpret_cast<const float4*>(&slots.scale[sub][k]);
+        r.s[k] = four.x; r.s[k + 1] = four.y; r.s[k + 2] = four.z; r.s[k + 3] = four.w;
+      }
+#pragma unroll
+      for (uint32_t k = 0; k < kHotLoads; ++k) r.x[k] = Load4(src[k] + step);
+      const uint32_t wcol = dc.col0 + (dc.col0 + lane < dim ? lane : 0u);
+      const float* row = dc.ok ? T.state + uint64_t(dc.key & row_mask) * dim * 3 + wcol : idle;
+      const uint32_t ms = dc.ok ? dim : 0u;
+      r.wmv[0] = LoadF(row); r.wmv[1] = LoadF(row + ms); r.wmv[2] = LoadF(row + 2 * ms);
+    };
+    auto stage = [&](const HotRows& r, uint32_t j) {
+      const uint32_t t = j % kHotRing;
+      if (!stalled && !WaitCounter(&s_used[t], j / kHotRing, 1)) stalled = true;
+      // Load k writes (column 4*quad + i, reference 4k + sub) = TileAt(): the
+      // reference group k is rotated by the column's quarter quad / 4.
+      float* tile = s_tile[t] + 4 * quad * kHotPitch + sub;
+      if (r.c.cbase + kHotChunk <= r.c.end) {  // every reference inside the row
+#pragma unroll
+        for (uint32_t k = 0; k < kHotLoads; ++k) {
+          const float sv = r.s[k];
+          float* q = tile + 4u * (k ^ (quad >> 2));
+          q[0] = r.x[k].x * sv;
+          q[kHotPitch] = r.x[k].y * sv;
+          q[2 * kHotPitch] = r.x[k].z * sv;
+          q[3 * kHotPitch] = r.x[k].w * sv;
+        }
+      } else {  // references past the row's end add -0.0f, the identity
+#pragma unroll
+        for (uint32_t k = 0; k < kHotLoads; ++k) {
+          const bool in = r.c.cbase + kHotRefsPerLoad * k + sub < r.c.end;
+          const float sv = r.s[k];
+          float* q = tile + 4u * (k ^ (quad >> 2));
+          q[0] = in ? r.x[k].x * sv : -0.f;
+          q[kHotPitch] = in ? r.x[k].y * sv : -0.f;
+          q[2 * kHotPitch] = in ? r.x[k].z * sv : -0.f;
+          q[3 * kHotPitch] = in ? r.x[k].w * sv : -0.f;
         }
       }
-      acc = 0.f;
+      s_wmv[t][0][lane] = r.wmv[0];
+      s_wmv[t][1][lane] = r.wmv[1];
+      s_wmv[t][2][lane] = r.wmv[2];
+      PostCounter(&s_ready[t], j / kHotRing + 1);
+    };
+    HotRows ra, rb;
+    advance(p);
+    load_words();
+    decode();
+    advance(kProducers);
+    load_words();
+    load_rows(ra);
+    decode();
+    advance(kProducers);
+    load_words();
+    load_rows(rb);
+    // Own chunk o (chunk j = p + kProducers*o): stage rows(o) from buffer
+    // o % 2, decode words(o + 2), load words(o + 3), load rows(o + 2) into
+    // buffer o % 2.  Two own chunks per pass keep the buffers static.
+    auto own = [&](HotRows& r, uint32_t j) {
+      stage(r, j);
+      decode();
+      advance(kProducers);
+      load_words();
+      load_rows(r);
+    };
+    uint32_t j = p;
+    for (; j + kProducers < total; j += 2 * kProducers) {  // one exit: both halves always run
+      own(ra, j);
+      own(rb, j + kProducers);
     }
-    if (r_first) {
-#pragma unroll
-      for (uint32_t k = 0; k < 3; ++k) wmv_p[k] = wmv_r[k];
-    }
-    cp = cr;
-    cr = cw;
-    in_p = in_r;
-#pragma unroll
-    for (uint32_t k = 0; k < kStageLoads; ++k) sc_p[k] = sc_r[k];
+    if (j < total) stage(ra, j);
   }
-  FinishBlock(st, ctrl, a.bounds, write);
+  if (stalled) st.err |= EPS_HIP_STATUS_STALLED;
+  FinishBlock<kHotBlock / kWave>(st, ctrl, a.bounds, write);
 }
 
 template <uint32_t kLog2G>
@@ -900,7 +1080,7 @@ uint64_t SpanBlocks(uint64_t count) {
 constexpr int kPrimary = 1, kSecond = 2;
 constexpr uint64_t kVectorGrid = 4096;  // persistent grid cap of the vector kernels
 constexpr uint64_t kSecondGrid = 256;
-constexpr uint64_t kHotGrid = 1024;     // four blocks per CU (four waves per SIMD)
+constexpr uint64_t kHotGrid = 512;      // two blocks per CU (LDS: four 17 KiB tiles per block)
 
 template <uint32_t kLog2G>
 int LaunchRowRun(unsigned grid, const VecArgs& a, hipStream_t s) {
@@ -912,7 +1092,7 @@ int LaunchRowRun(unsigned grid, const VecArgs& a, hipStream_t s) {
 // Hot rows (any vector class) when `hot`, else the other rows of class `cls`.
 int LaunchVectorUpdate(uint32_t cls, bool hot, unsigned grid, const VecArgs& a, hipStream_t s) {
   if (hot) {
-    hipLaunchKernelGGL(HotSliceKernel, dim3(grid), dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL(HotSliceKernel, dim3(grid), dim3(kHotBlock), 0, s, a);
     EPS_HIP_LAUNCHED("hot row update");
     return EPS_HIP_OK;
   }
@@ -963,13 +1143,17 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
     va.ctrl = a.ctrl;
     va.bounds = bounds;
     va.row_bits = plan.row_bits;
-    va.slices = 1;
+    // Units per hot row: the widest vector table's slices, rounded up to a
+    // power of two (units past a row's dimension are skipped in the kernel).
+    uint32_t slices = 1;
     for (uint32_t t = 0; t < table_count; ++t)
       if (DimClass(tables[t].dim) < kClasses - 1)
-        va.slices = std::max(va.slices, (tables[t].dim + kSlice - 1) / kSlice);
+        slices = std::max(slices, (tables[t].dim + kSlice - 1) / kSlice);
+    va.slice_bits = 0;
+    while ((1u << va.slice_bits) < slices) ++va.slice_bits;
     uint64_t vector_occurrences = 0;
     for (uint32_t cls = 0; cls + 1 < kClasses; ++cls) vector_occurrences += plan.class_occurrences[cls];
-    const uint64_t hot_units = (vector_occurrences / (kLongRefs + 1)) * va.slices;
+    const uint64_t hot_units = (vector_occurrences / (kLongRefs + 1)) << va.slice_bits;
     for (int phase = kPrimary; phase <= kSecond; phase <<= 1) {
       if (!(phases & phase)) continue;
       va.fallback = phase == kSecond;
@@ -982,7 +1166,7 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
       // two run at full occupancy one after the other (side by side they
       // compete for the same registers and bandwidth and finish later).
       if (hot_units) {
-        const uint64_t blocks = xcd_grid(std::min<uint64_t>((hot_units + 3) / 4, std::min(cap, kHotGrid)));
+        const uint64_t blocks = xcd_grid(std::min<uint64_t>(hot_units, std::min(cap, kHotGrid)));
         EPS_HIP_TRY(LaunchVectorUpdate(0, true, unsigned(blocks), va, s));
       }
       for (uint32_t cls = 0; cls + 1 < kClasses; ++cls) {

@@ -25,13 +25,13 @@ constexpr uint32_t kKeygenItems = 4;      // occurrences per keygen thread
 constexpr uint32_t kClasses = 6;          // 5 vector widths + generic
 constexpr uint32_t kRefRowBits = 27;      // gradient row bits in a reference word
 constexpr uint32_t kLongRefs = 128;       // rows with more references take the sliced path
-constexpr uint32_t kSlice = 4;            // columns per sliced-path work unit
+constexpr uint32_t kSlice = 64;           // columns per hot-row work unit
 
 constexpr uint32_t kSrcSlots = 64;        // spread of the gradient/scale maximum atomics
 constexpr uint32_t kHistCopies = 16;      // spread of the keygen histogram atomics
 constexpr uint32_t kXcds = 8;             // XCDs of an MI355X
 constexpr uint32_t kHotBuckets = 4;       // hot-row lists per XCD, by length (longest first)
-constexpr uint32_t kHotChunk = 128;       // references per chunk of the hot-row kernel
+constexpr uint32_t kHotChunk = 64;        // references per chunk of the hot-row kernel
 
 // Control block at offset 0 of a push or update workspace (1 KiB).  Values
 // that many blocks update are kept in several copies (slots) written round

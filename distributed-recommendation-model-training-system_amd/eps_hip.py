@@ -28,8 +28,9 @@ STATUS_NONFINITE_GRAD = 0x2
 STATUS_REDUCE_OVERFLOW = 0x4
 STATUS_ADAM_OVERFLOW = 0x8
 STATUS_REJECTED = 0x10
+STATUS_STALLED = 0x20
 STATUS_CHECKED_PATH = 0x100
-STATUS_ERRORS = 0xF
+STATUS_ERRORS = 0xF | STATUS_STALLED
 MAX_FEATURES = 32
 MAX_TABLES = 32
 MAX_GATHER_PARTS = 32

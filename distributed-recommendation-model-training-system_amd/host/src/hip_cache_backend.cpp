@@ -396,6 +396,8 @@ struct HipCacheBackend::Impl {
     Require((status & (EPS_HIP_STATUS_BAD_INDEX | EPS_HIP_STATUS_NONFINITE_GRAD |
                        EPS_HIP_STATUS_REDUCE_OVERFLOW | EPS_HIP_STATUS_ADAM_OVERFLOW)) == 0,
             "HIP optimizer state would overflow");
+    Require((status & EPS_HIP_STATUS_STALLED) == 0, "HIP hot-row update did not complete",
+            Error::Code::run_failed);
     for (const auto& row : rows) ++t.rows.at(row.key).updates;
   }
 

@@ -53,6 +53,7 @@ extern "C" {
 #define EPS_HIP_STATUS_REDUCE_OVERFLOW 0x4u  /* batch_access.cpp:95 */
 #define EPS_HIP_STATUS_ADAM_OVERFLOW 0x8u    /* lazy_adam.cpp:19-20 */
 #define EPS_HIP_STATUS_REJECTED 0x10u        /* nothing was written */
+#define EPS_HIP_STATUS_STALLED 0x20u         /* internal: a hot-row hand-over timed out */
 #define EPS_HIP_STATUS_CHECKED_PATH 0x100u   /* info: the two-pass path ran */
 
 /* Per-launch limits (descriptors travel as kernel arguments). */
