@@ -270,7 +270,7 @@ struct FusedArgs {
   uint64_t reduce_stride;
   Control* ctrl;
   Bounds* bounds;
-  uint32_t row_bits, cls, log2g, ppb, vblocks, fallback, reduce, tables;
+  uint32_t row_bits, cls, cls_end, log2g, ppb, vblocks, fallback, reduce, tables;  // classes [cls, cls_end)
 };
 
 template <bool kGeneric>
@@ -299,7 +299,7 @@ __global__ void __launch_bounds__(kBlock) SortedUpdateKernel(FusedArgs a) {
     write = true;
   }
   const uint32_t start = ctrl->class_start[a.cls];
-  const uint32_t end = ctrl->class_start[a.cls + 1];
+  const uint32_t end = ctrl->class_start[a.cls_end];
   const uint32_t G = kGeneric ? kWave : (1u << a.log2g);
   const uint32_t lig = threadIdx.x & (G - 1);
   const uint32_t gid = threadIdx.x / G, ngroups = kBlock / G;
@@ -1079,7 +1079,7 @@ uint64_t SpanBlocks(uint64_t count) {
 
 constexpr int kPrimary = 1, kSecond = 2;
 constexpr uint64_t kVectorGrid = 4096;  // persistent grid cap of the vector kernels
-constexpr uint64_t kSecondGrid = 256;
+constexpr uint64_t kSecondGrid = 256;     // grid cap of the checked apply (usually exits at once)
 constexpr uint64_t kHotGrid = 512;      // two blocks per CU (LDS: four 17 KiB tiles per block)
 
 template <uint32_t kLog2G>
@@ -1154,26 +1154,23 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
     uint64_t vector_occurrences = 0;
     for (uint32_t cls = 0; cls + 1 < kClasses; ++cls) vector_occurrences += plan.class_occurrences[cls];
     const uint64_t hot_units = (vector_occurrences / (kLongRefs + 1)) << va.slice_bits;
-    for (int phase = kPrimary; phase <= kSecond; phase <<= 1) {
-      if (!(phases & phase)) continue;
-      va.fallback = phase == kSecond;
-      // The checked apply runs only after a validate-only pass; its launches
-      // usually exit at once, so they get small grids.
-      const uint64_t cap = phase == kSecond ? kSecondGrid : kVectorGrid;
+    if (phases & kPrimary) {
+      va.fallback = 0;
       // Grids are multiples of kXcds (the kernels split their work by XCD).
       auto xcd_grid = [](uint64_t b) { return (b + kXcds - 1) / kXcds * kXcds; };
       // Hot rows first, then the row runs of each class, in stream order: the
       // two run at full occupancy one after the other (side by side they
       // compete for the same registers and bandwidth and finish later).
       if (hot_units) {
-        const uint64_t blocks = xcd_grid(std::min<uint64_t>(hot_units, std::min(cap, kHotGrid)));
+        const uint64_t blocks = xcd_grid(std::min<uint64_t>(hot_units, kHotGrid));
         EPS_HIP_TRY(LaunchVectorUpdate(0, true, unsigned(blocks), va, s));
       }
       for (uint32_t cls = 0; cls + 1 < kClasses; ++cls) {
         if (!plan.class_occurrences[cls]) continue;
         va.cls = cls;
         const uint64_t blocks = xcd_grid(std::min<uint64_t>(
-            std::max<uint64_t>(1, (plan.class_occurrences[cls] + kRunPositions - 1) / kRunPositions), cap));
+            std::max<uint64_t>(1, (plan.class_occurrences[cls] + kRunPositions - 1) / kRunPositions),
+            kVectorGrid));
         EPS_HIP_TRY(LaunchVectorUpdate(cls, false, unsigned(blocks), va, s));
       }
     }
@@ -1182,6 +1179,7 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
     if (!plan.class_occurrences[cls]) continue;
     if (!reduce && cls + 1 < kClasses) continue;  // handled above
     a.cls = cls;
+    a.cls_end = cls + 1;
     a.log2g = cls + 2;
     a.ppb = PositionsPerBlock(cls);
     const uint64_t vb = (plan.class_occurrences[cls] + a.ppb - 1) / a.ppb;
@@ -1192,10 +1190,19 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
       hipLaunchKernelGGL(kernel, dim3(a.vblocks), dim3(kBlock), 0, s, a);
       EPS_HIP_LAUNCHED("sorted update");
     }
-    if (!reduce && (phases & kSecond)) {
-      a.fallback = 1;
-      hipLaunchKernelGGL(kernel, dim3(std::min<uint32_t>(a.vblocks, kFallbackGrid)), dim3(kBlock), 0,
-                         s, a);
+  }
+  // The checked apply (after a validate-only pass) is one launch over every
+  // class, one wavefront per row: it usually exits at once, and when it runs
+  // it adds each row's references in the same order as the passes above.
+  if (!reduce && (phases & kSecond)) {
+    a.cls = 0;
+    a.cls_end = kClasses;
+    a.ppb = PositionsPerBlock(kClasses - 1);
+    a.vblocks = uint32_t((plan.occurrences + a.ppb - 1) / a.ppb);
+    a.fallback = 1;
+    if (a.vblocks) {
+      hipLaunchKernelGGL(SortedUpdateKernel<true>, dim3(std::min<uint32_t>(a.vblocks, kSecondGrid)),
+                         dim3(kBlock), 0, s, a);
       EPS_HIP_LAUNCHED("sorted update (checked apply)");
     }
   }
