@@ -425,7 +425,8 @@ constexpr uint32_t kHotRefsPerLoad = kWave / kHotQuads;   // references per row 
 constexpr uint32_t kHotLoads = kHotChunk / kHotRefsPerLoad;  // row loads per producer lane per chunk
 constexpr uint32_t kProducers = kHotBlock / kWave - 1;
 static_assert(kSlice == kWave && kHotChunk == kWave && kHotQuads == 16, "hot-row tile shape");
-constexpr uint32_t kRunPositions = 128;
+constexpr uint32_t kRunPositions = 256;
+static_assert(kRunPositions <= kBlock, "one thread per staged position finds the row heads");
 constexpr uint32_t kRefBatch = 4;                       // gradient rows in flight per group
 
 struct VecArgs {

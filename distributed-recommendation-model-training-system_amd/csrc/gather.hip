@@ -29,7 +29,7 @@ int Check(hipError_t e, const char* what) {
 
 namespace {
 
-constexpr uint32_t kIdCap = 2048;     // occurrences staged in LDS per tile
+constexpr uint32_t kIdCap = 1024;     // occurrences staged in LDS per tile (LDS sets the occupancy)
 constexpr uint32_t kGatherBatch = 8;  // source rows in flight per lane group
 constexpr uint32_t kGenericLog2 = 0xff;
 
