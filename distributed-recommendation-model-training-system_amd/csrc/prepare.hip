@@ -207,11 +207,10 @@ __device__ __forceinline__ uint32_t BlockExclusiveScan(uint32_t x, uint32_t* s_w
   return before + inc - x;
 }
 
-template <bool kLast>
 __global__ void __launch_bounds__(kBlock) RadixPassKernel(
     const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
     uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out,
-    const uint64_t* __restrict__ refscale, uint64_t* __restrict__ sorted_rs, uint32_t n,
+    const uint64_t* __restrict__ rs_in, uint64_t* __restrict__ rs_out, uint32_t n,
     uint32_t shift, uint32_t bits, const uint32_t* __restrict__ hist, uint32_t* look,
     uint32_t* tile_counter) {
   __shared__ uint32_t s_tile;
@@ -221,6 +220,7 @@ __global__ void __launch_bounds__(kBlock) RadixPassKernel(
   __shared__ uint32_t s_scan[4];
   __shared__ uint32_t s_keys[kSortTile];
   __shared__ uint32_t s_vals[kSortTile];
+  __shared__ uint64_t s_rs[kSortTile];
 
   const uint32_t t = threadIdx.x, lane = t & (kWave - 1), wave = t / kWave;
   if (t == 0) s_tile = atomicAdd(tile_counter, 1u);
@@ -238,11 +238,13 @@ __global__ void __launch_bounds__(kBlock) RadixPassKernel(
   const uint32_t mask = (1u << bits) - 1;
   const uint32_t base = tile * kSortTile + wave * (kSortTile / 4);
   uint32_t key[kSortItems], val[kSortItems], rank[kSortItems];
+  uint64_t rs[kSortItems];
 #pragma unroll
   for (uint32_t i = 0; i < kSortItems; ++i) {
     const uint32_t p = base + i * kWave + lane;
     key[i] = p < n ? keys_in[p] : 0u;
     val[i] = p < n ? vals_in[p] : 0u;
+    rs[i] = p < n ? rs_in[p] : 0ull;
   }
   const uint64_t lt_mask = (1ull << lane) - 1;
 #pragma unroll
@@ -352,13 +354,14 @@ __global__ void __launch_bounds__(kBlock) RadixPassKernel(
       const uint32_t at = s_tile_start[digit] + s_wcount[wave][digit] + rank[i];
       s_keys[at] = key[i];
       s_vals[at] = val[i];
+      s_rs[at] = rs[i];
     }
   }
   __syncthreads();
-  // Scatter of the digit-sorted tile: all LDS reads, then (last pass) all
-  // reference-word gathers, then the stores, so no item waits on another's
-  // round trip.  Entries past the tile's end read stale LDS (in bounds) and
-  // are neither gathered nor stored.
+  // Scatter of the digit-sorted tile: all LDS reads, then the stores.  The
+  // reference words travel with their keys through every pass, so the last
+  // pass needs no gather by occurrence index.  Entries past the tile's end
+  // read stale LDS (in bounds) and are not stored.
   const uint32_t tile_n = min(kSortTile, n - tile * kSortTile);
   uint32_t dest[kSortItems];
 #pragma unroll
@@ -366,20 +369,16 @@ __global__ void __launch_bounds__(kBlock) RadixPassKernel(
     const uint32_t q = i * kBlock + t;
     key[i] = s_keys[q];
     val[i] = s_vals[q];
+    rs[i] = s_rs[q];
     const uint32_t digit = (key[i] >> shift) & mask;
     dest[i] = s_global[digit] + (q - s_tile_start[digit]);
-  }
-  uint64_t rs[kSortItems];
-  if (kLast) {
-#pragma unroll
-    for (uint32_t i = 0; i < kSortItems; ++i) rs[i] = refscale[i * kBlock + t < tile_n ? val[i] : 0u];
   }
 #pragma unroll
   for (uint32_t i = 0; i < kSortItems; ++i) {
     if (i * kBlock + t < tile_n) {
       keys_out[dest[i]] = key[i];
       vals_out[dest[i]] = val[i];
-      if (kLast) sorted_rs[dest[i]] = rs[i];
+      rs_out[dest[i]] = rs[i];
     }
   }
 }
@@ -651,7 +650,12 @@ int eps_hip_prepare(const eps_hip_table* tables, uint32_t table_count,
   args.hist = reinterpret_cast<uint32_t*>(ws + L.hist);
   args.keys = reinterpret_cast<uint32_t*>(ws + L.keys_a);
   args.vals = reinterpret_cast<uint32_t*>(ws + L.vals_a);
-  args.refscale = reinterpret_cast<uint64_t*>(ws + L.refscale);
+  // Reference words ping-pong between two buffers through the passes and
+  // end in sorted_rs: keygen writes them where an even number of swaps
+  // before the end starts.
+  uint64_t* rs[2] = {reinterpret_cast<uint64_t*>(ws + (plan.passes % 2 ? L.refscale : L.sorted_rs)),
+                     reinterpret_cast<uint64_t*>(ws + (plan.passes % 2 ? L.sorted_rs : L.refscale))};
+  args.refscale = rs[0];
   uint64_t occ = 0, blocks = 0;
   for (uint32_t i = 0; i < feature_count; ++i) {
     const auto& in = features[i];
@@ -672,12 +676,9 @@ int eps_hip_prepare(const eps_hip_table* tables, uint32_t table_count,
   auto* look = reinterpret_cast<uint32_t*>(ws + L.look);
   const uint32_t n = uint32_t(plan.occurrences);
   for (uint32_t p = 0; p < plan.passes; ++p) {
-    const bool last = p + 1 == plan.passes;
-    auto kernel = last ? RadixPassKernel<true> : RadixPassKernel<false>;
-    hipLaunchKernelGGL(kernel, dim3(unsigned(L.tiles)), dim3(kBlock), 0, s, keys[p % 2], vals[p % 2],
-                       keys[(p + 1) % 2], vals[(p + 1) % 2],
-                       reinterpret_cast<const uint64_t*>(ws + L.refscale),
-                       reinterpret_cast<uint64_t*>(ws + L.sorted_rs), n, plan.shift[p], plan.bits[p],
+    hipLaunchKernelGGL(RadixPassKernel, dim3(unsigned(L.tiles)), dim3(kBlock), 0, s, keys[p % 2], vals[p % 2],
+                       keys[(p + 1) % 2], vals[(p + 1) % 2], rs[p % 2], rs[(p + 1) % 2], n,
+                       plan.shift[p], plan.bits[p],
                        args.hist + p * kDigits, look + uint64_t(p) * L.tiles * kDigits,
                        &ctrl->tile_counter[p]);
     EPS_HIP_LAUNCHED("radix pass");
