@@ -836,8 +836,11 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
   FinishBlock<kHotBlock / kWave>(st, ctrl, a.bounds, write);
 }
 
+// Seven waves per SIMD (72 registers) where that needs no spill: more rows'
+// loads in flight per CU.
 template <uint32_t kLog2G>
-__global__ void __launch_bounds__(kBlock) RowRunKernel(VecArgs a) {
+__global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kLog2G == 2 || kLog2G == 6 ? 6 : 7)))
+RowRunKernel(VecArgs a) {
   constexpr uint32_t G = 1u << kLog2G;
   constexpr uint32_t ngroups = kBlock / G;
   constexpr uint32_t kStaged = kRunPositions + kLongRefs;
