@@ -56,6 +56,20 @@ class HipCacheBackend final : public GpuCacheAgent {
   std::future<Result<HipMemoryStats>> MemoryStats();
   std::future<Result<std::vector<DeviceTensorBlock>>> AssembleFeatures(DeviceAssemblyRequest);
 
+  // Device-resident push of this agent's rows: per-feature gradients that are
+  // already on this device ((bags, or occurrences for a sequence feature) x
+  // dimension, matched to the work by feature id), with the lookup's work and
+  // layouts and one UpdateContext per table.  Duplicate ids are aggregated in
+  // (feature, bag, position) order and LazyAdam is applied once per unique
+  // row, all on the device and all-or-nothing over the call.  The reference
+  // has no device entry for this: it copies device gradients to the host
+  // (adapters/entropy/runtime_c.cpp:200-204), reduces them there
+  // (src/access/batch_access.cpp:54-97) and applies each table's rows through
+  // ApplyHost (src/cuda/cache_backend.cu:501-513); the results are the same.
+  std::future<Result<Ack>> PushDevice(std::vector<UpdateContext> contexts, std::vector<AgentWork> work,
+                                      std::vector<FeatureInput> layouts,
+                                      std::vector<DeviceTensorBlock> gradients);
+
  private:
   struct Impl;
   std::unique_ptr<Impl> impl_;

@@ -11,6 +11,7 @@
 //   Load / ReadBack           -> eps_hip_scatter_rows / eps_hip_gather_rows
 //   AssembleFeatures          -> eps_hip_fill_u32, eps_hip_add_contribution,
 //                                eps_hip_normalize_mean
+//   PushDevice                -> eps_hip_prepare + eps_hip_push (device gradients)
 // Occurrence slots are resolved once per unique row (the reference looks the
 // row up in a hash map once per occurrence, src/cuda/cache_backend.cu:279-291).
 #include "eps/hip_cache_backend.hpp"
@@ -360,18 +361,25 @@ struct HipCacheBackend::Impl {
   }
 
   // src/cuda/cache_backend.cu:321-333.
-  Table& ValidateUpdate(const UpdateContext& c, const std::vector<RowKey>& rows) {
+  Table& CheckContext(const UpdateContext& c) {
     Table& t = Get(c.table);
     Require(std::isfinite(c.learning_rate) && c.learning_rate > 0 && c.beta1_power >= 0 &&
                 c.beta1_power < 1 && c.beta2_power >= 0 && c.beta2_power < 1,
             "invalid HIP update context");
+    return t;
+  }
+  static void CheckOwner(const UpdateContext& c, const Entry& e) {
+    Require(e.location.home == c.shard && e.updates != UINT64_MAX, "invalid HIP gradient owner/counter");
+  }
+  Table& ValidateUpdate(const UpdateContext& c, const std::vector<RowKey>& rows) {
+    Table& t = CheckContext(c);
     Limit(rows.size() * std::uint64_t(t.definition.dimension) * 4);
     std::set<Key> unique;
     for (const auto& row : rows) {
       auto it = t.rows.find(row.key);
-      Require(row.table == c.table && unique.insert(row.key).second && it != t.rows.end() &&
-                  it->second.location.home == c.shard && it->second.updates != UINT64_MAX,
+      Require(row.table == c.table && unique.insert(row.key).second && it != t.rows.end(),
               "invalid HIP gradient owner/counter");
+      CheckOwner(c, it->second);
     }
     return t;
   }
@@ -390,22 +398,36 @@ struct HipCacheBackend::Impl {
     return opt;
   }
   // All-or-nothing: the device status says whether anything was written.
-  void FinishUpdate(Table& t, const std::vector<RowKey>& rows) {
+  void CheckStatus(void* ws) {
     uint32_t status = 0;
-    Abi(eps_hip_read_status(workspace.pointer, &status, stream.value));
-    Require((status & (EPS_HIP_STATUS_BAD_INDEX | EPS_HIP_STATUS_NONFINITE_GRAD |
-                       EPS_HIP_STATUS_REDUCE_OVERFLOW | EPS_HIP_STATUS_ADAM_OVERFLOW)) == 0,
+    Abi(eps_hip_read_status(ws, &status, stream.value));
+    Require((status & EPS_HIP_STATUS_NONFINITE_GRAD) == 0, "non-finite gradient");
+    Require((status & EPS_HIP_STATUS_REDUCE_OVERFLOW) == 0, "gradient reduction overflow");
+    Require((status & (EPS_HIP_STATUS_BAD_INDEX | EPS_HIP_STATUS_ADAM_OVERFLOW)) == 0,
             "HIP optimizer state would overflow");
     Require((status & EPS_HIP_STATUS_STALLED) == 0, "HIP hot-row update did not complete",
             Error::Code::run_failed);
+  }
+  void FinishUpdate(Table& t, const std::vector<RowKey>& rows) {
+    CheckStatus(workspace.pointer);
     for (const auto& row : rows) ++t.rows.at(row.key).updates;
+  }
+  // The device push workspace grows to the largest call seen (the stream is
+  // idle between operations, so the old one can go).
+  void ReservePush(std::uint64_t bytes) {
+    if (bytes <= push_bytes) return;
+    push_workspace.Reset();
+    push_bytes = 0;
+    push_workspace.Allocate(bytes, options.device);
+    push_bytes = bytes;
   }
 
   HipCacheOptions options;
   Stream stream;
   Event done;
   Memory host_values, host_indices, device_values, device_indices, device_transient, workspace,
-      bounds, gather_status;
+      bounds, gather_status, push_workspace;
+  std::uint64_t push_bytes = 0;
   std::map<TableId, std::unique_ptr<Table>> tables;
   std::uint64_t allocated_state = 0;
   std::shared_ptr<OutputBudget> output_budget;
@@ -863,13 +885,159 @@ std::future<Result<std::vector<DeviceTensorBlock>>> HipCacheBackend::AssembleFea
   });
 }
 
+// Device-resident push.  Host work is the slot translation of the lookup's
+// occurrence maps (once per unique row, as in PrepareGather) and the owner and
+// counter checks of ValidateUpdate (src/cuda/cache_backend.cu:321-333); the
+// gradients never leave the device.  eps_hip_prepare sorts the occurrences by
+// (table, slot) and eps_hip_push runs ReduceGradients
+// (src/access/batch_access.cpp:54-97: non-finite inputs rejected, scale
+// 1/valid_length for mean, sums in (feature, bag, position) order, overflow of
+// a sum rejected) fused with LazyAdam (src/update/lazy_adam.cpp:7-42), writing
+// nothing unless the whole call is valid.
+std::future<Result<Ack>> HipCacheBackend::PushDevice(std::vector<UpdateContext> contexts,
+                                                     std::vector<AgentWork> work,
+                                                     std::vector<FeatureInput> layouts,
+                                                     std::vector<DeviceTensorBlock> gradients) {
+  return impl_->worker->Submit<Ack>([this, contexts = std::move(contexts), work = std::move(work),
+                                     layouts = std::move(layouts), gradients = std::move(gradients)] {
+    Impl& I = *impl_;
+    I.Activate();
+    struct PushTable {
+      Impl::Table* table;
+      const UpdateContext* context;
+      std::uint32_t index;
+      std::vector<Key> rows;  // unique rows touched, first-touch order
+      std::unordered_map<Key, std::uint64_t> slots;
+    };
+    std::map<TableId, PushTable> tables;
+    for (const auto& c : contexts) {
+      Impl::Table& t = I.CheckContext(c);
+      Require(tables.emplace(c.table, PushTable{&t, &c, UINT32_MAX, {}, {}}).second,
+              "duplicate HIP update context");
+    }
+    std::map<std::uint32_t, const DeviceTensorBlock*> gradient_of;
+    for (const auto& g : gradients)
+      Require(gradient_of.emplace(g.feature, &g).second, "duplicate gradient feature");
+    Require(gradients.size() == work.size(), "gradient feature count mismatch");
+    Require(work.size() <= EPS_HIP_MAX_FEATURES, "too many features for one HIP push",
+            Error::Code::capacity_exceeded);
+    struct Part {
+      PushTable* table;
+      const FeatureInput* layout;
+      const DeviceTensor* gradient;
+      std::uint64_t slots, offsets, lengths;
+    };
+    std::vector<Part> parts;
+    parts.reserve(work.size());
+    auto* index = I.host_indices.As<std::uint64_t>();
+    std::uint64_t used = 0, occurrences = 0;
+    std::uint32_t table_count = 0;
+    for (const auto& task : work) {
+      auto it = std::find_if(layouts.begin(), layouts.end(),
+                             [&](const FeatureInput& f) { return f.feature == task.feature; });
+      Require(it != layouts.end() && task.agent == I.options.agent &&
+                  task.route == AccessRoute::resident_gpu && task.transferred_weights.empty(),
+              "invalid HIP push work");
+      const FeatureInput& f = *it;
+      auto pt = tables.find(f.table);
+      Require(pt != tables.end(), "missing HIP update context");
+      PushTable& target = pt->second;
+      const std::uint64_t dim = target.table->definition.dimension;
+      Require(task.occurrence_to_unique.size() == f.keys.size() && !f.offsets.empty() &&
+                  f.offsets.front() == 0 && f.offsets.back() == f.keys.size() &&
+                  std::is_sorted(f.offsets.begin(), f.offsets.end()) &&
+                  f.valid_lengths.size() + 1 == f.offsets.size(),
+              "invalid HIP push layout");
+      auto g = gradient_of.find(f.feature);
+      Require(g != gradient_of.end(), "missing feature gradient");
+      const DeviceTensorBlock& block = *g->second;
+      const std::uint64_t rows = f.pooling == Pooling::sequence ? f.keys.size() : f.valid_lengths.size();
+      Require(block.tensor && block.shape == std::vector<std::uint64_t>{rows, dim} &&
+                  block.tensor->elements() == rows * dim && block.tensor->device() == I.options.device &&
+                  (rows == 0 || block.tensor->data() != nullptr),
+              "gradient tensor layout mismatch");
+      I.Limit((used + f.keys.size() + f.offsets.size() + f.valid_lengths.size()) * 8);
+      if (target.index == UINT32_MAX) target.index = table_count++;
+      Part part{&target, &f, block.tensor.get(), used, 0, 0};
+      constexpr std::uint64_t kUnresolved = std::numeric_limits<std::uint64_t>::max() - 1;
+      std::vector<std::uint64_t> slot_of(task.rows.size(), kUnresolved);
+      for (std::size_t i = 0; i < f.keys.size(); ++i) {
+        const std::uint64_t unique = task.occurrence_to_unique[i];
+        if (unique == UINT64_MAX) {
+          index[used++] = UINT64_MAX;
+          continue;
+        }
+        Require(unique < task.rows.size() && task.rows[unique].row == RowKey{f.table, f.keys[i]},
+                "invalid HIP occurrence map");
+        if (slot_of[unique] == kUnresolved) {
+          const Impl::Entry& e = I.Find(task.rows[unique]);
+          Impl::CheckOwner(*target.context, e);
+          slot_of[unique] = e.location.slot;
+          if (target.slots.emplace(f.keys[i], e.location.slot).second) target.rows.push_back(f.keys[i]);
+        }
+        index[used++] = slot_of[unique];
+      }
+      occurrences += f.keys.size();
+      part.offsets = used;
+      std::copy(f.offsets.begin(), f.offsets.end(), index + used);
+      used += f.offsets.size();
+      part.lengths = used;
+      std::copy(f.valid_lengths.begin(), f.valid_lengths.end(), index + used);
+      used += f.valid_lengths.size();
+      parts.push_back(part);
+    }
+    if (!occurrences) return Ack{};
+    std::vector<eps_hip_table> abi_tables(table_count);
+    std::vector<eps_hip_optimizer> optimizers(table_count);
+    for (auto& [id, t] : tables) {
+      if (t.index == UINT32_MAX) continue;
+      abi_tables[t.index] = t.table->abi;
+      optimizers[t.index] = I.Optimizer(*t.table, *t.context);
+    }
+    const std::uint64_t bytes = eps_hip_push_workspace_bytes(occurrences);
+    I.ReservePush(bytes);
+    hipStream_t s = I.stream.value;
+    try {
+      I.CopyIn(I.device_indices.pointer, I.host_indices.pointer, used * 8);
+      const auto* device = I.device_indices.As<std::uint64_t>();
+      std::vector<eps_hip_push_feature> features;
+      features.reserve(parts.size());
+      for (const auto& p : parts) {
+        p.gradient->WaitOnStream(s);
+        const FeatureInput& f = *p.layout;
+        eps_hip_push_feature x{};
+        x.indices = device + p.slots;
+        x.offsets = device + p.offsets;
+        x.valid_lengths = f.pooling == Pooling::mean ? device + p.lengths : nullptr;
+        x.gradients = static_cast<const float*>(p.gradient->data());
+        x.occurrences = f.keys.size();
+        x.bags = f.valid_lengths.size();
+        x.table = p.table->index;
+        x.pooling = PoolingCode(f.pooling);
+        features.push_back(x);
+      }
+      Abi(eps_hip_prepare(abi_tables.data(), table_count, features.data(), std::uint32_t(features.size()),
+                          I.push_workspace.pointer, bytes, s));
+      Abi(eps_hip_push(abi_tables.data(), optimizers.data(), table_count, features.data(),
+                       std::uint32_t(features.size()), I.push_workspace.pointer, bytes, I.bounds.pointer, s));
+      I.CheckStatus(I.push_workspace.pointer);
+    } catch (...) {
+      (void)hipStreamSynchronize(s);
+      throw;
+    }
+    for (auto& [id, t] : tables)
+      for (Key key : t.rows) ++t.table->rows.at(key).updates;
+    return Ack{};
+  });
+}
+
 std::future<Result<HipMemoryStats>> HipCacheBackend::MemoryStats() {
   return impl_->worker->Submit<HipMemoryStats>([this] {
     std::uint64_t state = 0;
     for (const auto& [id, table] : impl_->tables)
       state += impl_->options.rows_per_table * std::uint64_t(table->definition.dimension) * 12;
     const std::uint64_t staging = impl_->options.transfer_bytes * 3 + eps_hip_update_workspace_bytes() +
-                                  eps_hip_bounds_bytes() + 256;
+                                  eps_hip_bounds_bytes() + 256 + impl_->push_bytes;
     return HipMemoryStats{state, staging, impl_->output_budget->used.load(),
                           impl_->output_budget->allocations.load()};
   });

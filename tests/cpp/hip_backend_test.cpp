@@ -7,7 +7,8 @@
 // two ApplyCompact steps on a bounded table (clipping exercised); overflow
 // rejection that leaves every row untouched; slot reclamation and stale
 // generations after reuse; the atomic slot reserve of concurrent loads; plus
-// device feature assembly (tests/device_pull_tests.cpp's ReferenceAssembly).
+// device feature assembly (tests/device_pull_tests.cpp's ReferenceAssembly);
+// and the device-resident push (ReduceGradients + LazyAdam on the device).
 // Expected values come from the oracle (oracle/eps_oracle.h, the CPU
 // restatement of the reference shard) and are compared bit for bit.
 #include <algorithm>
@@ -19,6 +20,8 @@
 #include <stdexcept>
 #include <string>
 #include <vector>
+
+#include <hip/hip_runtime_api.h>
 
 #include "eps/hip_cache_backend.hpp"
 #include "eps_oracle.h"
@@ -159,6 +162,100 @@ void ApplyModel(Model& model, TableId table, const std::vector<Key>& keys, const
   }
 }
 
+// A caller-owned device gradient (the training framework's tensor), written
+// synchronously, so there is nothing to wait for.
+class DeviceBuffer final : public DeviceTensor {
+ public:
+  explicit DeviceBuffer(const std::vector<float>& values) : count_(values.size()) {
+    if (!count_) return;
+    Check(hipMalloc(&pointer_, count_ * 4) == hipSuccess &&
+              hipMemcpy(pointer_, values.data(), count_ * 4, hipMemcpyHostToDevice) == hipSuccess,
+          "device gradient upload");
+  }
+  ~DeviceBuffer() override {
+    if (pointer_) (void)hipFree(pointer_);
+  }
+  void* data() const override { return pointer_; }
+  std::uint64_t elements() const override { return count_; }
+  int device() const override { return 0; }
+  void WaitOnStream(void*) const override {}
+  std::vector<float> CopyToHost() const override {
+    std::vector<float> values(count_);
+    if (count_) Check(hipMemcpy(values.data(), pointer_, count_ * 4, hipMemcpyDeviceToHost) == hipSuccess, "download");
+    return values;
+  }
+
+ private:
+  void* pointer_ = nullptr;
+  std::uint64_t count_;
+};
+
+// Per-feature gradients of the Layouts() lookup: (bags, or keys for the
+// sequence feature) x dimension.
+std::vector<std::vector<float>> PushGradients(const std::vector<FeatureInput>& layouts, int step) {
+  std::vector<std::vector<float>> out;
+  for (const auto& f : layouts) {
+    const std::uint32_t dim = f.table == 1 ? 128 : 64;
+    const std::uint64_t rows = f.pooling == Pooling::sequence ? f.keys.size() : f.valid_lengths.size();
+    std::vector<float> g(rows * dim);
+    for (std::size_t i = 0; i < g.size(); ++i)
+      g[i] = 0.03f * std::sin(float(i * 7 + f.feature * 11 + step * 5)) - 0.004f * float(i % 3);
+    out.push_back(std::move(g));
+  }
+  return out;
+}
+
+std::vector<DeviceTensorBlock> Upload(const std::vector<FeatureInput>& layouts,
+                                      const std::vector<std::vector<float>>& g) {
+  std::vector<DeviceTensorBlock> out;
+  for (std::size_t i = 0; i < layouts.size(); ++i) {
+    const std::uint64_t dim = layouts[i].table == 1 ? 128 : 64;
+    out.push_back({layouts[i].feature, {g[i].size() / dim, dim}, std::make_shared<DeviceBuffer>(g[i])});
+  }
+  return out;
+}
+
+// The reference push of the same gradients: ReduceGradients per table over all
+// of the lookup's features (the hole key 999 is reduced too and then routed
+// elsewhere), LazyAdam on this agent's rows.
+void ApplyPushModel(Model& model, const std::vector<FeatureInput>& layouts,
+                    const std::vector<std::vector<float>>& g, const std::map<TableId, std::pair<float, float>>& powers) {
+  for (const auto& [table, p] : powers) {
+    const std::uint32_t dim = table == 1 ? 128 : 64;
+    eps_or_table_def def{};
+    def.id = table;
+    def.dim = dim;
+    def.shard_count = 1;
+    eps_or_store* store = eps_or_create(&def);
+    std::vector<eps_or_feature> features;
+    std::vector<const float*> grads;
+    std::uint64_t keys = 0;
+    for (std::size_t i = 0; i < layouts.size(); ++i) {
+      const auto& f = layouts[i];
+      if (f.table != table) continue;
+      features.push_back({f.keys.data(), f.keys.size(), f.offsets.data(), f.valid_lengths.data(), nullptr,
+                          f.valid_lengths.size(), uint32_t(f.pooling), f.feature});
+      grads.push_back(g[i].data());
+      keys += f.keys.size();
+    }
+    std::vector<std::uint64_t> row_keys(keys);
+    std::vector<float> values(keys * dim);
+    std::uint64_t count = 0;
+    const int rc = eps_or_reduce_gradients(store, features.data(), grads.data(), uint32_t(features.size()),
+                                           row_keys.data(), values.data(), &count);
+    eps_or_destroy(store);
+    Check(rc == 0, "oracle gradient reduction failed");
+    std::vector<Key> mine;
+    std::vector<float> mine_values;
+    for (std::uint64_t u = 0; u < count; ++u) {
+      if (!model.rows.count({table, row_keys[u]})) continue;  // served by another owner
+      mine.push_back(row_keys[u]);
+      mine_values.insert(mine_values.end(), values.begin() + u * dim, values.begin() + (u + 1) * dim);
+    }
+    ApplyModel(model, table, mine, mine_values, p.first, p.second);
+  }
+}
+
 HipCacheOptions SmallOptions(std::uint64_t rows_per_table) {
   HipCacheOptions o;
   o.rows_per_table = rows_per_table;
@@ -233,6 +330,52 @@ void Assembly(HipCacheBackend& gpu, const std::vector<LocatedRow>& located, cons
   assembled[0].tensor->WaitOnStream(nullptr);
   Check(SameBits(assembled[0].tensor->CopyToHost(), mean), "assembled mean feature");
   Check(SameBits(assembled[1].tensor->CopyToHost(), seq), "assembled projected sequence feature");
+}
+
+// Device-resident push: two steps over both tables (mean with a hole, a
+// sequence, a sum with an empty bag) against the oracle's ReduceGradients +
+// LazyAdam, then rejections that leave every row as it was.
+void DevicePush(HipCacheBackend& gpu, const std::vector<LocatedRow>& located, Model& model,
+                float& b1, float& b2) {
+  const auto layouts = Layouts();
+  const auto work = Work(located);
+  float t2b1 = 0.9f, t2b2 = 0.999f;
+  for (int step = 0; step < 2; ++step) {
+    const auto g = PushGradients(layouts, step);
+    std::vector<UpdateContext> contexts = {{{"hip-push", 0, std::uint64_t(step), Phase::push}, 0, 1, 0, kLr, b1, b2},
+                                           {{"hip-push", 0, std::uint64_t(step), Phase::push}, 0, 2, 0, kLr, t2b1, t2b2}};
+    Take(gpu.PushDevice(contexts, work, layouts, Upload(layouts, g)));
+    ApplyPushModel(model, layouts, g, {{1, {b1, b2}}, {2, {t2b1, t2b2}}});
+    b1 *= 0.9f;
+    b2 *= 0.999f;
+    t2b1 *= 0.9f;
+    t2b2 *= 0.999f;
+    CompareStates(Take(gpu.ReadBack({"read", 0, located, Placement::cpu, 0})), model, "state after device push");
+  }
+  const std::vector<UpdateContext> contexts = {{{"hip-push", 0, 9, Phase::push}, 0, 1, 0, kLr, b1, b2},
+                                               {{"hip-push", 0, 9, Phase::push}, 0, 2, 0, kLr, t2b1, t2b2}};
+  auto g = PushGradients(layouts, 3);
+  g[2][64 + 5] = std::numeric_limits<float>::quiet_NaN();  // the empty bag's gradient row
+  Check(Fails(gpu.PushDevice(contexts, work, layouts, Upload(layouts, g)), "non-finite device gradient") ==
+            Error::Code::invalid_argument,
+        "non-finite gradient code");
+  g = PushGradients(layouts, 3);
+  std::fill(g[1].begin(), g[1].end(), std::numeric_limits<float>::max());
+  Fails(gpu.PushDevice(contexts, work, layouts, Upload(layouts, g)), "overflowing device push");
+  g = PushGradients(layouts, 3);
+  auto short_blocks = Upload(layouts, g);
+  short_blocks[1].shape[0] = 2;
+  Check(Fails(gpu.PushDevice(contexts, work, layouts, short_blocks), "mis-shaped device gradient") ==
+            Error::Code::invalid_argument,
+        "gradient shape code");
+  Fails(gpu.PushDevice({contexts[0]}, work, layouts, Upload(layouts, g)), "push without a table context");
+  auto stale = work;
+  stale[2].rows[0].generation += 1;
+  Check(Fails(gpu.PushDevice(contexts, stale, layouts, Upload(layouts, g)), "stale device push") ==
+            Error::Code::stale_generation,
+        "stale push code");
+  CompareStates(Take(gpu.ReadBack({"read", 0, located, Placement::cpu, 0})), model,
+                "state after rejected device pushes");
 }
 
 void Main() {
@@ -349,6 +492,8 @@ void Main() {
   for (std::size_t i = 0; i < device.size(); ++i)
     Check(SameBits(device[i].tensor->CopyToHost(), before[i].values), "device result changed after updates");
 
+  DevicePush(*gpu, located, model, b1, b2);
+
   Assembly(*gpu, located, model);
   auto stats = Take(gpu->MemoryStats());
   Check(stats.resident_state_bytes == 8ull * (128 + 64) * 12, "resident state bytes");
@@ -374,8 +519,8 @@ int main() {
   try {
     Main();
     std::cout << "PASS HIP backend: " << g_checks
-              << " checks (gathers, optimizer states, atomic rejection, slot reuse, assembly, "
-                 "device-result lifetime)\n";
+              << " checks (gathers, optimizer states, device push, atomic rejection, slot reuse, "
+                 "assembly, device-result lifetime)\n";
     return 0;
   } catch (const std::exception& e) {
     std::cerr << "FAIL HIP backend: " << e.what() << '\n';

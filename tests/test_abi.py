@@ -42,7 +42,8 @@ def test_backend_library_loads(pkg):
     names = subprocess.run(["nm", "-DC", "--defined-only", str(path)], capture_output=True,
                            text=True, check=True).stdout
     for method in ("Define", "FreeSlots", "Load", "GatherHost", "GatherDevice", "ApplyHost",
-                   "ApplyCompact", "ReadBack", "CommitEviction", "MemoryStats", "AssembleFeatures"):
+                   "ApplyCompact", "ReadBack", "CommitEviction", "MemoryStats", "AssembleFeatures",
+                   "PushDevice"):
         assert f"eps::HipCacheBackend::{method}(" in names, method
 
 
