@@ -158,10 +158,15 @@ struct TableDesc {
   float* state;
   uint32_t dim;
   float beta1, beta2, omb1, omb2, lr, eps, lo, hi;
+  uint32_t bounded;  // lo/hi are the table's weight bounds (else -FLT_MAX/FLT_MAX)
 };
 
+// Running maxima of magnitude bits over a thread's elements: of the reduced
+// gradients (bg), and of m, v and w (before and after the clamp) as computed.
+// A maximum at or above the infinity pattern means a non-finite value; the
+// m, v, w maxima of what a launch writes feed the bounds domain.
 struct RowStats {
-  uint32_t err = 0, bw = 0, bm = 0, bv = 0;
+  uint32_t err = 0, bg = 0, bw = 0, bm = 0, bv = 0;
 };
 
 // Block-wide copy of a kernel-argument array to LDS, one 32-bit word per
@@ -173,23 +178,46 @@ __device__ __forceinline__ void CopyWords(void* dst, const void* src, uint32_t b
   for (uint32_t i = threadIdx.x; i < bytes / 4; i += kThreads) to[i] = from[i];
 }
 
-// One element: Adam in the reference's operation order; returns w (unclamped).
+// Correctly rounded square root.  For x in [2^-96, infinity) it is the
+// hardware estimate s corrected to s - 1 ulp or s + 1 ulp by the signs of the
+// residuals fma(-(s -/+ ulp), s, x): the steps hipcc emits for sqrtf once its
+// range handling (scaling of tiny inputs, zero and infinity) is out of the
+// way, so both give the same bits.  Other inputs take sqrtf.
+__device__ __forceinline__ float SqrtRn(float x) {
+  const uint32_t b = __float_as_uint(x);
+  if (b - 0x0f800000u < 0x7f800000u - 0x0f800000u) {
+    const float s = __builtin_amdgcn_sqrtf(x);
+    const float below = __uint_as_float(__float_as_uint(s) - 1u);
+    const float above = __uint_as_float(__float_as_uint(s) + 1u);
+    const float r = fmaf(-below, s, x) <= 0.f ? below : s;
+    return fmaf(-above, s, x) > 0.f ? above : r;
+  }
+  return sqrtf(x);
+}
+
+// One element: Adam in the reference's operation order, w clamped to the
+// table's bounds (kClamp false: an unbounded table, whose clamp to
+// -FLT_MAX..FLT_MAX changes no finite w, and a non-finite w is an error that
+// nothing is written for).  vn is +0 or more, or NaN (v >= 0 and
+// (omb2 * g) * g >= 0), so its raw bits order like its magnitude.
+template <bool kClamp = true>
 __device__ __forceinline__ void AdamElement(const TableDesc& T, float g, float& w, float& m,
                                             float& v, RowStats& st) {
   const float mn = T.beta1 * m + T.omb1 * g;
   const float vn = T.beta2 * v + (T.omb2 * g) * g;
-  const float wn = w - (T.lr * mn) / (sqrtf(vn) + T.eps);
-  if (!Finite(g)) st.err |= EPS_HIP_STATUS_REDUCE_OVERFLOW;
-  if (!(Finite(mn) && Finite(vn) && Finite(wn))) st.err |= EPS_HIP_STATUS_ADAM_OVERFLOW;
-  w = Clamp(wn, T.lo, T.hi);
+  const float wn = w - (T.lr * mn) / (SqrtRn(vn) + T.eps);
+  st.bg = max(st.bg, AbsBits(g));
+  st.bm = max(st.bm, AbsBits(mn));
+  st.bv = max(st.bv, __float_as_uint(vn));
+  if (kClamp) {
+    w = Clamp(wn, T.lo, T.hi);
+    st.bw = max(st.bw, max(AbsBits(wn), AbsBits(w)));
+  } else {
+    w = wn;
+    st.bw = max(st.bw, AbsBits(wn));
+  }
   m = mn;
   v = vn;
-}
-
-__device__ __forceinline__ void Track(RowStats& st, float w, float m, float v) {
-  st.bw = max(st.bw, AbsBits(w));
-  st.bm = max(st.bm, AbsBits(m));
-  st.bv = max(st.bv, AbsBits(v));
 }
 
 // Vector row update: lane owns columns [c, c+4).
@@ -205,8 +233,6 @@ __device__ __forceinline__ void AdamRow4(const TableDesc& T, uint64_t slot, uint
     Store4(row + c, w);
     Store4(row + T.dim + c, m);
     Store4(row + 2 * T.dim + c, v);
-    Track(st, w.x, m.x, v.x); Track(st, w.y, m.y, v.y);
-    Track(st, w.z, m.z, v.z); Track(st, w.w, m.w, v.w);
   }
 }
 
@@ -217,7 +243,6 @@ __device__ __forceinline__ void AdamRow1(const TableDesc& T, uint64_t slot, uint
   AdamElement(T, g, w, m, v, st);
   if (write) {
     StoreF(row + c, w); StoreF(row + T.dim + c, m); StoreF(row + 2 * T.dim + c, v);
-    Track(st, w, m, v);
   }
 }
 
@@ -228,12 +253,15 @@ __device__ __forceinline__ void Accumulate4(float4& acc, float4 x, float s) {
   acc.w = acc.w + x.w * s;
 }
 
-// Block-level fold of the per-lane statistics: error bits to the status word,
-// written maxima to one slot of the bounds domain.
+// Block-level fold of the per-lane statistics: error bits (with those the
+// maxima imply) to the status word, written maxima to one slot of the bounds
+// domain.
 template <uint32_t kWaves = kBlock / kWave>
 __device__ void FinishBlock(const RowStats& st, Control* ctrl, Bounds* bounds, bool wrote) {
   __shared__ uint32_t s_red[kWaves][4];
   uint32_t e = st.err;
+  if (st.bg >= 0x7f800000u) e |= EPS_HIP_STATUS_REDUCE_OVERFLOW;
+  if (max(st.bw, max(st.bm, st.bv)) >= 0x7f800000u) e |= EPS_HIP_STATUS_ADAM_OVERFLOW;
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) e |= uint32_t(__shfl_xor(int(e), o));
   const uint32_t w = WaveMax(st.bw), m = WaveMax(st.bm), v = WaveMax(st.bv);
@@ -674,7 +702,6 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
           if (write) {
             float* row = T.state + uint64_t(c.key & row_mask) * T.dim * 3 + c.col0 + lane;
             StoreF(row, w); StoreF(row + T.dim, m); StoreF(row + 2 * T.dim, v);
-            Track(st, w, m, v);
           }
         }
         acc = 0.f;
@@ -851,6 +878,7 @@ RowRunKernel(VecArgs a) {
   __shared__ float s_scale[kStaged];
   __shared__ uint32_t s_heads[kRunPositions];
   __shared__ uint32_t s_wave_heads[kBlock / kWave];
+  __shared__ uint32_t s_next;               // next unclaimed row (head index) of the window
   bool write = false;
   if (!VecPrologue(a, s_t, s_grad, write)) return;
   Control* ctrl = a.ctrl;
@@ -879,7 +907,10 @@ RowRunKernel(VecArgs a) {
     // Stage keys and, per position, the gradient row it references and its
     // scale (one coalesced pass; the table and feature lookups happen here
     // once per position instead of once per lane).
-    if (threadIdx.x == 0) s_key[0] = p0 > begin ? a.keys[p0 - 1] : ~a.keys[p0];
+    if (threadIdx.x == 0) {
+      s_key[0] = p0 > begin ? a.keys[p0 - 1] : ~a.keys[p0];
+      s_next = ngroups;
+    }
     for (uint32_t i = threadIdx.x; i < staged; i += kBlock) {
       const uint32_t key = a.keys[p0 + i];
       s_key[i + 1] = key;
@@ -898,11 +929,19 @@ RowRunKernel(VecArgs a) {
     for (uint32_t w = 0; w < kBlock / kWave; ++w) nheads += s_wave_heads[w];
     if (head) s_heads[before + uint32_t(__popcll(ballot & ((1ull << lane) - 1)))] = threadIdx.x;
     __syncthreads();
-    for (uint32_t h = gid; h < nheads; h += ngroups) {
+    // Groups take rows in order from a shared counter (claimed at the top of
+    // a row, used at its end), so a group held up by a row with many
+    // references does not hold up the rows behind it.
+    for (uint32_t h = gid; h < nheads;) {
+      uint32_t claim = 0;
+      if (lig == 0) claim = atomicAdd(&s_next, 1u);
       const uint32_t sb = s_heads[h];
       const uint32_t key = s_key[sb + 1];
       // Hot rows (more than kLongRefs references) belong to HotSliceKernel.
-      if (sb + kLongRefs < staged && s_key[sb + kLongRefs + 1] == key) continue;
+      if (sb + kLongRefs < staged && s_key[sb + kLongRefs + 1] == key) {
+        h = uint32_t(__shfl(int(claim), 0, int(G)));
+        continue;
+      }
       uint32_t se = h + 1 < nheads ? s_heads[h + 1] : p1 - p0;
       while (se < staged && s_key[se + 1] == key) ++se;
       const TableDesc& T = s_t[key >> a.row_bits];
@@ -935,19 +974,26 @@ RowRunKernel(VecArgs a) {
       };
       batch(sb);
       for (uint32_t j0 = sb + kRefBatch; j0 < se; j0 += kRefBatch) batch(j0);
-      if (!active) continue;
-      float4 w = w0, m = m0, v = v0;
-      AdamElement(T, g.x, w.x, m.x, v.x, st);
-      AdamElement(T, g.y, w.y, m.y, v.y, st);
-      AdamElement(T, g.z, w.z, m.z, v.z, st);
-      AdamElement(T, g.w, w.w, m.w, v.w, st);
-      if (write) {
-        Store4Stream(row + c, w);
-        Store4Stream(row + dim + c, m);
-        Store4Stream(row + 2 * dim + c, v);
-        Track(st, w.x, m.x, v.x); Track(st, w.y, m.y, v.y);
-        Track(st, w.z, m.z, v.z); Track(st, w.w, m.w, v.w);
+      if (active) {
+        float4 w = w0, m = m0, v = v0;
+        if (T.bounded) {
+          AdamElement<true>(T, g.x, w.x, m.x, v.x, st);
+          AdamElement<true>(T, g.y, w.y, m.y, v.y, st);
+          AdamElement<true>(T, g.z, w.z, m.z, v.z, st);
+          AdamElement<true>(T, g.w, w.w, m.w, v.w, st);
+        } else {
+          AdamElement<false>(T, g.x, w.x, m.x, v.x, st);
+          AdamElement<false>(T, g.y, w.y, m.y, v.y, st);
+          AdamElement<false>(T, g.z, w.z, m.z, v.z, st);
+          AdamElement<false>(T, g.w, w.w, m.w, v.w, st);
+        }
+        if (write) {
+          Store4Stream(row + c, w);
+          Store4Stream(row + dim + c, m);
+          Store4Stream(row + 2 * dim + c, v);
+        }
       }
+      h = uint32_t(__shfl(int(claim), 0, int(G)));
     }
   }
   FinishBlock(st, ctrl, a.bounds, write);
@@ -1041,6 +1087,7 @@ TableDesc MakeTable(const eps_hip_table& t, const eps_hip_optimizer& o) {
   d.eps = o.epsilon;
   d.lo = o.bounded ? o.weight_min : -FLT_MAX;
   d.hi = o.bounded ? o.weight_max : FLT_MAX;
+  d.bounded = o.bounded ? 1u : 0u;
   return d;
 }
 
