@@ -9,8 +9,10 @@
 // update counters, pinned staging, one stream and the device-output budget.
 #pragma once
 
+#include <filesystem>
 #include <future>
 #include <memory>
+#include <string>
 #include <vector>
 
 #include "eps/cache_agent.hpp"
@@ -36,6 +38,25 @@ struct HipMemoryStats {
   std::uint64_t outstanding_output_bytes;
   std::uint64_t output_allocations;
   bool operator==(const HipMemoryStats&) const = default;
+};
+
+// Identity of a shard snapshot and one of its tables, as the shard holds them
+// (the fields WriteSnapshot takes from ShardStore, src/store/snapshot.cpp:159-194).
+struct SnapshotIdentity {
+  std::string run;
+  ShardId shard;
+  std::uint32_t shard_count;
+  std::uint64_t epoch;
+};
+struct SnapshotTable {
+  TableDefinition definition;
+  std::uint64_t optimizer_sequence;
+  float beta1_power, beta2_power;
+  std::vector<Key> keys;  // row order of the file (the shard's key order)
+};
+struct SnapshotFile {
+  std::uint64_t bytes, checksum, device_rows;
+  bool operator==(const SnapshotFile&) const = default;
 };
 
 class HipCacheBackend final : public GpuCacheAgent {
@@ -69,6 +90,17 @@ class HipCacheBackend final : public GpuCacheAgent {
   std::future<Result<Ack>> PushDevice(std::vector<UpdateContext> contexts, std::vector<AgentWork> work,
                                       std::vector<FeatureInput> layouts,
                                       std::vector<DeviceTensorBlock> gradients);
+
+  // Snapshot format 2 of a shard whose rows live in this backend, written
+  // straight from HBM: the same bytes as the reference's WriteSnapshot
+  // (src/store/snapshot.cpp:159-194) of a store holding these tables and rows,
+  // with the same staging-file publication.  Each key is a row resident here
+  // or one of `host_rows` (rows the shard's CPU store holds).  The reference
+  // first moves every GPU row back to the CPU store, 64 rows per request
+  // (src/server/service.cpp:599-612), then writes from there.
+  std::future<Result<SnapshotFile>> WriteSnapshot(std::filesystem::path file, SnapshotIdentity identity,
+                                                  std::vector<SnapshotTable> tables,
+                                                  std::vector<RowState> host_rows);
 
  private:
   struct Impl;

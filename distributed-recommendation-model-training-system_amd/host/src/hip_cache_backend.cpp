@@ -12,6 +12,7 @@
 //   AssembleFeatures          -> eps_hip_fill_u32, eps_hip_add_contribution,
 //                                eps_hip_normalize_mean
 //   PushDevice                -> eps_hip_prepare + eps_hip_push (device gradients)
+//   WriteSnapshot             -> eps_hip_gather_rows into pinned staging, double buffered
 // Occurrence slots are resolved once per unique row (the reference looks the
 // row up in a hash map once per occurrence, src/cuda/cache_backend.cu:279-291).
 #include "eps/hip_cache_backend.hpp"
@@ -30,6 +31,7 @@
 
 #include "eps_hip.h"
 #include "executor.hpp"
+#include "snapshot_writer.hpp"
 
 namespace eps {
 namespace {
@@ -1028,6 +1030,161 @@ std::future<Result<Ack>> HipCacheBackend::PushDevice(std::vector<UpdateContext> 
     for (auto& [id, t] : tables)
       for (Key key : t.rows) ++t.table->rows.at(key).updates;
     return Ack{};
+  });
+}
+
+// Snapshot writeback.  Rows are encoded in file order chunk by chunk: the
+// device rows of chunk c + 1 are gathered into one half of the pinned staging
+// (eps_hip_gather_rows writes host memory directly) while the host hashes and
+// writes chunk c from the other half.  The checksum, a byte-serial FNV-1a, is
+// the host's share and bounds the rate.
+std::future<Result<SnapshotFile>> HipCacheBackend::WriteSnapshot(std::filesystem::path file,
+                                                                 SnapshotIdentity identity,
+                                                                 std::vector<SnapshotTable> tables,
+                                                                 std::vector<RowState> host_rows) {
+  return impl_->worker->Submit<SnapshotFile>([this, file = std::move(file), identity = std::move(identity),
+                                              tables = std::move(tables),
+                                              host_rows = std::move(host_rows)] {
+    Impl& I = *impl_;
+    I.Activate();
+    // The identity and schema checks the reference reader applies
+    // (src/store/snapshot.cpp:201-206,230-245), so a written file restores.
+    Require(!identity.run.empty() && identity.run.size() <= 1024 && identity.shard_count > 0 &&
+                identity.shard < identity.shard_count && identity.epoch > 0 && tables.size() <= 1024,
+            "invalid snapshot identity");
+    std::map<std::pair<TableId, Key>, const RowState*> host;
+    for (const auto& r : host_rows)
+      Require(host.emplace(std::make_pair(r.row.table, r.row.key), &r).second, "duplicate snapshot host row");
+    std::set<TableId> ids;
+    std::uint64_t device_rows = 0;
+    for (const auto& t : tables) {
+      const auto& d = t.definition;
+      Require(ids.insert(d.id).second && d.dimension > 0 && d.dimension <= 65536 &&
+                  d.shard_count == identity.shard_count && d.partition_epoch == identity.epoch &&
+                  t.beta1_power >= 0 && t.beta1_power < 1 && t.beta2_power >= 0 && t.beta2_power < 1,
+              "invalid snapshot table");
+      auto it = I.tables.find(d.id);
+      Require(it == I.tables.end() || it->second->definition == d, "HIP table configuration mismatch");
+      std::set<Key> keys;
+      for (Key key : t.keys) {
+        Require(keys.insert(key).second, "duplicate snapshot row");
+        const bool resident = it != I.tables.end() && it->second->rows.count(key);
+        auto h = host.find({d.id, key});
+        Require(resident != (h != host.end()), "snapshot row must be held by exactly one store");
+        if (resident) {
+          ++device_rows;
+        } else {
+          const RowState& r = *h->second;
+          Require(r.weights.size() == d.dimension && r.first_moment.size() == d.dimension &&
+                      r.second_moment.size() == d.dimension,
+                  "snapshot host row shape mismatch");
+        }
+      }
+      Require(it == I.tables.end() || 2 * std::uint64_t(d.dimension) * 12 <= I.options.transfer_bytes,
+              "snapshot row exceeds the staging buffer", Error::Code::capacity_exceeded);
+    }
+
+    hip_detail::SnapshotWriter out(file);
+    out.U64(hip_detail::SnapshotWriter::kMagicV2);
+    out.String(identity.run);
+    out.U64(identity.shard);
+    out.U64(identity.shard_count);
+    out.U64(identity.epoch);
+    out.U64(tables.size());
+    Event ready[2] = {Event(I.options.device), Event(I.options.device)};
+    const std::uint64_t half_bytes = I.options.transfer_bytes / 2;
+    for (const auto& t : tables) {
+      const auto& d = t.definition;
+      const auto& o = d.optimizer;
+      out.U64(d.id);
+      out.U64(d.dimension);
+      out.U64(d.shard_count);
+      out.U64(d.partition_epoch);
+      out.F32(o.learning_rate);
+      out.F32(o.beta1);
+      out.F32(o.beta2);
+      out.F32(o.epsilon);
+      out.F32(o.initial_beta1_power);
+      out.F32(o.initial_beta2_power);
+      out.U64(o.weight_bounds ? 1 : 0);
+      if (o.weight_bounds) {
+        out.F32(o.weight_bounds->minimum);
+        out.F32(o.weight_bounds->maximum);
+      }
+      out.F32(d.initialization_min);
+      out.F32(d.initialization_max);
+      out.U64(d.initialization_seed);
+      out.U64(t.optimizer_sequence);
+      out.F32(t.beta1_power);
+      out.F32(t.beta2_power);
+      out.U64(t.keys.size());
+      auto it = I.tables.find(d.id);
+      Impl::Table* table = it == I.tables.end() ? nullptr : it->second.get();
+      const std::uint64_t floats = std::uint64_t(d.dimension) * 3;
+      const std::uint64_t cap = table ? std::min(half_bytes / (floats * 4), half_bytes / 8) : 0;
+      // Chunks: [begin, end) of the key list holding at most `cap` device rows.
+      std::vector<std::pair<std::size_t, std::size_t>> chunks;
+      for (std::size_t b = 0; b < t.keys.size();) {
+        std::size_t e = b;
+        std::uint64_t n = 0;
+        while (e < t.keys.size() && (!table || !table->rows.count(t.keys[e]) || n < cap)) {
+          if (table && table->rows.count(t.keys[e])) ++n;
+          ++e;
+        }
+        chunks.emplace_back(b, e);
+        b = e;
+      }
+      auto issue = [&](std::size_t c) {
+        const int h = int(c % 2);
+        auto* slots = I.host_indices.As<std::uint64_t>() + h * (half_bytes / 8);
+        std::uint64_t n = 0;
+        for (std::size_t i = chunks[c].first; i < chunks[c].second; ++i)
+          if (table)
+            if (auto r = table->rows.find(t.keys[i]); r != table->rows.end()) slots[n++] = r->second.location.slot;
+        if (n) {
+          auto* dslots = I.device_indices.As<std::uint64_t>() + h * (half_bytes / 8);
+          I.CopyIn(dslots, slots, n * 8);
+          Abi(eps_hip_gather_rows(&table->abi, dslots,
+                                  reinterpret_cast<float*>(I.host_values.As<unsigned char>() + h * half_bytes), n,
+                                  I.stream.value));
+        }
+        Hip(hipEventRecord(ready[h].value, I.stream.value));
+      };
+      try {
+        if (!chunks.empty()) issue(0);
+        for (std::size_t c = 0; c < chunks.size(); ++c) {
+          if (c + 1 < chunks.size()) issue(c + 1);
+          const int h = int(c % 2);
+          Hip(hipEventSynchronize(ready[h].value));
+          const float* staged = reinterpret_cast<const float*>(I.host_values.As<unsigned char>() + h * half_bytes);
+          std::uint64_t n = 0;
+          for (std::size_t i = chunks[c].first; i < chunks[c].second; ++i) {
+            const Key key = t.keys[i];
+            out.U64(key);
+            const Impl::Entry* entry = nullptr;
+            if (table)
+              if (auto r = table->rows.find(key); r != table->rows.end()) entry = &r->second;
+            if (entry) {
+              out.U64(entry->updates);
+              out.Bytes(staged + n * floats, floats * 4);
+              ++n;
+            } else {
+              const RowState& row = *host.at({d.id, key});
+              out.U64(row.row_updates);
+              out.Bytes(row.weights.data(), d.dimension * 4);
+              out.Bytes(row.first_moment.data(), d.dimension * 4);
+              out.Bytes(row.second_moment.data(), d.dimension * 4);
+            }
+          }
+        }
+      } catch (...) {
+        (void)hipStreamSynchronize(I.stream.value);
+        throw;
+      }
+    }
+    const std::uint64_t bytes = out.bytes() + 8;
+    const std::uint64_t checksum = out.Publish();
+    return SnapshotFile{bytes, checksum, device_rows};
   });
 }
 

@@ -1,0 +1,172 @@
+// snapshot_writer.hpp -- the reference's snapshot byte stream, written to a
+// staging file and published atomically.
+//
+// Format (src/store/snapshot.cpp:29-76,159-194): little-endian u64 and IEEE
+// float fields, strings as a u64 length plus their bytes, and a trailing u64
+// FNV-1a checksum of every byte before it.  Publication follows WriteSnapshot:
+// the bytes go to "<file>.pending" (created exclusively), are fsync'ed, hard
+// linked to <file> (which must not exist yet), the staging name is removed
+// and the directory fsync'ed.  I/O failures are Error::Code::unavailable.
+// The checksum is byte-serial, so the caller's thread only hashes and fills
+// buffers; a second thread writes the full ones.
+#pragma once
+
+#include <fcntl.h>
+#include <sys/stat.h>
+#include <unistd.h>
+
+#include <bit>
+#include <cerrno>
+#include <condition_variable>
+#include <cstdint>
+#include <cstring>
+#include <filesystem>
+#include <mutex>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "executor.hpp"
+
+namespace eps::hip_detail {
+
+static_assert(std::endian::native == std::endian::little,
+              "snapshot rows are copied as little-endian bytes");
+
+class SnapshotWriter {
+ public:
+  static constexpr std::uint64_t kMagicV2 = 0x3253504541524853ULL;  // "SHRAEPS2"
+
+  explicit SnapshotWriter(std::filesystem::path file)
+      : file_(std::move(file)), pending_(file_.string() + ".pending") {
+    std::error_code ec;
+    if (file_.has_parent_path()) std::filesystem::create_directories(file_.parent_path(), ec);
+    fd_ = ::open(pending_.c_str(), O_WRONLY | O_CREAT | O_EXCL, 0600);
+    Require(fd_ >= 0, "cannot create snapshot staging file", Error::Code::unavailable);
+    for (auto& b : buffers_) b.resize(kBuffer);
+    io_ = std::thread([this] { Drain(); });
+  }
+  ~SnapshotWriter() {
+    Stop();
+    if (fd_ >= 0) ::close(fd_);
+    if (!published_) ::unlink(pending_.c_str());
+  }
+  SnapshotWriter(const SnapshotWriter&) = delete;
+  SnapshotWriter& operator=(const SnapshotWriter&) = delete;
+
+  void U64(std::uint64_t v) { Bytes(&v, 8); }
+  void F32(float x) { Bytes(&x, 4); }
+  void String(const std::string& s) {
+    U64(s.size());
+    Bytes(s.data(), s.size());
+  }
+  // Hashed bytes, appended as they lie in memory (little-endian host).
+  void Bytes(const void* data, std::size_t size) {
+    const auto* p = static_cast<const unsigned char*>(data);
+    std::uint64_t h = hash_;
+    for (std::size_t i = 0; i < size; ++i) h = (h ^ p[i]) * kPrime;
+    hash_ = h;
+    Append(p, size);
+  }
+  std::uint64_t bytes() const { return written_ + filled_; }
+
+  // Appends the checksum, makes the file durable and publishes it.
+  std::uint64_t Publish() {
+    const std::uint64_t checksum = hash_;
+    Append(&checksum, 8);
+    Hand();
+    Stop();
+    Require(!io_failed_, "snapshot write failed", Error::Code::unavailable);
+    Require(::fsync(fd_) == 0, "snapshot fsync failed", Error::Code::unavailable);
+    ::close(fd_);
+    fd_ = -1;
+    Require(::link(pending_.c_str(), file_.c_str()) == 0,
+            "snapshot already exists or cannot be published", Error::Code::unavailable);
+    published_ = true;
+    ::unlink(pending_.c_str());
+    const auto dir = file_.has_parent_path() ? file_.parent_path() : std::filesystem::path(".");
+    const int d = ::open(dir.c_str(), O_RDONLY);
+    Require(d >= 0, "cannot open snapshot directory", Error::Code::unavailable);
+    const int rc = ::fsync(d);
+    ::close(d);
+    Require(rc == 0, "snapshot fsync failed", Error::Code::unavailable);
+    return checksum;
+  }
+
+ private:
+  static constexpr std::uint64_t kOffset = 14695981039346656037ULL;
+  static constexpr std::uint64_t kPrime = 1099511628211ULL;
+  static constexpr std::size_t kBuffer = 4u << 20;
+
+  void Append(const void* data, std::size_t size) {
+    const auto* p = static_cast<const unsigned char*>(data);
+    while (size) {
+      auto& buffer = buffers_[current_];
+      const std::size_t n = std::min(size, buffer.size() - filled_);
+      std::memcpy(buffer.data() + filled_, p, n);
+      filled_ += n;
+      p += n;
+      size -= n;
+      if (filled_ == buffer.size()) Hand();
+    }
+  }
+  // Passes the current buffer to the writing thread and waits for the other.
+  void Hand() {
+    std::unique_lock<std::mutex> lock(mutex_);
+    idle_.wait(lock, [&] { return !busy_; });
+    Require(!io_failed_, "snapshot write failed", Error::Code::unavailable);
+    ready_ = current_;
+    ready_bytes_ = filled_;
+    busy_ = true;
+    written_ += filled_;
+    filled_ = 0;
+    current_ ^= 1;
+    wake_.notify_one();
+  }
+  void Drain() {
+    std::unique_lock<std::mutex> lock(mutex_);
+    for (;;) {
+      wake_.wait(lock, [&] { return busy_ || stop_; });
+      if (!busy_) return;
+      const unsigned char* data = buffers_[ready_].data();
+      const std::size_t size = ready_bytes_;
+      lock.unlock();
+      bool ok = true;
+      for (std::size_t pos = 0; pos < size && ok;) {
+        const ssize_t n = ::write(fd_, data + pos, size - pos);
+        if (n < 0 && errno == EINTR) continue;
+        ok = n > 0;
+        if (ok) pos += std::size_t(n);
+      }
+      lock.lock();
+      io_failed_ = io_failed_ || !ok;
+      busy_ = false;
+      idle_.notify_one();
+    }
+  }
+  void Stop() {
+    if (!io_.joinable()) return;
+    {
+      std::unique_lock<std::mutex> lock(mutex_);
+      idle_.wait(lock, [&] { return !busy_; });
+      stop_ = true;
+    }
+    wake_.notify_one();
+    io_.join();
+  }
+
+  std::filesystem::path file_;
+  std::string pending_;
+  std::vector<unsigned char> buffers_[2];
+  unsigned current_ = 0, ready_ = 0;
+  std::size_t filled_ = 0, ready_bytes_ = 0;
+  std::uint64_t written_ = 0, hash_ = kOffset;
+  int fd_ = -1;
+  bool published_ = false;
+  std::mutex mutex_;
+  std::condition_variable wake_, idle_;
+  bool busy_ = false, stop_ = false, io_failed_ = false;
+  std::thread io_;
+};
+
+}  // namespace eps::hip_detail

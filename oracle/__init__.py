@@ -122,6 +122,9 @@ def lib():
             "eps_or_validate_compact": (C.c_int, [U64, P, U32, P, U64, P, P, P, U64]),
             "eps_or_expand_compact": (C.c_int, [U64, P, U32, P, U64, P, P, P, U64, P]),
             "eps_or_build_compact": (C.c_int, [P, P, U32, U32, P, U64, P, P, P, P, P, P]),
+            "eps_or_fnv1a": (U64, [U64, P, U64]),
+            "eps_or_snapshot_write": (C.c_int, [C.c_char_p, C.c_char_p, U64, U64, U64, P, U32]),
+            "eps_or_snapshot_read": (C.c_int, [C.c_char_p, P, U64, P, P, P, P, P, U32, P, P]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -339,6 +342,50 @@ def build_compact(features, gradients, dim, row_keys):
 _ref = None
 
 
+FNV_OFFSET = 14695981039346656037
+
+
+def fnv1a(data: bytes, start: int = FNV_OFFSET) -> int:
+    buf = np.frombuffer(bytes(data), dtype=np.uint8)
+    return int(lib().eps_or_fnv1a(start, buf.ctypes.data if len(buf) else None, len(buf)))
+
+
+def snapshot_write(path, run: str, shard: int, shard_count: int, epoch: int, stores) -> None:
+    """WriteSnapshot (format 2) of the given stores, in the given order."""
+    arr = (C.c_void_p * len(stores))(*[s.h for s in stores])
+    rc = lib().eps_or_snapshot_write(str(path).encode(), run.encode(), shard, shard_count, epoch,
+                                     arr, len(stores))
+    if rc:
+        raise OSError(last_error())
+
+
+class _SnapshotStore(Store):
+    def __init__(self, handle, defn):  # takes ownership of a store made by the reader
+        self.defn = defn
+        self.dim = defn.dim
+        self.h = handle
+
+
+def snapshot_read(path, capacity: int = 1024) -> dict:
+    """ReadSnapshot (format 1 or 2): identity, version, checksum and the tables."""
+    run = C.create_string_buffer(1025)
+    shard, count, epoch, checksum = C.c_uint64(), C.c_uint64(), C.c_uint64(), C.c_uint64()
+    version, tables = C.c_uint32(), C.c_uint32()
+    arr = (C.c_void_p * capacity)()
+    rc = lib().eps_or_snapshot_read(str(path).encode(), run, 1025, C.byref(shard), C.byref(count),
+                                    C.byref(epoch), C.byref(version), arr, capacity,
+                                    C.byref(tables), C.byref(checksum))
+    if rc:
+        raise ValueError(last_error())
+    stores = []
+    for i in range(tables.value):
+        d = TableDef.from_address(arr[i])  # eps_or_store starts with its definition
+        stores.append(_SnapshotStore(arr[i], TableDef.from_buffer_copy(d)))
+    return {"run": run.value.decode(), "shard": shard.value, "shard_count": count.value,
+            "epoch": epoch.value, "version": version.value, "checksum": checksum.value,
+            "tables": stores}
+
+
 def ref_available() -> bool:
     return REF_PATH.exists()
 
@@ -371,6 +418,7 @@ def ref_lib():
             "ref_host_backend_load": (C.c_int, [P, U32, U32, P, U64, P, P, P]),
             "ref_host_backend_apply": (C.c_int, [P, U32, F, F, F, P, U64, P, U32]),
             "ref_host_backend_read": (C.c_int, [P, U32, U32, P, P, U64, P, P]),
+            "ref_shard_write_snapshot": (C.c_int, [P, C.c_char_p, C.c_char_p]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -416,6 +464,11 @@ class RefShard:
         if rc:
             raise KeyError(self.error())
         return w, m, v, u.value
+
+    def write_snapshot(self, path, run: str) -> None:
+        rc = self.L.ref_shard_write_snapshot(self.h, str(path).encode(), run.encode())
+        if rc:
+            raise OSError(self.error())
 
     def powers(self, table):
         b1, b2, seq = C.c_float(), C.c_float(), C.c_uint64()

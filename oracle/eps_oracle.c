@@ -637,3 +637,197 @@ int eps_or_build_compact(const eps_or_feature* features, const float* const* gra
   return eps_or_validate_compact(rows, row_keys, dim, source_values, nsources * dim,
                                  row_offsets, source_rows, scales, nrefs);
 }
+
+/* ------------------------------------------------------------------------ */
+/* Snapshot format: src/store/snapshot.cpp.  Little-endian u64 and float
+ * fields, strings as a u64 length plus bytes, FNV-1a over every byte before
+ * the trailing checksum (Binary::Bytes/U64/Float/String, :29-76). */
+#define FNV_PRIME 1099511628211ULL
+#define SNAPSHOT_MAGIC_V1 0x3153504541524853ULL
+#define SNAPSHOT_MAGIC_V2 0x3253504541524853ULL
+
+uint64_t eps_or_fnv1a(uint64_t hash, const void* data, uint64_t size) {
+  const unsigned char* p = (const unsigned char*)data;
+  for (uint64_t i = 0; i < size; ++i) hash = (hash ^ p[i]) * FNV_PRIME;
+  return hash;
+}
+
+typedef struct snap_io {
+  FILE* f;
+  uint64_t hash;
+  int failed;
+} snap_io;
+
+static void snap_put(snap_io* io, const void* data, uint64_t size, int hashed) {
+  if (fwrite(data, 1, size, io->f) != size) io->failed = 1;
+  if (hashed) io->hash = eps_or_fnv1a(io->hash, data, size);
+}
+static void snap_u64(snap_io* io, uint64_t v, int hashed) {
+  unsigned char b[8];
+  for (int i = 0; i < 8; ++i) b[i] = (unsigned char)(v >> (8 * i));
+  snap_put(io, b, 8, hashed);
+}
+static void snap_f32(snap_io* io, float x) {
+  uint32_t u;
+  memcpy(&u, &x, 4);
+  unsigned char b[4];
+  for (int i = 0; i < 4; ++i) b[i] = (unsigned char)(u >> (8 * i));
+  snap_put(io, b, 4, 1);
+}
+static int snap_get(snap_io* io, void* data, uint64_t size, int hashed) {
+  if (fread(data, 1, size, io->f) != size) return io->failed = 1, 0;
+  if (hashed) io->hash = eps_or_fnv1a(io->hash, data, size);
+  return 1;
+}
+static uint64_t snap_get_u64(snap_io* io, int hashed) {
+  unsigned char b[8] = {0};
+  snap_get(io, b, 8, hashed);
+  uint64_t v = 0;
+  for (int i = 0; i < 8; ++i) v |= (uint64_t)b[i] << (8 * i);
+  return v;
+}
+static float snap_get_f32(snap_io* io) {
+  unsigned char b[4] = {0};
+  snap_get(io, b, 4, 1);
+  uint32_t u = 0;
+  for (int i = 0; i < 4; ++i) u |= (uint32_t)b[i] << (8 * i);
+  float x;
+  memcpy(&x, &u, 4);
+  return x;
+}
+
+/* Binary::Definition (:77-98): id, dimension, shard count, partition epoch,
+ * the six optimizer floats, [bounds flag (+ min, max) in format 2], the
+ * initializer bounds and seed. */
+static void snap_put_definition(snap_io* io, const eps_or_table_def* d, uint64_t epoch) {
+  snap_u64(io, d->id, 1);
+  snap_u64(io, d->dim, 1);
+  snap_u64(io, d->shard_count, 1);
+  snap_u64(io, epoch, 1);
+  snap_f32(io, d->learning_rate); snap_f32(io, d->beta1); snap_f32(io, d->beta2);
+  snap_f32(io, d->epsilon); snap_f32(io, d->initial_beta1_power); snap_f32(io, d->initial_beta2_power);
+  snap_u64(io, d->bounded ? 1 : 0, 1);
+  if (d->bounded) { snap_f32(io, d->weight_min); snap_f32(io, d->weight_max); }
+  snap_f32(io, d->init_min); snap_f32(io, d->init_max);
+  snap_u64(io, d->init_seed, 1);
+}
+
+int eps_or_snapshot_write(const char* path, const char* run, uint64_t shard,
+                          uint64_t shard_count, uint64_t epoch, eps_or_store* const* stores,
+                          uint32_t table_count) {
+  snap_io io = {fopen(path, "wb"), EPS_OR_FNV_OFFSET, 0};
+  if (!io.f) return fail(EPS_OR_UNAVAILABLE, "cannot create snapshot");
+  snap_u64(&io, SNAPSHOT_MAGIC_V2, 1);
+  const uint64_t run_bytes = strlen(run);
+  snap_u64(&io, run_bytes, 1);
+  snap_put(&io, run, run_bytes, 1);
+  snap_u64(&io, shard, 1); snap_u64(&io, shard_count, 1); snap_u64(&io, epoch, 1);
+  snap_u64(&io, table_count, 1);
+  for (uint32_t t = 0; t < table_count; ++t) {
+    const eps_or_store* s = stores[t];
+    snap_put_definition(&io, &s->def, epoch);
+    snap_u64(&io, s->optimizer_sequence, 1);
+    snap_f32(&io, s->beta1_power);
+    snap_f32(&io, s->beta2_power);
+    snap_u64(&io, s->rows, 1);
+    const uint64_t n = (uint64_t)s->def.dim * 3;
+    for (uint64_t r = 0; r < s->rows; ++r) {
+      snap_u64(&io, s->keys[r], 1);
+      snap_u64(&io, s->updates[r], 1);
+      const float* row = row_ptr(s, r);
+      for (uint64_t i = 0; i < n; ++i) snap_f32(&io, row[i]);
+    }
+  }
+  snap_u64(&io, io.hash, 0);
+  if (fclose(io.f) != 0) io.failed = 1;
+  return io.failed ? fail(EPS_OR_UNAVAILABLE, "snapshot write failed") : EPS_OR_OK;
+}
+
+int eps_or_snapshot_read(const char* path, char* run, uint64_t run_capacity, uint64_t* shard,
+                         uint64_t* shard_count, uint64_t* epoch, uint32_t* version,
+                         eps_or_store** stores, uint32_t capacity, uint32_t* table_count,
+                         uint64_t* checksum) {
+  snap_io io = {fopen(path, "rb"), EPS_OR_FNV_OFFSET, 0};
+  if (!io.f) return fail(EPS_OR_UNAVAILABLE, "cannot open snapshot");
+  uint32_t made = 0;
+  int rc = EPS_OR_OK;
+  const uint64_t magic = snap_get_u64(&io, 1);
+  if (magic != SNAPSHOT_MAGIC_V1 && magic != SNAPSHOT_MAGIC_V2) {
+    rc = fail(EPS_OR_INVALID_ARGUMENT, "unsupported snapshot format");
+    goto done;
+  }
+  *version = magic == SNAPSHOT_MAGIC_V2 ? 2 : 1;
+  const uint64_t run_bytes = snap_get_u64(&io, 1);
+  if (run_bytes > 1024 || run_bytes + 1 > run_capacity) {
+    rc = fail(EPS_OR_INVALID_ARGUMENT, "snapshot string too long");
+    goto done;
+  }
+  snap_get(&io, run, run_bytes, 1);
+  run[run_bytes] = 0;
+  *shard = snap_get_u64(&io, 1); *shard_count = snap_get_u64(&io, 1); *epoch = snap_get_u64(&io, 1);
+  const uint64_t tables = snap_get_u64(&io, 1);
+  if (tables > capacity || tables > 1024) {
+    rc = fail(EPS_OR_INVALID_ARGUMENT, "snapshot table count exceeds limit");
+    goto done;
+  }
+  for (uint64_t t = 0; t < tables && !io.failed; ++t) {
+    eps_or_table_def d;
+    memset(&d, 0, sizeof d);
+    d.id = (uint32_t)snap_get_u64(&io, 1);
+    d.dim = (uint32_t)snap_get_u64(&io, 1);
+    d.shard_count = (uint32_t)snap_get_u64(&io, 1);
+    d.shard = (uint32_t)*shard;
+    const uint64_t table_epoch = snap_get_u64(&io, 1);
+    d.learning_rate = snap_get_f32(&io); d.beta1 = snap_get_f32(&io); d.beta2 = snap_get_f32(&io);
+    d.epsilon = snap_get_f32(&io); d.initial_beta1_power = snap_get_f32(&io);
+    d.initial_beta2_power = snap_get_f32(&io);
+    if (*version == 2) {
+      const uint64_t enabled = snap_get_u64(&io, 1);
+      if (enabled > 1) { rc = fail(EPS_OR_INVALID_ARGUMENT, "invalid snapshot weight-bounds flag"); goto done; }
+      d.bounded = (int32_t)enabled;
+      if (enabled) { d.weight_min = snap_get_f32(&io); d.weight_max = snap_get_f32(&io); }
+    }
+    d.init_min = snap_get_f32(&io); d.init_max = snap_get_f32(&io);
+    d.init_seed = snap_get_u64(&io, 1);
+    if (d.dim == 0 || d.dim > 65536 || d.shard_count != *shard_count || table_epoch != *epoch) {
+      rc = fail(EPS_OR_INVALID_ARGUMENT, "table partition does not match snapshot");
+      goto done;
+    }
+    eps_or_store* s = eps_or_create(&d);
+    if (!s) { rc = EPS_OR_INVALID_ARGUMENT; goto done; }
+    stores[made++] = s;
+    s->optimizer_sequence = snap_get_u64(&io, 1);
+    s->beta1_power = snap_get_f32(&io);
+    s->beta2_power = snap_get_f32(&io);
+    const uint64_t rows = snap_get_u64(&io, 1);
+    const uint32_t dim = d.dim;
+    float* buf = (float*)malloc((uint64_t)dim * 3 * sizeof(float));
+    for (uint64_t r = 0; r < rows && !io.failed; ++r) {
+      const uint64_t key = snap_get_u64(&io, 1), updates = snap_get_u64(&io, 1);
+      for (uint64_t i = 0; i < (uint64_t)dim * 3; ++i) buf[i] = snap_get_f32(&io);
+      if (!io.failed && eps_or_import(s, key, buf, buf + dim, buf + 2 * dim, updates)) {
+        rc = EPS_OR_INVALID_ARGUMENT;
+        free(buf);
+        goto done;
+      }
+    }
+    free(buf);
+  }
+  {
+    const uint64_t actual = io.hash;
+    const uint64_t expected = snap_get_u64(&io, 0);
+    unsigned char extra;
+    if (io.failed) rc = fail(EPS_OR_UNAVAILABLE, "snapshot truncated");
+    else if (actual != expected) rc = fail(EPS_OR_INVALID_ARGUMENT, "snapshot checksum mismatch");
+    else if (fread(&extra, 1, 1, io.f) == 1) rc = fail(EPS_OR_INVALID_ARGUMENT, "snapshot contains trailing data");
+    *checksum = expected;
+  }
+done:
+  fclose(io.f);
+  *table_count = made;
+  if (rc != EPS_OR_OK) {
+    for (uint32_t i = 0; i < made; ++i) eps_or_destroy(stores[i]);
+    *table_count = 0;
+  }
+  return rc;
+}

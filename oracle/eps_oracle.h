@@ -36,6 +36,7 @@ extern "C" {
 /* Status codes: 0 ok, else eps::Error::Code + 1 (include/eps/types.hpp:17-22). */
 #define EPS_OR_OK 0
 #define EPS_OR_INVALID_ARGUMENT 1
+#define EPS_OR_UNAVAILABLE 2
 #define EPS_OR_STALE_GENERATION 3
 #define EPS_OR_CAPACITY_EXCEEDED 5
 
@@ -133,6 +134,24 @@ int eps_or_build_compact(const eps_or_feature* features, const float* const* gra
                          uint64_t rows, float* source_values, uint64_t* source_value_count,
                          uint64_t* row_offsets, uint64_t* source_rows, float* scales,
                          uint64_t* references);
+
+/* ---- snapshot format: src/store/snapshot.cpp ---- */
+#define EPS_OR_FNV_OFFSET 14695981039346656037ULL
+/* FNV-1a (64-bit) over `size` bytes, continuing from `hash`. */
+uint64_t eps_or_fnv1a(uint64_t hash, const void* data, uint64_t size);
+/* WriteSnapshot (snapshot.cpp:159-194): format 2, the tables in the order given
+ * (the reference writes its hash map's order), each table's rows in its store's
+ * key order, every table's partition epoch = epoch.  Writes `path` directly. */
+int eps_or_snapshot_write(const char* path, const char* run, uint64_t shard,
+                          uint64_t shard_count, uint64_t epoch, eps_or_store* const* stores,
+                          uint32_t table_count);
+/* ReadSnapshot (snapshot.cpp:221-267) of format 1 or 2 into new stores, tables
+ * in file order (the caller destroys them).  run receives the NUL-terminated
+ * run ID (run_capacity >= 1025). */
+int eps_or_snapshot_read(const char* path, char* run, uint64_t run_capacity, uint64_t* shard,
+                         uint64_t* shard_count, uint64_t* epoch, uint32_t* version,
+                         eps_or_store** stores, uint32_t capacity, uint32_t* table_count,
+                         uint64_t* checksum);
 
 #ifdef __cplusplus
 }

@@ -3,7 +3,8 @@
 // TEST INFRASTRUCTURE ONLY.  oracle/Makefile compiles this file together with
 // the reference's unmodified sources (src/store/shard_store.cpp,
 // src/access/batch_access.cpp, src/access/compact_gradients.cpp,
-// src/update/lazy_adam.cpp, src/cache/host_backend.cpp) where they lie in the
+// src/update/lazy_adam.cpp, src/cache/host_backend.cpp, src/store/snapshot.cpp)
+// where they lie in the
 // reference checkout, into oracle/_ref/libeps_ref.so.  Tests use it to pin the
 // C restatement in oracle/eps_oracle.c; bench.py may time it as the CPU
 // baseline.  Nothing here is part of the product.
@@ -20,6 +21,7 @@
 #include "eps/cache_backend.hpp"
 #include "eps/compact_gradients.hpp"
 #include "store/shard_store.hpp"
+#include "store/snapshot.hpp"
 #include "update/lazy_adam.hpp"
 
 #include "eps_oracle.h"
@@ -68,6 +70,11 @@ void* ref_shard_create(std::uint32_t shard, std::uint32_t count) {
   return new Shard(shard, count);
 }
 void ref_shard_destroy(void* h) { delete static_cast<Shard*>(h); }
+
+// WriteSnapshot of the shard (format 2; the file must not exist yet).
+int ref_shard_write_snapshot(void* h, const char* path, const char* run) {
+  return Guard([&] { detail::WriteSnapshot(path, run, static_cast<Shard*>(h)->store); });
+}
 
 int ref_shard_create_table(void* h, const eps_or_table_def* t) {
   return Guard([&] { static_cast<Shard*>(h)->store.Create(Definition(*t)); });

@@ -8,12 +8,18 @@
 // rejection that leaves every row untouched; slot reclamation and stale
 // generations after reuse; the atomic slot reserve of concurrent loads; plus
 // device feature assembly (tests/device_pull_tests.cpp's ReferenceAssembly);
-// and the device-resident push (ReduceGradients + LazyAdam on the device).
+// the device-resident push (ReduceGradients + LazyAdam on the device); and the
+// snapshot writeback from HBM, read back and rewritten by the oracle's
+// restatement of src/store/snapshot.cpp, which must give the same bytes.
 // Expected values come from the oracle (oracle/eps_oracle.h, the CPU
 // restatement of the reference shard) and are compared bit for bit.
+#include <unistd.h>
+
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <filesystem>
+#include <fstream>
 #include <iostream>
 #include <limits>
 #include <map>
@@ -378,8 +384,127 @@ void DevicePush(HipCacheBackend& gpu, const std::vector<LocatedRow>& located, Mo
                 "state after rejected device pushes");
 }
 
+std::string FileBytes(const std::filesystem::path& p) {
+  std::ifstream in(p, std::ios::binary);
+  return {std::istreambuf_iterator<char>(in), std::istreambuf_iterator<char>()};
+}
+
+RowState MakeRow(TableId table, Key key, std::uint32_t dim) {
+  RowState r{{table, key}, std::vector<float>(dim), std::vector<float>(dim), std::vector<float>(dim),
+             key % 13};
+  for (std::uint32_t d = 0; d < dim; ++d) {
+    r.weights[d] = 0.01f * std::sin(float(key * 7 + d));
+    r.first_moment[d] = 1e-4f * std::cos(float(key + 3 * d));
+    r.second_moment[d] = 1e-6f * float(1 + (key + d) % 5);
+  }
+  return r;
+}
+
+// Snapshot writeback: 2,000 device rows of a bounded table interleaved with
+// CPU-store rows in the file's key order (several staging chunks), a table the
+// backend defines but holds no rows of, and a table only the CPU store holds.
+void SnapshotWriteback() {
+  const auto dir = std::filesystem::temp_directory_path() / ("eps-snapshot-" + std::to_string(::getpid()));
+  std::filesystem::remove_all(dir);
+  HipCacheOptions o = SmallOptions(4096);
+  o.transfer_bytes = 64 << 10;  // 170 rows of dim 16 per staging half
+  o.state_bytes = 64 << 20;
+  HipCacheBackend gpu(o);
+  TableDefinition big{5, 16, 1, 1, {0.01f, 0.9f, 0.999f, 1e-8f, 0.9f, 0.999f}, -0.1f, 0.1f, 77};
+  big.optimizer.weight_bounds = WeightBounds{-0.5f, 0.5f};
+  const TableDefinition empty = Table(2, 64), host_only = Table(9, 8);
+  Take(gpu.Define(big));
+  Take(gpu.Define(empty));
+  std::map<std::pair<TableId, Key>, RowState> expect;
+  std::vector<RowState> host_rows;
+  std::vector<Key> order;
+  for (Key k = 0; k < 3000; ++k) order.push_back((k * 1777) % 3001 + 1);  // a permutation of 1..3001 minus one
+  std::vector<RowState> device;
+  for (Key key : order) {
+    RowState r = MakeRow(5, key, 16);
+    expect[{5, key}] = r;
+    (key % 3 == 0 ? host_rows : device).push_back(r);
+  }
+  for (std::size_t b = 0; b < device.size(); b += 300) {
+    std::vector<RowState> part(device.begin() + b, device.begin() + std::min(device.size(), b + 300));
+    Take(gpu.Load(Plan(part), part));
+  }
+  std::vector<Key> keys2 = {40, 8, 16}, keys9 = {3, 1, 2};
+  for (Key key : keys2) host_rows.push_back(expect[{2, key}] = MakeRow(2, key, 64));
+  for (Key key : keys9) host_rows.push_back(expect[{9, key}] = MakeRow(9, key, 8));
+  std::vector<SnapshotTable> tables = {{big, 12, 0.2f, 0.3f, order}, {empty, 0, 0.9f, 0.999f, keys2},
+                                       {host_only, 5, 0.5f, 0.6f, keys9}};
+  const SnapshotIdentity id{"run-hip", 0, 1, 1};
+  const auto file = dir / "step" / "shard-0.bin";
+  const SnapshotFile written = Take(gpu.WriteSnapshot(file, id, tables, host_rows));
+  Check(written.device_rows == device.size() && written.bytes == std::filesystem::file_size(file) &&
+            !std::filesystem::exists(file.string() + ".pending"),
+        "snapshot file summary");
+
+  // The oracle reads it back (checksum, identity, schema, every row) ...
+  char run[1025];
+  std::uint64_t shard = 0, count = 0, epoch = 0, checksum = 0;
+  std::uint32_t version = 0, ntables = 0;
+  eps_or_store* stores[8] = {};
+  Check(eps_or_snapshot_read(file.c_str(), run, sizeof run, &shard, &count, &epoch, &version, stores, 8,
+                             &ntables, &checksum) == 0,
+        std::string("oracle rejected the snapshot: ") + eps_or_last_error());
+  Check(std::string(run) == id.run && shard == 0 && count == 1 && epoch == 1 && version == 2 &&
+            ntables == 3 && checksum == written.checksum,
+        "snapshot identity");
+  for (std::uint32_t t = 0; t < ntables; ++t) {
+    const auto& want = tables[t];
+    float b1 = 0, b2 = 0;
+    std::uint64_t seq = 0;
+    eps_or_powers(stores[t], &b1, &b2, &seq);
+    Check(b1 == want.beta1_power && b2 == want.beta2_power && seq == want.optimizer_sequence &&
+              eps_or_row_count(stores[t]) == want.keys.size(),
+          "snapshot table clock");
+    const std::uint32_t dim = want.definition.dimension;
+    for (std::size_t i = 0; i < want.keys.size(); ++i) {
+      const Key key = want.keys[i];
+      Check(eps_or_key_at(stores[t], i) == key, "snapshot row order");
+      std::vector<float> w(dim), m(dim), v(dim);
+      std::uint64_t updates = 0;
+      Check(eps_or_read(stores[t], key, w.data(), m.data(), v.data(), &updates) == 0, "snapshot row missing");
+      const RowState& r = expect.at({want.definition.id, key});
+      Check(SameBits(w, r.weights) && SameBits(m, r.first_moment) && SameBits(v, r.second_moment) &&
+                updates == r.row_updates,
+            "snapshot row differs");
+    }
+  }
+  // ... and its own writer, given the same content, produces the same bytes.
+  const auto again = dir / "oracle.bin";
+  Check(eps_or_snapshot_write(again.c_str(), run, shard, count, epoch, stores, ntables) == 0, "oracle writer");
+  Check(FileBytes(again) == FileBytes(file), "snapshot bytes differ from the oracle writer's");
+  for (std::uint32_t t = 0; t < ntables; ++t) eps_or_destroy(stores[t]);
+
+  // Published files are immutable; bad requests are refused before any I/O.
+  const std::string before = FileBytes(file);
+  Check(Fails(gpu.WriteSnapshot(file, id, tables, host_rows), "overwrite") == Error::Code::unavailable,
+        "snapshot overwrite code");
+  Check(FileBytes(file) == before && !std::filesystem::exists(file.string() + ".pending"),
+        "refused overwrite changed the snapshot");
+  auto dup = tables;
+  dup[2].keys.push_back(3);
+  Check(Fails(gpu.WriteSnapshot(dir / "dup.bin", id, dup, host_rows), "duplicate key") ==
+            Error::Code::invalid_argument,
+        "duplicate key code");
+  auto twice = host_rows;
+  twice.push_back(MakeRow(5, order[0] % 3 == 0 ? order[1] : order[0], 16));
+  Fails(gpu.WriteSnapshot(dir / "twice.bin", id, tables, twice), "row held twice");
+  auto missing = tables;
+  missing[1].keys.push_back(77);
+  Fails(gpu.WriteSnapshot(dir / "missing.bin", id, missing, host_rows), "missing row");
+  Fails(gpu.WriteSnapshot(dir / "bad.bin", {"run-hip", 1, 1, 1}, tables, host_rows), "shard out of range");
+  for (const char* name : {"dup.bin", "twice.bin", "missing.bin", "bad.bin"})
+    Check(!std::filesystem::exists(dir / name), "refused snapshot left a file");
+  std::filesystem::remove_all(dir);
+}
+
 void Main() {
   AtomicReserve();
+  SnapshotWriteback();
   auto gpu = std::make_shared<HipCacheBackend>(SmallOptions(8));
   for (const auto& t : {Table(1, 128), Table(2, 64)}) Take(gpu->Define(t));
   Take(gpu->Define(Table(1, 128)));  // identical redefinition is accepted
@@ -519,8 +644,8 @@ int main() {
   try {
     Main();
     std::cout << "PASS HIP backend: " << g_checks
-              << " checks (gathers, optimizer states, device push, atomic rejection, slot reuse, "
-                 "assembly, device-result lifetime)\n";
+              << " checks (gathers, optimizer states, device push, snapshot writeback, atomic "
+                 "rejection, slot reuse, assembly, device-result lifetime)\n";
     return 0;
   } catch (const std::exception& e) {
     std::cerr << "FAIL HIP backend: " << e.what() << '\n';
