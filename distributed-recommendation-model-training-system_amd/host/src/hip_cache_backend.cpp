@@ -934,9 +934,11 @@ std::future<Result<Ack>> HipCacheBackend::PushDevice(std::vector<UpdateContext> 
     auto* index = I.host_indices.As<std::uint64_t>();
     std::uint64_t used = 0, occurrences = 0;
     std::uint32_t table_count = 0;
+    std::set<std::uint32_t> features;
     for (const auto& task : work) {
       auto it = std::find_if(layouts.begin(), layouts.end(),
                              [&](const FeatureInput& f) { return f.feature == task.feature; });
+      Require(features.insert(task.feature).second, "duplicate HIP push feature");
       Require(it != layouts.end() && task.agent == I.options.agent &&
                   task.route == AccessRoute::resident_gpu && task.transferred_weights.empty(),
               "invalid HIP push work");

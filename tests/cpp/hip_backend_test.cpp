@@ -375,6 +375,9 @@ void DevicePush(HipCacheBackend& gpu, const std::vector<LocatedRow>& located, Mo
             Error::Code::invalid_argument,
         "gradient shape code");
   Fails(gpu.PushDevice({contexts[0]}, work, layouts, Upload(layouts, g)), "push without a table context");
+  auto twice = work;
+  twice[1] = work[0];  // feature 0 twice, feature 1's gradient unused
+  Fails(gpu.PushDevice(contexts, twice, layouts, Upload(layouts, g)), "a feature pushed twice");
   auto stale = work;
   stale[2].rows[0].generation += 1;
   Check(Fails(gpu.PushDevice(contexts, stale, layouts, Upload(layouts, g)), "stale device push") ==
