@@ -16,6 +16,7 @@ constexpr uint64_t kHole = ~0ull;         // "row not on this device" (UINT64_MA
 constexpr uint32_t kBoundSlots = 64;      // spread of the bound atomics
 constexpr uint32_t kSortTile = 4096;      // keys per radix-sort tile (256 x 16)
 constexpr uint32_t kSortItems = 16;
+constexpr uint32_t kGroupTiles = 16;     // radix tiles per look-back group
 constexpr uint32_t kMaxPasses = 4;
 constexpr uint32_t kRadixBits = 9;        // largest radix digit
 constexpr uint32_t kDigits = 1u << kRadixBits;
@@ -63,18 +64,20 @@ struct HotEntry { uint32_t start, end, key, pad; };
 
 // Workspace layout of a push, for `n` occurrences.
 struct PushLayout {
-  uint64_t n, tiles;
-  uint64_t hist, look, keys_a, keys_b, vals_a, vals_b, refscale, sorted_rs, flags, ranks,
-      block_sums, long_list, total;
+  uint64_t n, tiles, groups;
+  uint64_t hist, look, group_look, keys_a, keys_b, vals_a, vals_b, refscale, sorted_rs, flags,
+      ranks, block_sums, long_list, total;
   // Capacity of each hot-row list (any one may hold every hot row).
   uint64_t HotCapacity() const { return n / kLongRefs + 1; }
   explicit PushLayout(uint64_t occurrences) {
     n = occurrences;
     tiles = (n + kSortTile - 1) / kSortTile;
+    groups = (tiles + kGroupTiles - 1) / kGroupTiles;
     auto align = [](uint64_t x) { return (x + 255) & ~uint64_t(255); };
     uint64_t at = sizeof(Control);
     hist = at; at = align(at + kHistCopies * kMaxPasses * kDigits * 4);
     look = at; at = align(at + kMaxPasses * tiles * kDigits * 4);
+    group_look = at; at = align(at + kMaxPasses * groups * kDigits * 4);
     keys_a = at; at = align(at + n * 4);
     keys_b = at; at = align(at + n * 4);
     vals_a = at; at = align(at + n * 4);

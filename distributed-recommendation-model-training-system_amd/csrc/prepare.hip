@@ -13,8 +13,8 @@
 //            (gradient row | scale) reference word, all-pass digit histograms,
 //            per-class valid counts, max |scale|.
 //   passes : onesweep (single pass per digit): per-tile stable ranking with
-//            wavefront ballots, decoupled look-back across tiles for the digit
-//            prefix, LDS-staged scatter so each digit run is written
+//            wavefront ballots, two-level decoupled look-back (over groups of
+//            tiles) for the digit prefix, LDS-staged scatter so each digit run is written
 //            contiguously.  The last pass also scatters the reference words.
 //   unique : first-occurrence ranks (PrepareFeature's unique order) from a
 //            head-flag scan in occurrence space.
@@ -31,7 +31,7 @@ namespace {
 constexpr uint32_t kFlagAggregate = 1u << 30;
 constexpr uint32_t kFlagInclusive = 2u << 30;
 constexpr uint32_t kValueMask = (1u << 30) - 1;
-constexpr uint32_t kLookWindow = 16;  // predecessor tiles read per look-back round
+constexpr uint32_t kLookWindow = 16;  // predecessor groups read per look-back round
 constexpr uint32_t kStageBags = 2048;   // bag offsets a keygen block stages in LDS
 
 struct PrepFeature {
@@ -212,7 +212,7 @@ __global__ void __launch_bounds__(kBlock) RadixPassKernel(
     uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out,
     const uint64_t* __restrict__ rs_in, uint64_t* __restrict__ rs_out, uint32_t n,
     uint32_t shift, uint32_t bits, const uint32_t* __restrict__ hist, uint32_t* look,
-    uint32_t* tile_counter) {
+    uint32_t* group_look, uint32_t tiles, uint32_t* tile_counter) {
   __shared__ uint32_t s_tile;
   __shared__ uint32_t s_wcount[4][kDigits];
   __shared__ uint32_t s_tile_start[kDigits];
@@ -281,63 +281,100 @@ __global__ void __launch_bounds__(kBlock) RadixPassKernel(
       total[j] += c;
     }
   }
+  // Two-level look-back.  Tiles form groups of kGroupTiles; every tile
+  // publishes its digit counts.  A tile's exclusive prefix is the counts of
+  // the tiles before it in its group plus the prefix of the groups before
+  // its group.  The group's last tile publishes the group total, then (after
+  // its own walk) the group's inclusive prefix.  The walk over groups is
+  // windowed and stops at the first inclusive prefix, as a tile-level
+  // look-back would, but the chain runs through groups, not tiles.  A tile
+  // waits only on tiles claimed before it (the tile counter hands tiles out in
+  // order), so the waits always end.
+  const uint32_t group = tile / kGroupTiles, first = group * kGroupTiles;
+  const bool leader = tile + 1 == min(first + kGroupTiles, tiles);
   uint32_t* mine = look + uint64_t(tile) * kDigits + kDigitsPerThread * t;
-  if (tile == 0) {
 #pragma unroll
-    for (uint32_t j = 0; j < kDigitsPerThread; ++j)
-      __hip_atomic_store(mine + j, kFlagInclusive | total[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  } else {
+  for (uint32_t j = 0; j < kDigitsPerThread; ++j)
+    __hip_atomic_store(mine + j, kFlagAggregate | total[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // Counts of the tiles before this one in its group (all published or about to be).
+  uint32_t within[kDigitsPerThread] = {0, 0};
+  {
+    uint32_t missing = (1u << (tile - first)) - 1;  // bit w: tile first + w still to add
+    while (missing) {
+      uint32_t v[kDigitsPerThread][kGroupTiles];
 #pragma unroll
-    for (uint32_t j = 0; j < kDigitsPerThread; ++j)
-      __hip_atomic_store(mine + j, kFlagAggregate | total[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // Windowed look-back, both digits together: each round reads the next
-    // kLookWindow predecessors of every unfinished digit at once and adds
-    // their counts, nearest first, up to the first inclusive prefix (done) or
-    // the first tile that has not published yet (read again from there).
-    // Tile 0 always publishes inclusive prefixes, so each walk ends at or
-    // before it; reads before tile 0 are never issued.
-    int64_t next[kDigitsPerThread];
-    bool done[kDigitsPerThread];
+      for (uint32_t w = 0; w < kGroupTiles; ++w)
 #pragma unroll
-    for (uint32_t j = 0; j < kDigitsPerThread; ++j) { next[j] = int64_t(tile) - 1; done[j] = false; }
-    while (!done[0] || !done[1]) {
-      uint32_t v[kDigitsPerThread][kLookWindow];
-#pragma unroll
-      for (uint32_t j = 0; j < kDigitsPerThread; ++j)
-#pragma unroll
-        for (uint32_t w = 0; w < kLookWindow; ++w) {
-          const int64_t q = next[j] - int64_t(w);
-          v[j][w] = (!done[j] && q >= 0)
-                        ? __hip_atomic_load(look + uint64_t(q) * kDigits + kDigitsPerThread * t + j,
+        for (uint32_t j = 0; j < kDigitsPerThread; ++j)
+          v[j][w] = (missing >> w) & 1u
+                        ? __hip_atomic_load(look + uint64_t(first + w) * kDigits + kDigitsPerThread * t + j,
                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                        : kFlagInclusive;
-        }
+                        : 0u;
 #pragma unroll
-      for (uint32_t j = 0; j < kDigitsPerThread; ++j) {
-        if (done[j]) continue;
-        bool stop = false;
-        uint32_t taken = 0;
+      for (uint32_t w = 0; w < kGroupTiles; ++w) {
+        if (!((missing >> w) & 1u) || !(v[0][w] & ~kValueMask) || !(v[1][w] & ~kValueMask)) continue;
 #pragma unroll
-        for (uint32_t w = 0; w < kLookWindow; ++w) {
-          const uint32_t flag = v[j][w] & ~kValueMask;
-          if (!stop) {
-            if (flag == 0) {
-              stop = true;  // not published yet
-            } else {
-              exclusive[j] += v[j][w] & kValueMask;
-              ++taken;
-              if (flag == kFlagInclusive) stop = done[j] = true;
-            }
-          }
-        }
-        next[j] -= int64_t(taken);
+        for (uint32_t j = 0; j < kDigitsPerThread; ++j) within[j] += v[j][w] & kValueMask;
+        missing &= ~(1u << w);
       }
     }
+  }
+  uint32_t* group_mine = group_look + uint64_t(group) * kDigits + kDigitsPerThread * t;
+  if (leader)
 #pragma unroll
     for (uint32_t j = 0; j < kDigitsPerThread; ++j)
-      __hip_atomic_store(mine + j, kFlagInclusive | (exclusive[j] + total[j]), __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(group_mine + j, (group == 0 ? kFlagInclusive : kFlagAggregate) | (within[j] + total[j]),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // Windowed walk over the groups before this one: each round reads the
+  // next kLookWindow predecessors of every unfinished digit at once and adds
+  // their counts, nearest first, up to the first inclusive prefix (done) or
+  // the first group that has not published yet (read again from there).
+  // Group 0 always publishes an inclusive prefix, so each walk ends at or
+  // before it; reads before group 0 are never issued.
+  int64_t next[kDigitsPerThread];
+  bool done[kDigitsPerThread];
+#pragma unroll
+  for (uint32_t j = 0; j < kDigitsPerThread; ++j) { next[j] = int64_t(group) - 1; done[j] = group == 0; }
+  while (!done[0] || !done[1]) {
+    uint32_t v[kDigitsPerThread][kLookWindow];
+#pragma unroll
+    for (uint32_t j = 0; j < kDigitsPerThread; ++j)
+#pragma unroll
+      for (uint32_t w = 0; w < kLookWindow; ++w) {
+        const int64_t q = next[j] - int64_t(w);
+        v[j][w] = (!done[j] && q >= 0)
+                      ? __hip_atomic_load(group_look + uint64_t(q) * kDigits + kDigitsPerThread * t + j,
+                                          __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                      : kFlagInclusive;
+      }
+#pragma unroll
+    for (uint32_t j = 0; j < kDigitsPerThread; ++j) {
+      if (done[j]) continue;
+      bool stop = false;
+      uint32_t taken = 0;
+#pragma unroll
+      for (uint32_t w = 0; w < kLookWindow; ++w) {
+        const uint32_t flag = v[j][w] & ~kValueMask;
+        if (!stop) {
+          if (flag == 0) {
+            stop = true;  // not published yet
+          } else {
+            exclusive[j] += v[j][w] & kValueMask;
+            ++taken;
+            if (flag == kFlagInclusive) stop = done[j] = true;
+          }
+        }
+      }
+      next[j] -= int64_t(taken);
+    }
   }
+  if (leader && group != 0)
+#pragma unroll
+    for (uint32_t j = 0; j < kDigitsPerThread; ++j)
+      __hip_atomic_store(group_mine + j, kFlagInclusive | (exclusive[j] + within[j] + total[j]),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+  for (uint32_t j = 0; j < kDigitsPerThread; ++j) exclusive[j] += within[j];
   // Exclusive scans in digit order: thread t's pair (2t, 2t+1) is one scan item.
   const uint32_t digit_base = BlockExclusiveScan(digit_count[0] + digit_count[1], s_scan);
   const uint32_t tile_start = BlockExclusiveScan(total[0] + total[1], s_scan);
@@ -674,12 +711,14 @@ int eps_hip_prepare(const eps_hip_table* tables, uint32_t table_count,
   uint32_t* keys[2] = {reinterpret_cast<uint32_t*>(ws + L.keys_a), reinterpret_cast<uint32_t*>(ws + L.keys_b)};
   uint32_t* vals[2] = {reinterpret_cast<uint32_t*>(ws + L.vals_a), reinterpret_cast<uint32_t*>(ws + L.vals_b)};
   auto* look = reinterpret_cast<uint32_t*>(ws + L.look);
+  auto* group_look = reinterpret_cast<uint32_t*>(ws + L.group_look);
   const uint32_t n = uint32_t(plan.occurrences);
   for (uint32_t p = 0; p < plan.passes; ++p) {
     hipLaunchKernelGGL(RadixPassKernel, dim3(unsigned(L.tiles)), dim3(kBlock), 0, s, keys[p % 2], vals[p % 2],
                        keys[(p + 1) % 2], vals[(p + 1) % 2], rs[p % 2], rs[(p + 1) % 2], n,
                        plan.shift[p], plan.bits[p],
                        args.hist + p * kDigits, look + uint64_t(p) * L.tiles * kDigits,
+                       group_look + uint64_t(p) * L.groups * kDigits, uint32_t(L.tiles),
                        &ctrl->tile_counter[p]);
     EPS_HIP_LAUNCHED("radix pass");
   }
