@@ -1087,39 +1087,12 @@ std::future<Result<SnapshotFile>> HipCacheBackend::WriteSnapshot(std::filesystem
     }
 
     hip_detail::SnapshotWriter out(file);
-    out.U64(hip_detail::SnapshotWriter::kMagicV2);
-    out.String(identity.run);
-    out.U64(identity.shard);
-    out.U64(identity.shard_count);
-    out.U64(identity.epoch);
-    out.U64(tables.size());
+    hip_detail::WriteSnapshotHeader(out, identity, tables.size());
     Event ready[2] = {Event(I.options.device), Event(I.options.device)};
     const std::uint64_t half_bytes = I.options.transfer_bytes / 2;
     for (const auto& t : tables) {
       const auto& d = t.definition;
-      const auto& o = d.optimizer;
-      out.U64(d.id);
-      out.U64(d.dimension);
-      out.U64(d.shard_count);
-      out.U64(d.partition_epoch);
-      out.F32(o.learning_rate);
-      out.F32(o.beta1);
-      out.F32(o.beta2);
-      out.F32(o.epsilon);
-      out.F32(o.initial_beta1_power);
-      out.F32(o.initial_beta2_power);
-      out.U64(o.weight_bounds ? 1 : 0);
-      if (o.weight_bounds) {
-        out.F32(o.weight_bounds->minimum);
-        out.F32(o.weight_bounds->maximum);
-      }
-      out.F32(d.initialization_min);
-      out.F32(d.initialization_max);
-      out.U64(d.initialization_seed);
-      out.U64(t.optimizer_sequence);
-      out.F32(t.beta1_power);
-      out.F32(t.beta2_power);
-      out.U64(t.keys.size());
+      hip_detail::WriteSnapshotTable(out, t);
       auto it = I.tables.find(d.id);
       Impl::Table* table = it == I.tables.end() ? nullptr : it->second.get();
       const std::uint64_t floats = std::uint64_t(d.dimension) * 3;
@@ -1162,20 +1135,14 @@ std::future<Result<SnapshotFile>> HipCacheBackend::WriteSnapshot(std::filesystem
           std::uint64_t n = 0;
           for (std::size_t i = chunks[c].first; i < chunks[c].second; ++i) {
             const Key key = t.keys[i];
-            out.U64(key);
             const Impl::Entry* entry = nullptr;
             if (table)
               if (auto r = table->rows.find(key); r != table->rows.end()) entry = &r->second;
             if (entry) {
-              out.U64(entry->updates);
-              out.Bytes(staged + n * floats, floats * 4);
+              hip_detail::WriteSnapshotRow(out, key, entry->updates, staged + n * floats, d.dimension);
               ++n;
             } else {
-              const RowState& row = *host.at({d.id, key});
-              out.U64(row.row_updates);
-              out.Bytes(row.weights.data(), d.dimension * 4);
-              out.Bytes(row.first_moment.data(), d.dimension * 4);
-              out.Bytes(row.second_moment.data(), d.dimension * 4);
+              hip_detail::WriteSnapshotRow(out, *host.at({d.id, key}));
             }
           }
         }

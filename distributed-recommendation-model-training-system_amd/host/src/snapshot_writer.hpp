@@ -26,6 +26,7 @@
 #include <thread>
 #include <vector>
 
+#include "eps/hip_cache_backend.hpp"
 #include "executor.hpp"
 
 namespace eps::hip_detail {
@@ -168,5 +169,59 @@ class SnapshotWriter {
   bool busy_ = false, stop_ = false, io_failed_ = false;
   std::thread io_;
 };
+
+// The stream's fields in WriteSnapshot's order (src/store/snapshot.cpp:164-185):
+// the identity and table count, then per table Binary::Definition (:77-98,
+// with the weight-bounds flag of format 2), the optimizer clock and the row
+// count, then per row its key, update counter and 3 x dim floats [w | m | v].
+inline void WriteSnapshotHeader(SnapshotWriter& out, const SnapshotIdentity& id, std::uint64_t tables) {
+  out.U64(SnapshotWriter::kMagicV2);
+  out.String(id.run);
+  out.U64(id.shard);
+  out.U64(id.shard_count);
+  out.U64(id.epoch);
+  out.U64(tables);
+}
+inline void WriteSnapshotTable(SnapshotWriter& out, const SnapshotTable& t) {
+  const auto& d = t.definition;
+  const auto& o = d.optimizer;
+  out.U64(d.id);
+  out.U64(d.dimension);
+  out.U64(d.shard_count);
+  out.U64(d.partition_epoch);
+  out.F32(o.learning_rate);
+  out.F32(o.beta1);
+  out.F32(o.beta2);
+  out.F32(o.epsilon);
+  out.F32(o.initial_beta1_power);
+  out.F32(o.initial_beta2_power);
+  out.U64(o.weight_bounds ? 1 : 0);
+  if (o.weight_bounds) {
+    out.F32(o.weight_bounds->minimum);
+    out.F32(o.weight_bounds->maximum);
+  }
+  out.F32(d.initialization_min);
+  out.F32(d.initialization_max);
+  out.U64(d.initialization_seed);
+  out.U64(t.optimizer_sequence);
+  out.F32(t.beta1_power);
+  out.F32(t.beta2_power);
+  out.U64(t.keys.size());
+}
+// One row whose [w | m | v] floats lie contiguously (the device layout).
+inline void WriteSnapshotRow(SnapshotWriter& out, Key key, std::uint64_t updates, const float* wmv,
+                             std::uint32_t dim) {
+  out.U64(key);
+  out.U64(updates);
+  out.Bytes(wmv, std::size_t(dim) * 12);
+}
+// One row held as three vectors (a CPU store's RowState).
+inline void WriteSnapshotRow(SnapshotWriter& out, const RowState& row) {
+  out.U64(row.row.key);
+  out.U64(row.row_updates);
+  out.Bytes(row.weights.data(), row.weights.size() * 4);
+  out.Bytes(row.first_moment.data(), row.first_moment.size() * 4);
+  out.Bytes(row.second_moment.data(), row.second_moment.size() * 4);
+}
 
 }  // namespace eps::hip_detail
