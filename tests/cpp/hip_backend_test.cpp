@@ -428,9 +428,10 @@ void SnapshotWriteback() {
     expect[{5, key}] = r;
     (key % 3 == 0 ? host_rows : device).push_back(r);
   }
+  std::map<Key, LocatedRow> where;  // table 5 rows as the backend placed them
   for (std::size_t b = 0; b < device.size(); b += 300) {
     std::vector<RowState> part(device.begin() + b, device.begin() + std::min(device.size(), b + 300));
-    Take(gpu.Load(Plan(part), part));
+    for (const auto& loc : Take(gpu.Load(Plan(part), part))) where[loc.row.key] = loc;
   }
   std::vector<Key> keys2 = {40, 8, 16}, keys9 = {3, 1, 2};
   for (Key key : keys2) host_rows.push_back(expect[{2, key}] = MakeRow(2, key, 64));
@@ -480,6 +481,45 @@ void SnapshotWriteback() {
   const auto again = dir / "oracle.bin";
   Check(eps_or_snapshot_write(again.c_str(), run, shard, count, epoch, stores, ntables) == 0, "oracle writer");
   Check(FileBytes(again) == FileBytes(file), "snapshot bytes differ from the oracle writer's");
+
+  // Restore and resume (tests/core_tests.cpp:107-129): a fresh backend loaded
+  // with the snapshot's rows and the original take the same update and end
+  // bit-identical, counters included.
+  {
+    HipCacheBackend restored(o);
+    Take(restored.Define(big));
+    std::vector<RowState> rows;
+    for (Key key : order) {
+      RowState r{{5, key}, std::vector<float>(16), std::vector<float>(16), std::vector<float>(16), 0};
+      Check(eps_or_read(stores[0], key, r.weights.data(), r.first_moment.data(), r.second_moment.data(),
+                        &r.row_updates) == 0,
+            "snapshot row");
+      rows.push_back(std::move(r));
+    }
+    std::map<Key, LocatedRow> where_restored;
+    for (std::size_t b = 0; b < rows.size(); b += 300) {
+      std::vector<RowState> part(rows.begin() + b, rows.begin() + std::min(rows.size(), b + 300));
+      for (const auto& loc : Take(restored.Load(Plan(part), part))) where_restored[loc.row.key] = loc;
+    }
+    RowGradients g;
+    MigrationPlan before{"read", 0, {}, Placement::cpu, 0}, after = before;
+    for (std::size_t i = 0; i < device.size(); i += 97) {
+      g.rows.push_back(device[i].row);
+      for (int d = 0; d < 16; ++d) g.values.push_back(0.3f * std::cos(float(i + d)));
+      before.rows.push_back(where.at(device[i].row.key));
+      after.rows.push_back(where_restored.at(device[i].row.key));
+    }
+    const UpdateContext c{{"resume", 0, 12, Phase::push}, 0, 5, 12, 0.01f, 0.2f, 0.3f};
+    Take(gpu.ApplyHost(c, g));
+    Take(restored.ApplyHost(c, g));
+    const auto a = Take(gpu.ReadBack(before)), b = Take(restored.ReadBack(after));
+    for (std::size_t i = 0; i < a.size(); ++i)
+      Check(a[i].row == b[i].row && SameBits(a[i].weights, b[i].weights) &&
+                SameBits(a[i].first_moment, b[i].first_moment) &&
+                SameBits(a[i].second_moment, b[i].second_moment) && a[i].row_updates == b[i].row_updates &&
+                a[i].row_updates == expect.at({5, a[i].row.key}).row_updates + 1,
+            "resumed training diverged from the original");
+  }
   for (std::uint32_t t = 0; t < ntables; ++t) eps_or_destroy(stores[t]);
 
   // Published files are immutable; bad requests are refused before any I/O.
