@@ -114,6 +114,81 @@ def cpu_baseline(wl, batches, budget_s=15.0, max_steps=8):
                       f"one shard on one thread ({'reference sources' if kind == 'reference' else 'C restatement'})"}
 
 
+class _ShardFeature:
+    """One shard's part of a feature: its keys (key % shards == shard) with the
+    bags' offsets recounted and the original valid lengths kept, as the
+    reference client routes a lookup (src/access/prepared_lookup.cpp:47-83)."""
+
+    def __init__(self, f, shard, shards):
+        keys = np.asarray(f.keys, np.uint64)
+        mine = keys % np.uint64(shards) == np.uint64(shard)
+        counts = np.add.reduceat(mine.astype(np.uint64), np.asarray(f.offsets[:-1], np.int64)) \
+            if len(keys) else np.zeros(len(f.valid_lengths), np.uint64)
+        counts[np.asarray(f.offsets[1:]) == np.asarray(f.offsets[:-1])] = 0  # empty bags
+        self.keys = keys[mine]
+        self.offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.uint64)
+        self.valid_lengths = np.asarray(f.valid_lengths, np.uint64)
+        self.pooling, self.feature, self.table, self.weights = f.pooling, f.feature, f.table, None
+        self.gradient = f.gradient[mine] if f.pooling == 2 else f.gradient  # sequence rows follow keys
+
+    @property
+    def rows(self):
+        return len(self.keys) if self.pooling == 2 else len(self.valid_lengths)
+
+
+def cpu_baseline_shards(wl, batches, shards, budget_s=10.0, max_steps=8):
+    """The reference's own scale-out on the host: `shards` CPU shards (the
+    reference sources), one thread each, keys routed by key % shards; each
+    shard runs PrepareFeature and Push on its part, the client adds the
+    partial sums and divides the means.  Routing is done before timing."""
+    import threading
+
+    import oracle
+
+    if not oracle.ref_available():
+        return None
+    refs = [oracle.RefShard([oracle.table_def(id=t.id, dim=t.dim, lr=t.lr, b1p=t.b1p, b2p=t.b2p,
+                                              init_min=t.init_min, init_max=t.init_max, seed=t.seed,
+                                              shard=i, shard_count=shards) for t in wl.tables],
+                            shard=i, shard_count=shards) for i in range(shards)]
+    parts = [[[_ShardFeature(f, i, shards) for f in feats] for i in range(shards)] for feats in batches]
+
+    def step(k):
+        outs = [None] * shards
+
+        def run(i):
+            out = []
+            for f in parts[k][i]:
+                out.append(refs[i].prepare(wl.tables[f.table].id, f)[2])
+            assert refs[i].push([f.gradient for f in parts[k][i]]) == 0
+            outs[i] = out
+
+        threads = [threading.Thread(target=run, args=(i,)) for i in range(shards)]
+        for t in threads:
+            t.start()
+        for t in threads:
+            t.join()
+        for j, f in enumerate(batches[k]):  # client merge and mean divide
+            total = outs[0][j].copy()
+            for i in range(1, shards):
+                total += outs[i][j]
+            if f.pooling == oracle.MEAN:
+                oracle.mean_divide(total, f.valid_lengths)
+
+    step(0)  # first touch, untimed
+    done, lookups, t0 = 0, 0, time.perf_counter()
+    while done < max_steps and (time.perf_counter() - t0) < budget_s:
+        k = (done + 1) % len(batches)
+        step(k)
+        lookups += sum(len(f.keys) for f in batches[k])
+        done += 1
+    elapsed = time.perf_counter() - t0
+    return {"value": lookups / elapsed, "unit": "lookups/s", "cores": shards,
+            "ms_per_step": 1e3 * elapsed / done,
+            "sample": f"{done} steps after one untimed first-touch step, {shards} reference shards "
+                      f"on {shards} threads, key % {shards} routing done before timing"}
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -273,6 +348,11 @@ def main(argv=None):
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(wl, batches)
+        shards = min(16, os.cpu_count() or 1)  # the host share of one GPU
+        if shards > 1:
+            all_cores = cpu_baseline_shards(wl, batches, shards)
+            if all_cores:
+                result["cpu_baseline"]["all_cores"] = all_cores
     print(json.dumps(result))
     return 0
 
