@@ -154,20 +154,26 @@ def cpu_baseline_shards(wl, batches, shards, budget_s=10.0, max_steps=8):
     parts = [[[_ShardFeature(f, i, shards) for f in feats] for i in range(shards)] for feats in batches]
 
     def step(k):
-        outs = [None] * shards
+        outs, errors = [None] * shards, []
 
         def run(i):
-            out = []
-            for f in parts[k][i]:
-                out.append(refs[i].prepare(wl.tables[f.table].id, f)[2])
-            assert refs[i].push([f.gradient for f in parts[k][i]]) == 0
-            outs[i] = out
+            try:
+                out = []
+                for f in parts[k][i]:
+                    out.append(refs[i].prepare(wl.tables[f.table].id, f)[2])
+                if refs[i].push([f.gradient for f in parts[k][i]]) != 0:
+                    raise RuntimeError(f"reference shard {i} rejected its push: {refs[i].error()}")
+                outs[i] = out
+            except Exception as e:  # surfaced on the calling thread
+                errors.append(e)
 
         threads = [threading.Thread(target=run, args=(i,)) for i in range(shards)]
         for t in threads:
             t.start()
         for t in threads:
             t.join()
+        if errors:
+            raise errors[0]
         for j, f in enumerate(batches[k]):  # client merge and mean divide
             total = outs[0][j].copy()
             for i in range(1, shards):
