@@ -387,6 +387,138 @@ void DevicePush(HipCacheBackend& gpu, const std::vector<LocatedRow>& located, Mo
                 "state after rejected device pushes");
 }
 
+// Device push at scale: three tables of 60,000 rows (dims 64, 64 bounded,
+// 128), four features (two on one table; mean and sum) of 2,048 bags of 1..20
+// skewed ids, so the hottest rows take thousands of references (the
+// hot-row kernel) and the rest the row-run kernel; ids past the loaded rows
+// are served elsewhere (holes).  Every touched row must match the oracle's
+// ReduceGradients + LazyAdam bit for bit, and an untouched row stays as it was.
+RowState MakeRow(TableId table, Key key, std::uint32_t dim);
+
+void DevicePushAtScale() {
+  HipCacheOptions o = SmallOptions(60000);
+  o.state_bytes = 256ull << 20;
+  o.transfer_bytes = 64ull << 20;  // a table's touched rows read back in one call
+  HipCacheBackend gpu(o);
+  std::vector<TableDefinition> defs = {Table(11, 64), Table(12, 64), Table(13, 128)};
+  defs[1].optimizer.weight_bounds = WeightBounds{-0.03f, 0.03f};
+  constexpr Key kLoaded = 59000, kIds = 60000;
+  std::map<std::pair<TableId, Key>, RowState> model;
+  std::map<std::pair<TableId, Key>, LocatedRow> where;
+  for (const auto& d : defs) {
+    Take(gpu.Define(d));
+    for (Key b = 0; b < kLoaded; b += 10000) {
+      std::vector<RowState> part;
+      for (Key k = b; k < std::min(kLoaded, b + 10000); ++k) {
+        RowState r = MakeRow(d.id, k, d.dimension);
+        model[{d.id, k}] = r;
+        part.push_back(r);
+      }
+      for (const auto& loc : Take(gpu.Load(Plan(part), part))) where[{loc.row.table, loc.row.key}] = loc;
+    }
+  }
+  std::uint64_t state = 12345;
+  auto next = [&]() {  // SplitMix64 stream
+    state += 0x9e3779b97f4a7c15ull;
+    std::uint64_t z = state;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+  };
+  struct Spec { TableId table; std::uint32_t feature; Pooling pooling; };
+  const std::vector<Spec> specs = {{11, 0, Pooling::mean}, {11, 1, Pooling::sum}, {12, 2, Pooling::sum},
+                                   {13, 3, Pooling::mean}};
+  std::vector<FeatureInput> layouts;
+  std::vector<AgentWork> work;
+  std::vector<std::vector<float>> grads;
+  for (const auto& sp : specs) {
+    FeatureInput f{sp.table, sp.feature, sp.pooling, {}, {0}, {}};
+    for (int b = 0; b < 2048; ++b) {
+      const std::uint64_t len = 1 + next() % 20;
+      for (std::uint64_t i = 0; i < len; ++i) {
+        const double u = double(next() >> 11) * 0x1.0p-53;
+        f.keys.push_back(Key(double(kIds) * u * u * u * u));  // skewed: key 0 is the hottest
+      }
+      f.offsets.push_back(f.keys.size());
+      f.valid_lengths.push_back(len + (b % 7 == 0 ? 2 : 0));  // some bags lost positions elsewhere
+    }
+    AgentWork w{sp.feature, AccessRoute::resident_gpu, 0, {}, std::vector<std::uint64_t>(f.keys.size()), {}};
+    std::map<Key, std::uint64_t> unique;
+    for (std::size_t i = 0; i < f.keys.size(); ++i) {
+      if (f.keys[i] >= kLoaded) { w.occurrence_to_unique[i] = UINT64_MAX; continue; }
+      auto [it, fresh] = unique.emplace(f.keys[i], w.rows.size());
+      if (fresh) w.rows.push_back(where.at({sp.table, f.keys[i]}));
+      w.occurrence_to_unique[i] = it->second;
+    }
+    const std::uint32_t dim = sp.table == 13 ? 128 : 64;
+    std::vector<float> g(f.valid_lengths.size() * dim);
+    for (auto& x : g) x = float(std::int64_t(next() % 2001) - 1000) * 1e-4f;
+    layouts.push_back(std::move(f));
+    work.push_back(std::move(w));
+    grads.push_back(std::move(g));
+  }
+  std::vector<UpdateContext> contexts;
+  std::map<TableId, std::pair<float, float>> powers;
+  for (const auto& d : defs) {
+    contexts.push_back({{"scale", 0, 1, Phase::push}, 0, d.id, 1, kLr, 0.81f, 0.998f});
+    powers[d.id] = {0.81f, 0.998f};
+  }
+  std::vector<DeviceTensorBlock> blocks;
+  for (std::size_t i = 0; i < layouts.size(); ++i) {
+    const std::uint64_t dim = layouts[i].table == 13 ? 128 : 64;
+    blocks.push_back({layouts[i].feature, {grads[i].size() / dim, dim}, std::make_shared<DeviceBuffer>(grads[i])});
+  }
+  Take(gpu.PushDevice(contexts, work, layouts, blocks));
+  // Expected: the reference's per-table reduce over every feature of the table, then Adam.
+  std::size_t touched = 0;
+  for (const auto& d : defs) {
+    eps_or_table_def def{};
+    def.id = d.id; def.dim = d.dimension; def.shard_count = 1;
+    eps_or_store* store = eps_or_create(&def);
+    std::vector<eps_or_feature> fs;
+    std::vector<const float*> gs;
+    std::uint64_t keys = 0;
+    for (std::size_t i = 0; i < layouts.size(); ++i) {
+      if (layouts[i].table != d.id) continue;
+      const auto& f = layouts[i];
+      fs.push_back({f.keys.data(), f.keys.size(), f.offsets.data(), f.valid_lengths.data(), nullptr,
+                    f.valid_lengths.size(), uint32_t(f.pooling), f.feature});
+      gs.push_back(grads[i].data());
+      keys += f.keys.size();
+    }
+    std::vector<std::uint64_t> row_keys(keys);
+    std::vector<float> values(keys * d.dimension);
+    std::uint64_t count = 0;
+    Check(eps_or_reduce_gradients(store, fs.data(), gs.data(), uint32_t(fs.size()), row_keys.data(),
+                                  values.data(), &count) == 0,
+          "oracle reduce at scale");
+    eps_or_destroy(store);
+    MigrationPlan read{"read", 0, {}, Placement::cpu, 0};
+    std::vector<std::uint64_t> mine;
+    for (std::uint64_t u = 0; u < count; ++u) {
+      if (row_keys[u] >= kLoaded) continue;
+      RowState& r = model.at({d.id, row_keys[u]});
+      Check(eps_or_adam_rows_ctx(r.weights.data(), r.first_moment.data(), r.second_moment.data(),
+                                 values.data() + u * d.dimension, 1, d.dimension, kBeta1, kBeta2, kEps, kLr,
+                                 powers[d.id].first, powers[d.id].second, d.optimizer.weight_bounds ? 1 : 0,
+                                 -0.03f, 0.03f) == 0,
+            "oracle Adam at scale");
+      ++r.row_updates;
+      read.rows.push_back(where.at({d.id, row_keys[u]}));
+    }
+    read.rows.push_back(where.at({d.id, kLoaded - 1}));  // untouched (ids near the end are rare)
+    for (const auto& got : Take(gpu.ReadBack(read))) {
+      const RowState& want = model.at({got.row.table, got.row.key});
+      Check(SameBits(got.weights, want.weights) && SameBits(got.first_moment, want.first_moment) &&
+                SameBits(got.second_moment, want.second_moment) && got.row_updates == want.row_updates,
+            "device push at scale differs from the oracle (table " + std::to_string(d.id) + ", key " +
+                std::to_string(got.row.key) + ")");
+      ++touched;
+    }
+  }
+  Check(touched > 10000, "device push at scale touched too few rows");
+}
+
 std::string FileBytes(const std::filesystem::path& p) {
   std::ifstream in(p, std::ios::binary);
   return {std::istreambuf_iterator<char>(in), std::istreambuf_iterator<char>()};
@@ -548,6 +680,7 @@ void SnapshotWriteback() {
 void Main() {
   AtomicReserve();
   SnapshotWriteback();
+  DevicePushAtScale();
   auto gpu = std::make_shared<HipCacheBackend>(SmallOptions(8));
   for (const auto& t : {Table(1, 128), Table(2, 64)}) Take(gpu->Define(t));
   Take(gpu->Define(Table(1, 128)));  // identical redefinition is accepted
