@@ -350,7 +350,13 @@ def main(argv=None):
                                "HotSliceKernel + RowRunKernel)", "bound": "hbm",
                      "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBPS, "traffic": traffic,
-                     "algorithmic_bytes_per_launch": mean["fused_bytes"]},
+                     "algorithmic_bytes_per_launch": mean["fused_bytes"],
+                     # measured HBM bytes (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated)
+                     # over the same duration
+                     "traffic_GBps": traffic / (fused_ms * 1e-3) / 1e9 if traffic else None},
+        # Occurrence-based pull rate: every pooled lookup reads one dim-wide row
+        # (N x d x 4 bytes, repeats included, most served by the caches).
+        "gather_effective_GBps": mean["lookups"] * wl.tables[0].dim * 4 / (gather_ms * 1e-3) / 1e9,
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(wl, batches)
