@@ -1130,7 +1130,8 @@ uint64_t SpanBlocks(uint64_t count) {
 
 constexpr int kPrimary = 1, kSecond = 2;
 constexpr uint64_t kVectorGrid = 4096;  // persistent grid cap of the vector kernels
-constexpr uint64_t kSecondGrid = 256;     // grid cap of the checked apply (usually exits at once)
+constexpr uint64_t kSecondGrid = 32;      // grid cap of the checked apply: it usually exits at
+                                          // once, and a small grid launches faster
 constexpr uint64_t kHotGrid = 512;      // two blocks per CU (LDS: four 17 KiB tiles per block)
 
 template <uint32_t kLog2G>
