@@ -1,29 +1,44 @@
 #!/usr/bin/env python3
 """Benchmark of the parameter-shard embedding step on one MI355X.
 
-Workload: 26 fp32 tables x 1,000,000 rows x dim 64, batch 4096 bags per table,
-bag length U{1..20}, ids Zipf(1.05); tables 0-12 sum pooling, 13-25 mean;
-per-bag gradients N(0, 1e-2); sparse Adam lr 1e-3, betas 0.9/0.999, eps 1e-8.
-One step = pooled pull of every table + device dedup of the lookup (radix sort,
-on a second stream, running ahead of the pull and push) + fused duplicate-id
-aggregation and Adam of every unique row.  Inputs (ids,
-offsets, lengths, gradients) are resident in HBM before the timed region;
-several pre-generated batches are cycled.
+`--config N` picks the workload (default 2, the headline one):
+  1  movielens : 2 tables (943, 1682 rows) x 32, 128 single-hot pairs per step.
+  2  criteo26  : 26 x 1,000,000 x 64, 4096 bags per table, lengths U{1..20},
+                 Zipf(1.05), 13 sum + 13 mean tables.
+  3  dup10m    : 1 x 10,000,000 x 128, 65,536 (row, gradient) pairs per step,
+                 Zipf(1.2); the step is the push alone (no pull).
+  4  large4    : 4 x 12,500,000 x 128 (77 GB of state), 262,144 bags x 32 per
+                 table, Zipf(1.1), mean pooling.
+  5  ragged8   : 8 tables, dims 16..256, rows 100k..5M, 8192 weighted-sum bags
+                 per table, Poisson(8) lengths, Zipf(1.05), plus cache-tier row
+                 moves: 5% of the touched rows admitted from pinned host memory
+                 (w, m, v) and as many written back, every step.
+All use sparse Adam lr 1e-3, betas 0.9/0.999, eps 1e-8, N(0, 1e-2) gradients.
 
-Prints one JSON line (rank 0).  `value` is pooled lookups/s; Adam rows/s, the
-step's algorithmic HBM bandwidth and its fraction of the 8 TB/s peak ride
-along.  `roofline` is the fused update kernel's own (HIP events on its stream);
-`cpu_baseline` times the reference CPU shard on the host over a bounded sample.
+One step (pipeline.StepPipeline) = pooled pull of every table + device dedup of
+the lookup (radix sort on a side stream, one batch ahead) + fused duplicate-id
+aggregation and Adam of every unique row (+ the tier moves of config 5).
+Inputs (ids, offsets, lengths, weights, gradients) are resident in HBM before
+the timed region; several pre-generated batches are cycled.
+
+Prints one JSON line.  `value` is pooled lookups/s (config 3: Adam rows/s);
+Adam rows/s, the step's algorithmic HBM bandwidth and its fraction of the
+8 TB/s peak ride along.  `roofline` is the fused update's own (HIP events on
+its stream, every FUSED_EVERY-th timed step); `cpu_baseline` times the
+reference CPU shard (or the oracle's C restatement of it) on the host over a
+bounded sample, on one core and on the GPU's share of host cores.
 """
 from __future__ import annotations
 
 import argparse
 import gc
 import json
+import math
 import os
 import pathlib
 import platform
 import sys
+import threading
 import time
 
 import numpy as np
@@ -35,9 +50,30 @@ from __graft_entry__ import package  # noqa: E402
 
 METRIC = "pooled lookups/s + Adam rows/s on 1 GPU; achieved HBM GB/s (% of peak)"
 HBM_PEAK_GBPS = 8000.0
-PROFILE_SUMMARY = ROOT / "profiles" / "fused_update_criteo26.md"
 COPY_BYTES = 1 << 30
 FUSED_EVERY = 5  # timed steps between two timings of the fused update
+HOST_SHARE = 16  # host cores of one GPU's share of the box
+
+CONFIGS = {
+    1: dict(workload="movielens", batches=4, steps=200, warmup=20, cpu_fraction=1.0,
+            desc="2 fp32 tables (943 and 1682 rows) x dim 32 (w|m|v AoS), 128 single-hot (user, item) "
+                 "pairs per step, explicit N(0, 0.01) initial weights, pull + device dedup + fused sparse Adam"),
+    2: dict(workload="criteo26", batches=4, steps=50, warmup=20, cpu_fraction=1.0,
+            desc="26 tables x 1,000,000 rows x dim 64 fp32 (w|m|v AoS), batch 4096 bags per table, bag "
+                 "length U{1..20}, Zipf(1.05), 13 sum + 13 mean pooling, pull + device dedup + fused "
+                 "sparse Adam (lr 1e-3, 0.9/0.999, 1e-8)"),
+    3: dict(workload="dup10m", batches=4, steps=50, warmup=10, cpu_fraction=1.0, pull=False,
+            desc="1 table x 10,000,000 rows x dim 128 fp32 (w|m|v AoS), 65,536 (row, gradient) pairs per "
+                 "step, Zipf(1.2), device sort + segment reduce + fused sparse Adam, t = 1..50"),
+    4: dict(workload="large4", batches=2, steps=10, warmup=3, cpu_fraction=1 / 64,
+            desc="4 tables x 12,500,000 rows x dim 128 fp32 (w|m|v AoS, 76.8 GB), 262,144 bags x 32 ids per "
+                 "table, Zipf(1.1), mean pooling, pull + device dedup + fused sparse Adam"),
+    5: dict(workload="ragged8", batches=4, steps=50, warmup=10, cpu_fraction=1.0, moves=True,
+            desc="8 fp32 tables, dims {16,32,64,96,128,192,256,256}, rows {100k,1M,5M,5M,2M,1M,500k,200k}, "
+                 "8192 weighted-sum bags per table, Poisson(8) lengths clipped to 1..64, Zipf(1.05), pull + "
+                 "device dedup + fused sparse Adam + tier moves (5% of touched rows admitted from pinned "
+                 "host memory with w/m/v, as many written back, per step)"),
+}
 
 
 def cpu_model() -> str:
@@ -50,85 +86,62 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def batch_stats(wl, feats):
-    unique = [len(np.unique(f.keys)) for f in feats]
+def make_workload(W, name):
+    return {"movielens": W.MovieLens, "criteo26": W.Criteo26, "dup10m": W.Dup10M,
+            "large4": W.Large4, "ragged8": W.Ragged8}[name]()
+
+
+def batch_stats(W, wl, feats, pull):
+    by_table = {}
+    for f in feats:
+        by_table.setdefault(f.table, []).append(f.keys)
+    unique_t = {t: len(np.unique(np.concatenate(k))) for t, k in by_table.items()}
+    unique = [unique_t[f.table] if i == min(j for j, g in enumerate(feats) if g.table == f.table) else 0
+              for i, f in enumerate(feats)]
+    pull_b, push_b = W.algorithmic_bytes(wl.tables, feats, unique)
     lookups = sum(len(f.keys) for f in feats)
-    bags = sum(len(f.valid_lengths) for f in feats)
-    pull, push = wl_bytes(wl, feats, unique)
-    fused = sum(u * wl.tables[f.table].dim * 24 + f.rows * wl.tables[f.table].dim * 4
-                for f, u in zip(feats, unique))
-    return dict(lookups=lookups, unique=sum(unique), bags=bags, pull_bytes=pull, push_bytes=push,
-                fused_bytes=fused)
+    fused = sum(u * wl.tables[f.table].dim * 24 for f, u in zip(feats, unique)) + \
+        sum(f.rows * wl.tables[f.table].dim * 4 for f in feats)
+    return dict(lookups=lookups, unique=sum(unique_t.values()), pull_bytes=pull_b if pull else 0,
+                push_bytes=push_b, fused_bytes=fused)
 
 
-def wl_bytes(wl, feats, unique):
-    W = package().workloads
-    return W.algorithmic_bytes(wl.tables, feats, unique)
+# ---------------------------------------------------------------------------
+# CPU baseline: the reference's own CPU shard sources (oracle/_ref) where they
+# cover the workload, else the oracle's C restatement of them.
+def sample(feats, fraction):
+    """The first ceil(bags * fraction) bags of each feature (ids, lengths,
+    weights and gradient rows with them)."""
+    if fraction >= 1.0:
+        return feats
+    out = []
+    for f in feats:
+        bags = max(1, int(math.ceil(len(f.valid_lengths) * fraction)))
+        end = int(f.offsets[bags])
+        seq = f.pooling == 2
+        out.append(type(f)(f.table, f.feature, f.pooling, f.keys[:end], f.offsets[:bags + 1].copy(),
+                           f.valid_lengths[:bags], None if f.weights is None else f.weights[:end],
+                           f.gradient[:end] if seq else f.gradient[:bags]))
+    return out
 
 
-def cpu_baseline(wl, batches, budget_s=15.0, max_steps=8):
-    """Reference CPU shard (Lookup: PrepareFeature + client mean; Push:
-    ReduceGradients + ValidateLazyAdam + ApplyLazyAdam) on one core."""
-    import oracle
-
-    if oracle.ref_available():
-        kind = "reference"
-        defs = [oracle.table_def(id=t.id, dim=t.dim, lr=t.lr, b1p=t.b1p, b2p=t.b2p,
-                                 init_min=t.init_min, init_max=t.init_max, seed=t.seed)
-                for t in wl.tables]
-        shard = oracle.RefShard(defs)
-
-        def step(feats):
-            for f in feats:
-                _, _, c = shard.prepare(wl.tables[f.table].id, f)
-                if f.pooling == oracle.MEAN:
-                    oracle.mean_divide(c, f.valid_lengths)
-            assert shard.push([f.gradient for f in feats]) == 0
-    else:
-        kind = "port"
-        stores = [oracle.Store(oracle.table_def(id=t.id, dim=t.dim, lr=t.lr, b1p=t.b1p, b2p=t.b2p,
-                                                init_min=t.init_min, init_max=t.init_max,
-                                                seed=t.seed)) for t in wl.tables]
-
-        def step(feats):
-            for f in feats:
-                _, _, c = stores[f.table].prepare(f)
-                if f.pooling == oracle.MEAN:
-                    oracle.mean_divide(c, f.valid_lengths)
-            assert oracle.push(stores, feats, [f.table for f in feats],
-                               [f.gradient for f in feats]) == 0
-
-    step(batches[0])  # first touch of the hot rows, untimed
-    done, lookups, rows, t0 = 0, 0, 0, time.perf_counter()
-    while done < max_steps and (time.perf_counter() - t0) < budget_s:
-        feats = batches[(done + 1) % len(batches)]
-        step(feats)
-        lookups += sum(len(f.keys) for f in feats)
-        rows += sum(len(np.unique(f.keys)) for f in feats)
-        done += 1
-    elapsed = time.perf_counter() - t0
-    return {"value": lookups / elapsed, "unit": "lookups/s", "cores": 1, "kind": kind,
-            "adam_rows_per_s": rows / elapsed, "ms_per_step": 1e3 * elapsed / done,
-            "cpu": cpu_model(),
-            "sample": f"{done} steps of the same workload after one untimed first-touch step, "
-                      f"one shard on one thread ({'reference sources' if kind == 'reference' else 'C restatement'})"}
-
-
-class _ShardFeature:
-    """One shard's part of a feature: its keys (key % shards == shard) with the
+class _ShardPart:
+    """One shard's part of a feature: its keys (key % shards == shard), the
     bags' offsets recounted and the original valid lengths kept, as the
     reference client routes a lookup (src/access/prepared_lookup.cpp:47-83)."""
 
     def __init__(self, f, shard, shards):
         keys = np.asarray(f.keys, np.uint64)
         mine = keys % np.uint64(shards) == np.uint64(shard)
-        counts = np.add.reduceat(mine.astype(np.uint64), np.asarray(f.offsets[:-1], np.int64)) \
-            if len(keys) else np.zeros(len(f.valid_lengths), np.uint64)
+        starts = np.asarray(f.offsets[:-1], np.int64)
+        counts = np.add.reduceat(mine.astype(np.uint64), starts) if len(keys) else \
+            np.zeros(len(f.valid_lengths), np.uint64)
         counts[np.asarray(f.offsets[1:]) == np.asarray(f.offsets[:-1])] = 0  # empty bags
         self.keys = keys[mine]
         self.offsets = np.concatenate([[0], np.cumsum(counts)]).astype(np.uint64)
         self.valid_lengths = np.asarray(f.valid_lengths, np.uint64)
-        self.pooling, self.feature, self.table, self.weights = f.pooling, f.feature, f.table, None
+        self.pooling, self.feature, self.table = f.pooling, f.feature, f.table
+        self.weights = None if f.weights is None else f.weights[mine]
         self.gradient = f.gradient[mine] if f.pooling == 2 else f.gradient  # sequence rows follow keys
 
     @property
@@ -136,79 +149,125 @@ class _ShardFeature:
         return len(self.keys) if self.pooling == 2 else len(self.valid_lengths)
 
 
-def cpu_baseline_shards(wl, batches, shards, budget_s=10.0, max_steps=8):
-    """The reference's own scale-out on the host: `shards` CPU shards (the
-    reference sources), one thread each, keys routed by key % shards; each
-    shard runs PrepareFeature and Push on its part, the client adds the
-    partial sums and divides the means.  Routing is done before timing."""
-    import threading
-
+def cpu_shards(wl, shards, use_ref):
+    """`shards` CPU shards of every table (key % shards routing); returns a
+    function running one shard's Lookup + Push on its parts of a batch."""
     import oracle
 
-    if not oracle.ref_available():
-        return None
-    refs = [oracle.RefShard([oracle.table_def(id=t.id, dim=t.dim, lr=t.lr, b1p=t.b1p, b2p=t.b2p,
-                                              init_min=t.init_min, init_max=t.init_max, seed=t.seed,
-                                              shard=i, shard_count=shards) for t in wl.tables],
-                            shard=i, shard_count=shards) for i in range(shards)]
-    parts = [[[_ShardFeature(f, i, shards) for f in feats] for i in range(shards)] for feats in batches]
+    def defn(t, i):
+        return oracle.table_def(id=t.id, dim=t.dim, lr=t.lr, b1p=t.b1p, b2p=t.b2p, init_min=t.init_min,
+                                init_max=t.init_max, seed=t.seed, shard=i, shard_count=shards)
+
+    if use_ref:
+        refs = [oracle.RefShard([defn(t, i) for t in wl.tables], shard=i, shard_count=shards)
+                for i in range(shards)]
+
+        def run(i, parts):
+            out = [refs[i].prepare(wl.tables[f.table].id, f)[2] for f in parts]
+            if refs[i].push([f.gradient for f in parts]) != 0:
+                raise RuntimeError(f"reference shard {i} rejected its push: {refs[i].error()}")
+            return out
+    else:
+        stores = [[oracle.Store(defn(t, i)) for t in wl.tables] for i in range(shards)]
+
+        def run(i, parts):
+            out = [stores[i][f.table].prepare(f)[2] for f in parts]
+            if oracle.push(stores[i], parts, [f.table for f in parts], [f.gradient for f in parts]) != 0:
+                raise RuntimeError(f"oracle shard {i} rejected its push: {oracle.last_error()}")
+            return out
+    return run
+
+
+def cpu_baseline(wl, batches, shards, fraction, budget_s, max_steps, pull=True):
+    """Lookup (PrepareFeature + client merge and mean divide) and Push
+    (ReduceGradients + ValidateLazyAdam + ApplyLazyAdam) on `shards` shards,
+    one thread each; the routing is done before timing."""
+    import oracle
+
+    weighted = any(f.weights is not None for b in batches for f in b)
+    use_ref = oracle.ref_available() and not weighted  # the reference has no weighted sum
+    run = cpu_shards(wl, shards, use_ref)
+    feats = [sample(b, fraction) for b in batches]
+    parts = [[[_ShardPart(f, i, shards) for f in b] for i in range(shards)] for b in feats]
 
     def step(k):
         outs, errors = [None] * shards, []
 
-        def run(i):
+        def one(i):
             try:
-                out = []
-                for f in parts[k][i]:
-                    out.append(refs[i].prepare(wl.tables[f.table].id, f)[2])
-                if refs[i].push([f.gradient for f in parts[k][i]]) != 0:
-                    raise RuntimeError(f"reference shard {i} rejected its push: {refs[i].error()}")
-                outs[i] = out
+                outs[i] = run(i, parts[k][i])
             except Exception as e:  # surfaced on the calling thread
                 errors.append(e)
 
-        threads = [threading.Thread(target=run, args=(i,)) for i in range(shards)]
-        for t in threads:
-            t.start()
-        for t in threads:
-            t.join()
+        if shards == 1:
+            one(0)
+        else:
+            threads = [threading.Thread(target=one, args=(i,)) for i in range(shards)]
+            for t in threads:
+                t.start()
+            for t in threads:
+                t.join()
         if errors:
             raise errors[0]
-        for j, f in enumerate(batches[k]):  # client merge and mean divide
-            total = outs[0][j].copy()
-            for i in range(1, shards):
-                total += outs[i][j]
-            if f.pooling == oracle.MEAN:
-                oracle.mean_divide(total, f.valid_lengths)
+        if pull:
+            for j, f in enumerate(feats[k]):  # client merge and mean divide
+                total = outs[0][j].copy()
+                for i in range(1, shards):
+                    total += outs[i][j]
+                if f.pooling == oracle.MEAN:
+                    oracle.mean_divide(total, f.valid_lengths)
 
-    step(0)  # first touch, untimed
-    done, lookups, t0 = 0, 0, time.perf_counter()
+    step(0)  # first touch of the hot rows, untimed
+    done, lookups, rows, t0 = 0, 0, 0, time.perf_counter()
     while done < max_steps and (time.perf_counter() - t0) < budget_s:
-        k = (done + 1) % len(batches)
+        k = (done + 1) % len(feats)
         step(k)
-        lookups += sum(len(f.keys) for f in batches[k])
+        lookups += sum(len(f.keys) for f in feats[k])
+        rows += sum(len(np.unique(np.concatenate([g.keys for g in feats[k] if g.table == t])))
+                    for t in {f.table for f in feats[k]})
         done += 1
     elapsed = time.perf_counter() - t0
-    return {"value": lookups / elapsed, "unit": "lookups/s", "cores": shards,
+    what = "reference CPU sources (oracle/_ref)" if use_ref else "oracle C restatement"
+    frac = "whole batches" if fraction >= 1 else f"the first {fraction:.4g} of each feature's bags"
+    return {"value": (lookups if pull else rows) / elapsed, "unit": "lookups/s" if pull else "Adam rows/s",
+            "cores": shards, "kind": "reference" if use_ref else "port",
+            "adam_rows_per_s": rows / elapsed, "lookups_per_s": lookups / elapsed,
             "ms_per_step": 1e3 * elapsed / done,
-            "sample": f"{done} steps after one untimed first-touch step, {shards} reference shards "
-                      f"on {shards} threads, key % {shards} routing done before timing"}
+            "sample": f"{done} steps of {frac} after one untimed first-touch step, {shards} shard(s) "
+                      f"on {shards} thread(s), key % {shards} routing done before timing ({what})"}
+
+
+# ---------------------------------------------------------------------------
+def profile_traffic(workload):
+    """HBM bytes per fused update from the committed rocprofv3 summary."""
+    path = ROOT / "profiles" / f"fused_update_{workload}.md"
+    if path.exists():
+        for line in path.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":", 1)[1])
+    return None
 
 
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--batches", type=int, default=4)
+    ap.add_argument("--config", type=int, default=2, choices=sorted(CONFIGS))
+    ap.add_argument("--steps", type=int, default=None)
+    ap.add_argument("--warmup", type=int, default=None)
+    ap.add_argument("--batches", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run three plain 1 GiB device copies (counter calibration)")
     args = ap.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(f"bench.py measures one GPU only (asked for {args.gpus}): the parameter shard runs on a "
-              "single MI355X here; multi-GPU sharding is not built.", file=sys.stderr)
+              "single MI355X here; multi-GPU sharding is designed, not built.", file=sys.stderr)
         return 2
+    cfg = CONFIGS[args.config]
+    steps = args.steps or cfg["steps"]
+    warmup = cfg["warmup"] if args.warmup is None else args.warmup
+    nbatch = args.batches or cfg["batches"]
+    pull = cfg.get("pull", True)
 
     import torch
 
@@ -223,85 +282,56 @@ def main(argv=None):
         del src, dst
 
     pkg = package()
-    W, H = pkg.workloads, pkg.eps_hip
-    wl = W.Criteo26()
-    batches = [wl.batch(i) for i in range(args.batches)]
-    stats = [batch_stats(wl, b) for b in batches]
-    shard = H.DeviceShard(torch, wl.tables, max_occurrences=max(s["lookups"] for s in stats),
-                          workspaces=2)
-    shard.init_rows()
+    W, H, P = pkg.workloads, pkg.eps_hip, pkg.pipeline
+    wl = make_workload(W, cfg["workload"])
+    batches = [wl.batch(i) for i in range(nbatch)]
+    stats = [batch_stats(W, wl, b, pull) for b in batches]
+    shard = H.DeviceShard(torch, wl.tables, max_occurrences=max(s["lookups"] for s in stats), workspaces=2)
+    if cfg["workload"] == "movielens":
+        for t, state in enumerate(wl.initial_state()):
+            shard.load_rows(t, torch.arange(state.shape[0], device="cuda"), torch.from_numpy(state).cuda())
+    else:
+        shard.init_rows()
     dev = [[H.DeviceFeature(torch, f) for f in b] for b in batches]
-    outputs = [torch.empty((wl.batch_size, t.dim), dtype=torch.float32, device="cuda")
-               for t in wl.tables]
-    stream = torch.cuda.current_stream()
+    outputs = [torch.empty((f.rows, wl.tables[f.table].dim), dtype=torch.float32, device="cuda")
+               for f in batches[0]] if pull else None
+    moves = None
+    if cfg.get("moves"):
+        touched = [[np.unique(f.keys) for f in b] for b in batches]
+        moves = P.TierMoves(torch, shard, wl.admissions(touched), wl.MOVE_LAG)
+        moves.prime()
+    pipe = P.StepPipeline(torch, shard, dev, outputs, pull=pull, moves=moves)
 
-    # Pipeline: the push's preparation (dedup sort and hot-row list) only reads
-    # the batch's ids, so it runs on a side stream ahead of the main stream
-    # (pull, then push).  Two workspaces alternate: the preparation of batch k
-    # waits for the push of batch k-2 (the last reader of its workspace), and
-    # the push of batch k waits for its preparation.
-    side = torch.cuda.Stream()
-    prepared = [torch.cuda.Event() for _ in range(2)]
-    pushed = [torch.cuda.Event() for _ in range(2)]
-
-    def step(k, fused=None, phases=None):
-        """One step; `fused` = two timing events around the fused update,
-        `phases` = seven events for the per-phase breakdown."""
-        feats = dev[k % len(dev)]
-        slot = k % 2
-        side.wait_event(pushed[slot])
-        if phases:
-            phases[0].record(stream)
-            phases[5].record(side)
-        shard.prepare(feats, stream=side, slot=slot)
-        prepared[slot].record(side)
-        if phases:
-            phases[6].record(side)
-        shard.lookup(feats, outputs, stream=stream)
-        if phases:
-            phases[1].record(stream)
-        stream.wait_event(prepared[slot])
-        if phases:
-            phases[2].record(stream)
-        shard.push(feats, stream=stream, slot=slot,
-                   events=fused or (tuple(phases[3:5]) if phases else None))
-        pushed[slot].record(stream)
-
-    # Warm-up steps are issued back to back like the timed ones, so whatever
-    # the runtime sets up when many launches are outstanding happens here.
-    for k in range(args.warmup):
-        step(k)
-    for slot in range(min(2, args.warmup)):
-        status = shard.status(slot=slot)
-        assert status & H.STATUS_ERRORS == 0, f"warm-up push status {status:#x}"
-    torch.cuda.synchronize()
+    # Warm-up steps are issued back to back like the timed ones.
+    for k in range(warmup):
+        pipe.step(k)
+    pipe.check()
     # Timed steps carry only the two events around the fused update (its
     # roofline), on every FUSED_EVERY-th step: every timing event costs GPU
     # time on its stream, and many outstanding timing events can stall the
     # host's launches.
     fused = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-             if k % FUSED_EVERY == 0 else None for k in range(args.steps)]
+             if k % FUSED_EVERY == 0 else None for k in range(steps)]
     torch.cuda.synchronize()
     gc.disable()  # no collector pause inside the timed region
     t0 = time.perf_counter()
-    for k in range(args.steps):
-        step(args.warmup + k, fused=fused[k])
+    for k in range(steps):
+        pipe.step(warmup + k, fused=fused[k])
     enqueued = time.perf_counter() - t0  # host time to issue the timed steps
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     gc.enable()
-    for slot in range(2):
-        status = shard.status(slot=slot)
-        assert status & H.STATUS_ERRORS == 0, f"timed push status {status:#x}"
+    pipe.check()  # any failed push voids the run
     # Per-phase breakdown on further (untimed) steps.
-    breakdown = min(args.steps, 10)
+    breakdown = min(steps, 10)
     events = [[torch.cuda.Event(enable_timing=True) for _ in range(7)] for _ in range(breakdown)]
     for k in range(breakdown):
-        step(args.warmup + args.steps + k, phases=events[k])
+        pipe.step(warmup + steps + k, phases=events[k])
     torch.cuda.synchronize()
+    pipe.check()
 
-    ms = elapsed * 1e3 / args.steps
-    used = [stats[(args.warmup + k) % len(stats)] for k in range(args.steps)]
+    ms = elapsed * 1e3 / steps
+    used = [stats[(warmup + k) % len(stats)] for k in range(steps)]
     mean = {key: float(np.mean([u[key] for u in used])) for key in used[0]}
     gather_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in events]))
     prepare_ms = float(np.mean([e[5].elapsed_time(e[6]) for e in events]))  # side stream
@@ -310,31 +340,31 @@ def main(argv=None):
     push_ms = float(np.mean([e[2].elapsed_time(e[4]) for e in events]))
     step_bytes = mean["pull_bytes"] + mean["push_bytes"]
     achieved = mean["fused_bytes"] / (fused_ms * 1e-3) / 1e9
-    traffic = None
-    if PROFILE_SUMMARY.exists():
-        for line in PROFILE_SUMMARY.read_text().splitlines():
-            if line.startswith("traffic_bytes_per_launch:"):
-                traffic = float(line.split(":", 1)[1])
+    traffic = profile_traffic(cfg["workload"])
+    value, unit = (mean["lookups"] / (ms * 1e-3), "lookups/s") if pull else \
+        (mean["unique"] / (ms * 1e-3), "Adam rows/s")
+    dims = sorted({t.dim for t in wl.tables})
     result = {
         "metric": METRIC,
-        "value": mean["lookups"] / (ms * 1e-3),
-        "unit": "lookups/s",
+        "value": value,
+        "unit": unit,
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": steps,
+        "warmup": warmup,
         "ms_per_step": ms,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic: seeded Zipf(1.05) ids, U{1..20} bags, N(0,1e-2) gradients, "
-                "reference SplitMix initializer U(-0.05,0.05); inputs resident in HBM",
-        "config": {"workload": "26 tables x 1,000,000 rows x dim 64 fp32 (w|m|v AoS), batch 4096 bags "
-                               "per table, bag length U{1..20}, Zipf(1.05), 13 sum + 13 mean pooling, "
-                               "pull + device dedup + fused sparse Adam (lr 1e-3, 0.9/0.999, 1e-8)",
-                   "tables": len(wl.tables), "rows_per_table": wl.tables[0].rows,
-                   "dim": wl.tables[0].dim, "batch": wl.batch_size, "batches_cycled": len(batches)},
-        "host_enqueue_ms_per_step": enqueued * 1e3 / args.steps,
+        "data": f"synthetic: seeded {cfg['workload']} batches (ids, bag lengths, weights, N(0,1e-2) "
+                "gradients), reference SplitMix initializer U(-0.05,0.05) (config 1: explicit N(0,0.01) "
+                "weights); inputs resident in HBM",
+        "config": {"workload": cfg["desc"], "config": args.config, "tables": len(wl.tables),
+                   "rows": [t.rows for t in wl.tables] if len(set(t.rows for t in wl.tables)) > 1
+                   else wl.tables[0].rows, "dim": dims if len(dims) > 1 else dims[0],
+                   "batches_cycled": len(batches)},
+        "host_enqueue_ms_per_step": enqueued * 1e3 / steps,
+        "lookups_per_s": mean["lookups"] / (ms * 1e-3),
         "adam_rows_per_s": mean["unique"] / (ms * 1e-3),
         "lookups_per_step": mean["lookups"],
         "adam_rows_per_step": mean["unique"],
@@ -344,8 +374,9 @@ def main(argv=None):
         "phases_ms": {"gather": gather_ms, "prepare": prepare_ms, "prepare_wait": wait_ms,
                       "push": push_ms, "fused_update": fused_ms,
                       "note": "gather/prepare/prepare_wait/push from untimed steps after the "
-                      "timed ones (prepare runs on a side stream, ahead of the pull and push); "
-                      "fused_update from every 5th timed step"},
+                      "timed ones (prepare runs on a side stream, ahead of the pull and push; gather "
+                      "includes the tier admissions of config 5); fused_update from every "
+                      f"{FUSED_EVERY}th timed step"},
         "roofline": {"kernel": "fused aggregation + sparse Adam (eps_hip_push_apply: "
                                "HotSliceKernel + RowRunKernel)", "bound": "hbm",
                      "achieved": achieved, "peak": HBM_PEAK_GBPS, "unit": "GB/s",
@@ -354,17 +385,27 @@ def main(argv=None):
                      # measured HBM bytes (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated)
                      # over the same duration
                      "traffic_GBps": traffic / (fused_ms * 1e-3) / 1e9 if traffic else None},
+    }
+    if pull:
         # Occurrence-based pull rate: every pooled lookup reads one dim-wide row
         # (N x d x 4 bytes, repeats included, most served by the caches).
-        "gather_effective_GBps": mean["lookups"] * wl.tables[0].dim * 4 / (gather_ms * 1e-3) / 1e9,
-    }
+        occ_bytes = sum(len(f.keys) * wl.tables[f.table].dim * 4 for f in batches[0])
+        result["gather_effective_GBps"] = occ_bytes / (gather_ms * 1e-3) / 1e9
+    if moves:
+        result["host_link"] = {"h2d_bytes_per_step": moves.bytes, "d2h_bytes_per_step": moves.bytes,
+                               "GBps_each_way": moves.bytes / (ms * 1e-3) / 1e9,
+                               "rows_each_way_per_step": int(sum(moves.counts)),
+                               "note": "admissions host->device and write-backs device->host on two "
+                                       "copy streams overlapped with the steps; not in the HBM bytes"}
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(wl, batches)
-        shards = min(16, os.cpu_count() or 1)  # the host share of one GPU
+        base = cpu_baseline(wl, batches, 1, cfg["cpu_fraction"], budget_s=15.0, max_steps=200 if
+                            args.config == 1 else 8, pull=pull)
+        base["cpu"] = cpu_model()
+        shards = min(HOST_SHARE, os.cpu_count() or 1)
         if shards > 1:
-            all_cores = cpu_baseline_shards(wl, batches, shards)
-            if all_cores:
-                result["cpu_baseline"]["all_cores"] = all_cores
+            base["all_cores"] = cpu_baseline(wl, batches, shards, cfg["cpu_fraction"], budget_s=10.0,
+                                             max_steps=200 if args.config == 1 else 8, pull=pull)
+        result["cpu_baseline"] = base
     print(json.dumps(result))
     return 0
 

@@ -7,4 +7,4 @@ kernels behind a C ABI (include/eps_hip.h, libeps_hip.so) and a C++ backend
 GpuCacheAgent interface.  This Python package is a thin ctypes binding used by
 tests and the benchmark.
 """
-from . import eps_hip, workloads  # noqa: F401
+from . import eps_hip, pipeline, workloads  # noqa: F401

@@ -27,23 +27,20 @@
 // or an out-of-range slot rejects the whole update before anything is written.
 #include "prepare.hpp"
 
+#include <atomic>
 #include <cfloat>
 #include <cmath>
 
 namespace eps_hip {
 
-int LaunchFill(uint32_t* target, uint32_t value, uint64_t count, hipStream_t stream);
-
 namespace {
 
-constexpr uint32_t kErrorBits = EPS_HIP_STATUS_BAD_INDEX | EPS_HIP_STATUS_NONFINITE_GRAD |
-                                EPS_HIP_STATUS_REDUCE_OVERFLOW | EPS_HIP_STATUS_ADAM_OVERFLOW;
 constexpr uint32_t kFallbackGrid = 2048;
 
 // ---------------------------------------------------------------------------
-// Gradient maximum (GradMaxKernel) and the guard decision (GuardDecideKernel).
-// A guarded input array: gradient values, reference scales, or 64-bit
-// indices that must all be below `limit` (checked before anything is written).
+// Gradient maximum (GradMaxKernel).  A guarded input array: gradient values,
+// reference scales, or 64-bit indices that must all be below `limit` (checked
+// before anything is written).
 enum SpanKind : uint32_t { kGradientSpan = 0, kScaleSpan = 1, kIndexSpan = 2 };
 struct Span {
   const float* p;
@@ -51,14 +48,10 @@ struct Span {
   uint32_t block_begin, kind;
   uint64_t limit;
 };
-struct GuardTable { float beta1, beta2, lr, eps; };
 struct GuardArgs {
   Span span[EPS_HIP_MAX_FEATURES + 1];
-  GuardTable t[EPS_HIP_MAX_TABLES];
-  uint32_t spans, tables, reset_scale, use_prep_status;
-  uint64_t refs_host;  // 0: take the prepared valid count
+  uint32_t spans;
   Control* ctrl;
-  const Bounds* bounds;
 };
 constexpr uint32_t kMaxItems = 16;  // float4 per thread per block
 
@@ -68,10 +61,11 @@ __global__ void __launch_bounds__(kBlock) GradMaxKernel(GuardArgs a) {
   const uint64_t begin = uint64_t(blockIdx.x - sp.block_begin) * per_block;
   const uint64_t end = min(begin + per_block, sp.count);
   uint32_t m = 0;
-  bool out_of_range = false;
+  uint32_t found = 0;  // prepare-status bits this thread found
   if (sp.kind == kIndexSpan) {
     const uint64_t* idx = reinterpret_cast<const uint64_t*>(sp.p);
-    for (uint64_t i = begin + threadIdx.x; i < end; i += kBlock) out_of_range |= idx[i] >= sp.limit;
+    for (uint64_t i = begin + threadIdx.x; i < end; i += kBlock)
+      if (idx[i] >= sp.limit) found = EPS_HIP_STATUS_BAD_INDEX;
   } else if (reinterpret_cast<uintptr_t>(sp.p) % 16 == 0) {
     // All kMaxItems loads of a thread are issued before any is consumed.
     const uint64_t vend = begin + ((end - begin) & ~uint64_t(3));
@@ -81,15 +75,27 @@ __global__ void __launch_bounds__(kBlock) GradMaxKernel(GuardArgs a) {
       const uint64_t i = begin + (uint64_t(k) * kBlock + threadIdx.x) * 4;
       x[k] = i < vend ? Load4(sp.p + i) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
+    uint32_t neg = 0;  // any value below zero (not -0.0)
 #pragma unroll
-    for (uint32_t k = 0; k < kMaxItems; ++k)
+    for (uint32_t k = 0; k < kMaxItems; ++k) {
       m = max(m, max(max(AbsBits(x[k].x), AbsBits(x[k].y)), max(AbsBits(x[k].z), AbsBits(x[k].w))));
-    for (uint64_t i = vend + threadIdx.x; i < end; i += kBlock) m = max(m, AbsBits(sp.p[i]));
+      neg |= (x[k].x < 0.f) | (x[k].y < 0.f) | (x[k].z < 0.f) | (x[k].w < 0.f);
+    }
+    for (uint64_t i = vend + threadIdx.x; i < end; i += kBlock) {
+      m = max(m, AbsBits(sp.p[i]));
+      neg |= sp.p[i] < 0.f;
+    }
+    if (sp.kind == kScaleSpan && neg) found = EPS_HIP_STATUS_BAD_SCALE;
   } else {
-    for (uint64_t i = begin + threadIdx.x; i < end; i += kBlock) m = max(m, AbsBits(sp.p[i]));
+    for (uint64_t i = begin + threadIdx.x; i < end; i += kBlock) {
+      m = max(m, AbsBits(sp.p[i]));
+      if (sp.kind == kScaleSpan && sp.p[i] < 0.f) found = EPS_HIP_STATUS_BAD_SCALE;
+    }
   }
+  // A compact scale must be finite and >= 0 (compact_gradients.cpp:21).
+  if (sp.kind == kScaleSpan && m >= 0x7f800000u) found = EPS_HIP_STATUS_BAD_SCALE;
   __shared__ uint32_t s_max[4];
-  if (out_of_range) atomicOr(&a.ctrl->prep_status, EPS_HIP_STATUS_BAD_INDEX);
+  if (found) atomicOr(&a.ctrl->prep_status, found);
   m = WaveMax(m);
   if ((threadIdx.x & (kWave - 1)) == 0) s_max[threadIdx.x / kWave] = m;
   __syncthreads();
@@ -99,57 +105,6 @@ __global__ void __launch_bounds__(kBlock) GradMaxKernel(GuardArgs a) {
       atomicMax(sp.kind == kScaleSpan ? &a.ctrl->scale_slots[blockIdx.x % kSrcSlots]
                                       : &a.ctrl->src_slots[blockIdx.x % kSrcSlots], bm);
   }
-}
-
-// The guard decision, one wavefront after GradMaxKernel on the same stream
-// (the kernel boundary orders the maxima before it; no cross-block fences).
-__global__ void __launch_bounds__(kWave) GuardDecideKernel(GuardArgs a) {
-  Control* ctrl = a.ctrl;
-  const uint32_t lane = threadIdx.x;
-  // Bounds domain and gradient-maximum slots: one slot per lane, then the
-  // wavefront maxima.  The gradient slots are cleared for the next push.
-  uint32_t wb = 0, mb = 0, vb = 0, gb = 0, scale_bits = 0;
-  for (uint32_t s = lane; s < kBoundSlots; s += kWave) {
-    wb = max(wb, a.bounds->v[s][0]); mb = max(mb, a.bounds->v[s][1]); vb = max(vb, a.bounds->v[s][2]);
-  }
-  for (uint32_t s = lane; s < kSrcSlots; s += kWave) {
-    gb = max(gb, ctrl->src_slots[s]);
-    scale_bits = max(scale_bits, ctrl->scale_slots[s]);
-    ctrl->src_slots[s] = 0;
-    if (a.reset_scale) ctrl->scale_slots[s] = 0;
-  }
-  wb = WaveMax(wb); mb = WaveMax(mb); vb = WaveMax(vb); gb = WaveMax(gb);
-  scale_bits = WaveMax(scale_bits);
-  uint32_t status = a.use_prep_status ? ctrl->prep_status : 0u;
-  uint32_t mode = kFused;
-  if (status & EPS_HIP_STATUS_BAD_INDEX) {
-    mode = kReject;
-  } else if (gb >= 0x7f800000u) {
-    status |= EPS_HIP_STATUS_NONFINITE_GRAD;
-    mode = kReject;
-  } else {
-    const double W = __uint_as_float(wb), M = __uint_as_float(mb), V = __uint_as_float(vb);
-    const double refs = double(a.refs_host ? a.refs_host : ctrl->valid_count);
-    const double scale = fmax(1.0, double(__uint_as_float(scale_bits)));
-    const double G = double(__uint_as_float(gb)) * scale * refs *
-                     exp((refs + 2.0) * 0x1.0p-24) * 1.01;
-    // One table per lane.
-    bool table_safe = true;
-    if (lane < a.tables) {
-      const GuardTable& T = a.t[lane];
-      const double b1 = T.beta1, b2 = T.beta2;
-      const double mbound = (b1 * M + (1.0 - b1) * G) * 1.01;
-      const double vbound = (b2 * V + (1.0 - b2) * G * G) * 1.01;
-      const double wbound = (W + double(T.lr) * mbound / double(T.eps)) * 1.01;
-      table_safe = mbound < 1e30 && vbound < 1e30 && wbound < 1e30 && double(T.eps) > 0.0;
-    }
-    const bool safe = G < 1e30 && __ballot(!table_safe) == 0;
-    if (!safe) { mode = kChecked; status |= EPS_HIP_STATUS_CHECKED_PATH; }
-  }
-  if (lane != 0) return;
-  if (mode == kReject) status |= EPS_HIP_STATUS_REJECTED;
-  ctrl->mode = mode;
-  ctrl->status = status;
 }
 
 // ---------------------------------------------------------------------------
@@ -253,6 +208,98 @@ __device__ __forceinline__ void Accumulate4(float4& acc, float4 x, float s) {
   acc.w = acc.w + x.w * s;
 }
 
+// The guard decision (see the file comment), made by every block of the first
+// kernel of an update from the gradient maxima, the prepare-time findings and
+// the bounds domain -- all written by earlier kernels, so every block reads
+// the same values and decides the same.  Block 0 publishes the mode and the
+// status bits for the kernels after it.  Runs in wavefront 0 (one bounds slot
+// and one gradient slot per lane); returns the mode to every thread.
+static_assert(kBoundSlots == kWave && kSrcSlots == kWave, "one guard slot per lane");
+struct GuardScalars {
+  uint64_t refs;       // references summed into one reduced gradient, at most; 0: the prepared count
+  uint32_t tables;
+};
+__device__ uint32_t DecideBlock(Control* ctrl, const Bounds* bounds, const TableDesc* t,
+                                const GuardScalars& gs, uint32_t* s_mode) {
+  if (threadIdx.x < kWave) {
+    const uint32_t lane = threadIdx.x;
+    const uint32_t wb = WaveMax(bounds->v[lane][0]), mb = WaveMax(bounds->v[lane][1]),
+                   vb = WaveMax(bounds->v[lane][2]);
+    const uint32_t gb = WaveMax(ctrl->src_slots[lane]);
+    const uint32_t scale_bits = WaveMax(ctrl->scale_slots[lane]);
+    uint32_t status = ctrl->prep_status;
+    uint32_t mode = kFused;
+    if (status & (EPS_HIP_STATUS_BAD_INDEX | EPS_HIP_STATUS_BAD_SCALE)) {
+      mode = kReject;
+    } else if (gb >= 0x7f800000u) {
+      status |= EPS_HIP_STATUS_NONFINITE_GRAD;
+      mode = kReject;
+    } else if (scale_bits >= 0x7f800000u) {  // a non-finite weight or scale
+      status |= EPS_HIP_STATUS_BAD_SCALE;
+      mode = kReject;
+    } else {
+      const double W = __uint_as_float(wb), M = __uint_as_float(mb), V = __uint_as_float(vb);
+      const double refs = double(gs.refs ? gs.refs : uint64_t(ctrl->valid_count));
+      const double scale = fmax(1.0, double(__uint_as_float(scale_bits)));
+      const double G = double(__uint_as_float(gb)) * scale * refs * exp((refs + 2.0) * 0x1.0p-24) * 1.01;
+      bool table_safe = true;  // one table per lane
+      if (lane < gs.tables) {
+        const TableDesc& T = t[lane];
+        const double b1 = T.beta1, b2 = T.beta2;
+        const double mbound = (b1 * M + (1.0 - b1) * G) * 1.01;
+        const double vbound = (b2 * V + (1.0 - b2) * G * G) * 1.01;
+        const double wbound = (W + double(T.lr) * mbound / double(T.eps)) * 1.01;
+        table_safe = mbound < 1e30 && vbound < 1e30 && wbound < 1e30 && double(T.eps) > 0.0;
+      }
+      if (!(G < 1e30) || __ballot(!table_safe) != 0) {
+        mode = kChecked;
+        status |= EPS_HIP_STATUS_CHECKED_PATH;
+      }
+    }
+    if (mode == kReject) status |= EPS_HIP_STATUS_REJECTED;
+    if (lane == 0) {
+      *s_mode = mode;
+      if (blockIdx.x == 0) {
+        ctrl->mode = mode;
+        ReportStatus(ctrl, status);
+      }
+    }
+  }
+  __syncthreads();
+  return *s_mode;
+}
+
+// Role of a launch in an update.  The first kernel decides (DecideBlock);
+// the primary kernels after it follow that decision; the fallback (the apply
+// pass of the checked path) runs only when the decision was "checked" and the
+// validate-only pass found nothing.
+enum Role : uint32_t { kDecide = 0, kFollow = 1, kFallback = 2 };
+
+// Whether this launch has work, and whether it writes (uniform over the
+// block).  s_t must hold the launch's tables; every thread calls it.
+__device__ bool LaunchGate(Control* ctrl, const Bounds* bounds, const TableDesc* s_t,
+                           const GuardScalars& gs, uint32_t role, uint32_t* s_mode, bool& write) {
+  if (role == kDecide) {
+    __syncthreads();  // s_t is staged
+    const uint32_t mode = DecideBlock(ctrl, bounds, s_t, gs, s_mode);
+    write = mode == kFused;
+    return mode != kReject;
+  }
+  const uint32_t mode = ctrl->mode, status = ctrl->status;
+  if (role == kFollow) {
+    // A stall in an earlier kernel of a fused update stops every later write.
+    write = mode == kFused;
+    return mode != kReject && !(status & EPS_HIP_STATUS_STALLED);
+  }
+  if (mode != kChecked) return false;
+  if (status & (kErrorBits | EPS_HIP_STATUS_STALLED)) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) ReportStatus(ctrl, EPS_HIP_STATUS_REJECTED);
+    return false;
+  }
+  write = true;
+  return true;
+}
+
 // Block-level fold of the per-lane statistics: error bits (with those the
 // maxima imply) to the status word, written maxima to one slot of the bounds
 // domain.
@@ -275,7 +322,7 @@ __device__ void FinishBlock(const RowStats& st, Control* ctrl, Bounds* bounds, b
     for (uint32_t i = 0; i < kWaves; ++i) {
       E |= s_red[i][0]; W = max(W, s_red[i][1]); M = max(M, s_red[i][2]); V = max(V, s_red[i][3]);
     }
-    if (E) atomicOr(&ctrl->status, E);
+    ReportStatus(ctrl, E);
     if (wrote && bounds) {
       uint32_t* slot = bounds->v[blockIdx.x % kBoundSlots];
       if (W) atomicMax(slot + 0, W);
@@ -298,7 +345,8 @@ struct FusedArgs {
   uint64_t reduce_stride;
   Control* ctrl;
   Bounds* bounds;
-  uint32_t row_bits, cls, cls_end, log2g, ppb, vblocks, fallback, reduce, tables;  // classes [cls, cls_end)
+  GuardScalars gs;
+  uint32_t row_bits, cls, cls_end, log2g, ppb, vblocks, role, reduce, tables;  // classes [cls, cls_end)
 };
 
 template <bool kGeneric>
@@ -307,25 +355,12 @@ __global__ void __launch_bounds__(kBlock) SortedUpdateKernel(FusedArgs a) {
   __shared__ const float* s_grad[EPS_HIP_MAX_FEATURES];
   __shared__ uint32_t s_heads[kBlock];
   __shared__ uint32_t s_wave_heads[4];
+  __shared__ uint32_t s_mode;
   CopyWords(s_t, a.t, sizeof(a.t));
   CopyWords(s_grad, a.grad, sizeof(a.grad));
   Control* ctrl = a.ctrl;
-  const uint32_t mode = ctrl->mode;
-  const uint32_t status = ctrl->status;
-  bool write;
-  if (a.reduce) {
-    write = true;
-  } else if (!a.fallback) {
-    if (mode == kReject) return;
-    write = mode == kFused;
-  } else {
-    if (mode != kChecked) return;
-    if (status & kErrorBits) {
-      if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(&ctrl->status, EPS_HIP_STATUS_REJECTED);
-      return;
-    }
-    write = true;
-  }
+  bool write = true;
+  if (!a.reduce && !LaunchGate(ctrl, a.bounds, s_t, a.gs, a.role, &s_mode, write)) return;
   const uint32_t start = ctrl->class_start[a.cls];
   const uint32_t end = ctrl->class_start[a.cls_end];
   const uint32_t G = kGeneric ? kWave : (1u << a.log2g);
@@ -465,7 +500,9 @@ struct VecArgs {
   const HotEntry* hot;
   Control* ctrl;
   Bounds* bounds;
-  uint32_t row_bits, cls, fallback, slice_bits, hot_capacity;
+  GuardScalars gs;
+  uint32_t row_bits, cls, role, slice_bits, hot_capacity;
+  uint32_t spin_limit;  // polls of a hot-row hand-over wait (0: give up at once)
 };
 
 // Position of (column c, reference r) in a hot-row tile.  Groups of four
@@ -487,23 +524,10 @@ __device__ __forceinline__ const float* RefSource(const float* const* grad, uint
 // returns false when it has nothing to do (uniform over the block).
 template <uint32_t kThreads = kBlock>
 __device__ __forceinline__ bool VecPrologue(const VecArgs& a, TableDesc* s_t, const float** s_grad,
-                                            bool& write) {
+                                            uint32_t* s_mode, bool& write) {
   CopyWords<kThreads>(s_t, a.t, sizeof(a.t));
   CopyWords<kThreads>(s_grad, a.grad, sizeof(a.grad));
-  Control* ctrl = a.ctrl;
-  const uint32_t mode = ctrl->mode;
-  if (!a.fallback) {
-    if (mode == kReject) return false;
-    write = mode == kFused;
-  } else {
-    if (mode != kChecked) return false;
-    if (ctrl->status & kErrorBits) {
-      if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(&ctrl->status, EPS_HIP_STATUS_REJECTED);
-      return false;
-    }
-    write = true;
-  }
-  return true;
+  return LaunchGate(a.ctrl, a.bounds, s_t, a.gs, a.role, s_mode, write);
 }
 
 // One chunk of a hot work unit: positions [cbase, cbase + kHotChunk) of the
@@ -539,19 +563,18 @@ struct HotRefs {
 // vmcnt and expcnt at their maxima, lgkmcnt 0.
 constexpr int kLgkmZero = 0xC07F;
 
-// Spin limit of the hand-over waits: a wait that has not been satisfied after
-// this many polls marks the push failed and stops waiting, so a block always
-// finishes.
-constexpr uint32_t kHotSpinLimit = 1u << 22;
-
 // Waits until the LDS counter reaches `target` (all lanes read the same word).
-// Returns false on a timeout.
-__device__ __forceinline__ bool WaitCounter(const uint32_t* counter, uint32_t target, uint32_t sleep) {
+// Returns false on a timeout: a wait that has not been satisfied after `limit`
+// polls marks the push failed and stops waiting, so a block always finishes
+// (limit 0: every wait times out at once, the host-driven test of that path).
+__device__ __forceinline__ bool WaitCounter(const uint32_t* counter, uint32_t target, uint32_t sleep,
+                                            uint32_t limit) {
+  if (limit == 0) return false;
   for (uint32_t spins = 0;; ++spins) {
     const uint32_t v = uint32_t(__builtin_amdgcn_readfirstlane(
         int(__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP))));
     if (v >= target) break;
-    if (spins >= kHotSpinLimit) return false;
+    if (spins >= limit) return false;
     if (sleep) __builtin_amdgcn_s_sleep(1);
   }
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
@@ -573,8 +596,9 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
   __shared__ __align__(16) HotRefs s_ref[kProducers];
   // ready[t]: chunks staged in tile t so far; used[t]: chunks added from it.
   __shared__ uint32_t s_ready[kHotRing], s_used[kHotRing];
+  __shared__ uint32_t s_mode;
   bool write = false;
-  if (!VecPrologue<kHotBlock>(a, s_t, s_grad, write)) return;
+  if (!VecPrologue<kHotBlock>(a, s_t, s_grad, &s_mode, write)) return;
   if (threadIdx.x < kHotRing) {
     s_ready[threadIdx.x] = 0;
     s_used[threadIdx.x] = 0;
@@ -643,7 +667,9 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
     }
     return take();
   };
-  bool stalled = false;  // a hand-over wait timed out: stop waiting, report failure
+  // A hand-over wait timed out: this wave stops waiting, staging, adding and
+  // writing, and the push reports a failure.
+  bool stalled = false;
 
   if (wave == 0) {
     // The adding wave: chunk j is the (j / kHotRing)-th use of tile j % kHotRing.
@@ -663,7 +689,7 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
         x[g] = *reinterpret_cast<const float4*>(tile + TileAt(lane, 4 * g));
     };
     auto ready = [&](uint32_t j) {
-      if (!stalled && !WaitCounter(&s_ready[j % kHotRing], j / kHotRing + 1, 0)) stalled = true;
+      if (!stalled && !WaitCounter(&s_ready[j % kHotRing], j / kHotRing + 1, 0, a.spin_limit)) stalled = true;
     };
     // Adds chunk j (values in x, chunk c); reads chunk j + 1 into y.
     auto add = [&](uint32_t j, const float4* x, float4* y) {
@@ -697,7 +723,7 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
       __builtin_amdgcn_sched_barrier(0);
       if (c.cbase + kHotChunk >= c.end) {  // the unit's last chunk
         const TableDesc& T = s_t[c.key >> a.row_bits];
-        if (c.col0 + lane < T.dim) {
+        if (c.col0 + lane < T.dim && !stalled) {
           AdamElement(T, acc, w, m, v, st);
           if (write) {
             float* row = T.state + uint64_t(c.key & row_mask) * T.dim * 3 + c.col0 + lane;
@@ -721,9 +747,9 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
       read_tile(0, xa);
       if (cn.ok) ready(1);
     }
-    for (uint32_t j = 0; c.ok; j += 2) {
+    for (uint32_t j = 0; c.ok && !stalled; j += 2) {
       add(j, xa, xb);
-      if (!c.ok) break;
+      if (!c.ok || stalled) break;
       add(j + 1, xb, xa);
     }
   } else {
@@ -800,7 +826,8 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
     };
     auto stage = [&](const HotRows& r, uint32_t j) {
       const uint32_t t = j % kHotRing;
-      if (!stalled && !WaitCounter(&s_used[t], j / kHotRing, 1)) stalled = true;
+      if (!stalled && !WaitCounter(&s_used[t], j / kHotRing, 1, a.spin_limit)) stalled = true;
+      if (stalled) return;  // nothing more is staged
       // Load k writes (column 4*quad + i, reference 4k + sub) = TileAt(): the
       // reference group k is rotated by the column's quarter quad / 4.
       float* tile = s_tile[t] + 4 * quad * kHotPitch + sub;
@@ -879,8 +906,9 @@ RowRunKernel(VecArgs a) {
   __shared__ uint32_t s_heads[kRunPositions];
   __shared__ uint32_t s_wave_heads[kBlock / kWave];
   __shared__ uint32_t s_next;               // next unclaimed row (head index) of the window
+  __shared__ uint32_t s_mode;
   bool write = false;
-  if (!VecPrologue(a, s_t, s_grad, write)) return;
+  if (!VecPrologue(a, s_t, s_grad, &s_mode, write)) return;
   Control* ctrl = a.ctrl;
   const uint32_t begin = ctrl->class_start[a.cls], end = ctrl->class_start[a.cls + 1];
   const uint32_t row_mask = (1u << a.row_bits) - 1;
@@ -1011,25 +1039,18 @@ struct RowArgs {
   uint64_t rows;
   Control* ctrl;
   Bounds* bounds;
-  uint32_t log2g, vblocks, fallback;
+  GuardScalars gs;
+  uint32_t log2g, vblocks, role;
 };
 
 template <bool kGeneric>
 __global__ void __launch_bounds__(kBlock) RowUpdateKernel(RowArgs a) {
+  __shared__ TableDesc s_t[1];
+  __shared__ uint32_t s_mode;
   Control* ctrl = a.ctrl;
-  const uint32_t mode = ctrl->mode;
-  bool write;
-  if (!a.fallback) {
-    if (mode == kReject) return;
-    write = mode == kFused;
-  } else {
-    if (mode != kChecked) return;
-    if (ctrl->status & kErrorBits) {
-      if (blockIdx.x == 0 && threadIdx.x == 0) atomicOr(&ctrl->status, EPS_HIP_STATUS_REJECTED);
-      return;
-    }
-    write = true;
-  }
+  if (threadIdx.x == 0) s_t[0] = a.t;
+  bool write = false;
+  if (!LaunchGate(ctrl, a.bounds, s_t, a.gs, a.role, &s_mode, write)) return;
   const TableDesc T = a.t;
   const uint32_t dim = T.dim;
   const uint32_t G = kGeneric ? kWave : (1u << a.log2g);
@@ -1110,16 +1131,12 @@ uint32_t Log2G(uint32_t dim) {
   return log2g;
 }
 
-int LaunchGuard(GuardArgs& g, uint64_t blocks, hipStream_t s) {
-  if (!blocks) {  // nothing to scan: still decide (one block over an empty span)
-    g.span[0] = Span{nullptr, 0, 0, kGradientSpan, 0};
-    g.spans = 1;
-    blocks = 1;
-  }
+// The gradient scan; the decision itself is made by the first kernel of the
+// update (DecideBlock), so nothing is launched when there is nothing to scan.
+int LaunchGuard(const GuardArgs& g, uint64_t blocks, hipStream_t s) {
+  if (!blocks) return EPS_HIP_OK;
   hipLaunchKernelGGL(GradMaxKernel, dim3(unsigned(blocks)), dim3(kBlock), 0, s, g);
   EPS_HIP_LAUNCHED("gradient guard");
-  hipLaunchKernelGGL(GuardDecideKernel, dim3(1), dim3(kWave), 0, s, g);
-  EPS_HIP_LAUNCHED("guard decision");
   return EPS_HIP_OK;
 }
 
@@ -1127,6 +1144,9 @@ uint64_t SpanBlocks(uint64_t count) {
   const uint64_t per = uint64_t(kBlock) * kMaxItems * 4;
   return (count + per - 1) / per;
 }
+
+std::atomic<uint32_t> g_spin_limit{1u << 22};
+uint32_t SpinLimit() { return g_spin_limit.load(std::memory_order_relaxed); }
 
 constexpr int kPrimary = 1, kSecond = 2;
 constexpr uint64_t kVectorGrid = 4096;  // persistent grid cap of the vector kernels
@@ -1175,6 +1195,9 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
   a.row_bits = plan.row_bits;
   a.reduce = reduce ? 1 : 0;
   a.tables = table_count;
+  a.gs = GuardScalars{0, table_count};  // refs: the prepared valid count
+  // The first kernel of the primary phase makes the guard decision.
+  uint32_t role = kDecide;
   for (uint32_t k = 0; k < table_count; ++k) {
     const uint32_t t = plan.table_of_key[k];
     eps_hip_optimizer o{};
@@ -1194,6 +1217,8 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
     va.hot_capacity = uint32_t(L.HotCapacity());
     va.ctrl = a.ctrl;
     va.bounds = bounds;
+    va.gs = a.gs;
+    va.spin_limit = SpinLimit();
     va.row_bits = plan.row_bits;
     // Units per hot row: the widest vector table's slices, rounded up to a
     // power of two (units past a row's dimension are skipped in the kernel).
@@ -1207,7 +1232,6 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
     for (uint32_t cls = 0; cls + 1 < kClasses; ++cls) vector_occurrences += plan.class_occurrences[cls];
     const uint64_t hot_units = (vector_occurrences / (kLongRefs + 1)) << va.slice_bits;
     if (phases & kPrimary) {
-      va.fallback = 0;
       // Grids are multiples of kXcds (the kernels split their work by XCD).
       auto xcd_grid = [](uint64_t b) { return (b + kXcds - 1) / kXcds * kXcds; };
       // Hot rows first, then the row runs of each class, in stream order: the
@@ -1215,11 +1239,15 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
       // compete for the same registers and bandwidth and finish later).
       if (hot_units) {
         const uint64_t blocks = xcd_grid(std::min<uint64_t>(hot_units, kHotGrid));
+        va.role = role;
         EPS_HIP_TRY(LaunchVectorUpdate(0, true, unsigned(blocks), va, s));
+        role = kFollow;
       }
       for (uint32_t cls = 0; cls + 1 < kClasses; ++cls) {
         if (!plan.class_occurrences[cls]) continue;
         va.cls = cls;
+        va.role = role;
+        role = kFollow;
         const uint64_t blocks = xcd_grid(std::min<uint64_t>(
             std::max<uint64_t>(1, (plan.class_occurrences[cls] + kRunPositions - 1) / kRunPositions),
             kVectorGrid));
@@ -1238,7 +1266,8 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
     a.vblocks = uint32_t(vb);
     auto kernel = cls == 5 ? SortedUpdateKernel<true> : SortedUpdateKernel<false>;
     if (phases & kPrimary) {
-      a.fallback = 0;
+      a.role = role;
+      role = kFollow;
       hipLaunchKernelGGL(kernel, dim3(a.vblocks), dim3(kBlock), 0, s, a);
       EPS_HIP_LAUNCHED("sorted update");
     }
@@ -1251,7 +1280,7 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
     a.cls_end = kClasses;
     a.ppb = PositionsPerBlock(kClasses - 1);
     a.vblocks = uint32_t((plan.occurrences + a.ppb - 1) / a.ppb);
-    a.fallback = 1;
+    a.role = kFallback;
     if (a.vblocks) {
       hipLaunchKernelGGL(SortedUpdateKernel<true>, dim3(std::min<uint32_t>(a.vblocks, kSecondGrid)),
                          dim3(kBlock), 0, s, a);
@@ -1304,16 +1333,7 @@ int eps_hip_push_begin(const eps_hip_table* tables, const eps_hip_optimizer* opt
     g.span[g.spans++] = Span{in.gradients, count, uint32_t(blocks), kGradientSpan, 0};
     blocks += SpanBlocks(count);
   }
-  for (uint32_t t = 0; t < table_count; ++t) {
-    const TableDesc d = MakeTable(tables[t], optimizers[t]);
-    g.t[t] = GuardTable{optimizers[t].beta1, optimizers[t].beta2, d.lr, optimizers[t].epsilon};
-  }
-  g.tables = table_count;
-  g.reset_scale = 0;
-  g.use_prep_status = 1;
-  g.refs_host = 0;
   g.ctrl = static_cast<Control*>(workspace);
-  g.bounds = static_cast<const Bounds*>(bounds);
   return LaunchGuard(g, blocks, AsStream(stream));
 }
 
@@ -1392,7 +1412,9 @@ static int RunRows(const eps_hip_table* table, const eps_hip_optimizer* optimize
   EPS_HIP_TRY(CheckOptimizer(*optimizer));
   const hipStream_t s = AsStream(stream);
   auto* ctrl = static_cast<Control*>(workspace);
-  EPS_HIP_TRY(LaunchFill(reinterpret_cast<uint32_t*>(ctrl), 0, sizeof(Control) / 4, s));
+  // The control block starts at zero, except the status history (its last word).
+  static_assert(kHistoryWord + 1 == sizeof(Control) / 4, "history is the control block's last word");
+  EPS_HIP_TRY(LaunchFill(reinterpret_cast<uint32_t*>(ctrl), 0, kHistoryWord, s));
   if (!rows) return EPS_HIP_OK;
   if (!slots || !src) return Fail(EPS_HIP_INVALID_ARGUMENT, "null update buffers");
   GuardArgs g{};
@@ -1412,13 +1434,7 @@ static int RunRows(const eps_hip_table* table, const eps_hip_optimizer* optimize
     add(sources, references, kIndexSpan, src_values / table->dim);
   }
   const TableDesc d = MakeTable(*table, *optimizer);
-  g.t[0] = GuardTable{optimizer->beta1, optimizer->beta2, d.lr, optimizer->epsilon};
-  g.tables = 1;
-  g.reset_scale = 1;
-  g.use_prep_status = 1;  // the index checks report there
-  g.refs_host = std::max<uint64_t>(1, offsets ? references : 1);
-  g.ctrl = ctrl;
-  g.bounds = static_cast<const Bounds*>(bounds);
+  g.ctrl = ctrl;  // the index checks report to its prepare status
   EPS_HIP_TRY(LaunchGuard(g, blocks, s));
   RowArgs a{};
   a.t = d;
@@ -1430,6 +1446,7 @@ static int RunRows(const eps_hip_table* table, const eps_hip_optimizer* optimize
   a.rows = rows;
   a.ctrl = ctrl;
   a.bounds = static_cast<Bounds*>(bounds);
+  a.gs = GuardScalars{std::max<uint64_t>(1, offsets ? references : 1), 1};
   const uint32_t cls = DimClass(table->dim);
   const bool generic = cls == 5 || reinterpret_cast<uintptr_t>(src) % 16 != 0;
   a.log2g = generic ? 6 : Log2G(table->dim);
@@ -1438,10 +1455,10 @@ static int RunRows(const eps_hip_table* table, const eps_hip_optimizer* optimize
   if (vb > 0xffffffffull) return Fail(EPS_HIP_CAPACITY_EXCEEDED, "too many rows");
   a.vblocks = uint32_t(vb);
   auto kernel = generic ? RowUpdateKernel<true> : RowUpdateKernel<false>;
-  a.fallback = 0;
+  a.role = kDecide;
   hipLaunchKernelGGL(kernel, dim3(a.vblocks), dim3(kBlock), 0, s, a);
   EPS_HIP_LAUNCHED("row update");
-  a.fallback = 1;
+  a.role = kFallback;
   hipLaunchKernelGGL(kernel, dim3(std::min<uint32_t>(a.vblocks, kFallbackGrid)), dim3(kBlock), 0, s, a);
   EPS_HIP_LAUNCHED("row update (checked apply)");
   return EPS_HIP_OK;
@@ -1469,6 +1486,15 @@ int eps_hip_adam_compact(const eps_hip_table* table, const eps_hip_optimizer* op
 
 uint32_t* eps_hip_status_word(void* workspace) {
   return workspace ? &static_cast<Control*>(workspace)->status : nullptr;
+}
+
+uint32_t* eps_hip_status_history_word(void* workspace) {
+  return workspace ? &static_cast<Control*>(workspace)->history : nullptr;
+}
+
+int eps_hip_debug_set_spin_limit(uint32_t polls) {
+  g_spin_limit.store(polls, std::memory_order_relaxed);
+  return EPS_HIP_OK;
 }
 
 int eps_hip_read_status(void* workspace, uint32_t* status, void* stream) {

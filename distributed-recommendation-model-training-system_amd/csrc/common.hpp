@@ -2,6 +2,7 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
+#include <cstddef>
 #include <cstdint>
 #include <cstdio>
 #include <string>
@@ -40,8 +41,8 @@ constexpr uint32_t kHotChunk = 64;        // references per chunk of the hot-row
 // address serialise in the memory-side atomic unit.
 struct Control {
   uint32_t status;          // result of the last push/update (0 = applied)
-  uint32_t prep_status;     // prepare-time findings (bad slots)
-  uint32_t src_slots[kSrcSlots];    // max |gradient| as float bits, per slot (self-resetting)
+  uint32_t prep_status;     // prepare-time findings (bad slots, bad scales)
+  uint32_t src_slots[kSrcSlots];    // max |gradient| as float bits, per slot
   uint32_t scale_slots[kSrcSlots];  // max |scale| above 1.0 as float bits, per slot
   uint32_t valid_count;     // prepared occurrences that are on this device
   uint32_t mode;            // guard decision of the last push
@@ -50,11 +51,31 @@ struct Control {
   uint32_t tile_counter[kMaxPasses];
   uint32_t class_start[8];  // first sorted position of each dimension class (+ end)
   uint32_t long_count[kXcds * kHotBuckets];  // entries of each hot-row list
-  uint32_t pad[78];
+  uint32_t pad[77];
+  // Error bits of every push or update run in this workspace, OR-ed in as they
+  // are found; the per-call clears of the block skip this word (it starts at
+  // zero with the workspace and only eps_hip_status_history_word's user
+  // clears it).  A caller that overlaps many pushes checks it once.
+  uint32_t history;
 };
 static_assert(sizeof(Control) == 1024, "control block is 1 KiB");
+constexpr uint32_t kHistoryWord = offsetof(Control, history) / 4;
+
+// Error bits (a call that sets any of them wrote nothing, except a stall).
+constexpr uint32_t kErrorBits = EPS_HIP_STATUS_BAD_INDEX | EPS_HIP_STATUS_NONFINITE_GRAD |
+                                EPS_HIP_STATUS_REDUCE_OVERFLOW | EPS_HIP_STATUS_ADAM_OVERFLOW |
+                                EPS_HIP_STATUS_BAD_SCALE;
+constexpr uint32_t kHistoryBits = kErrorBits | EPS_HIP_STATUS_REJECTED | EPS_HIP_STATUS_STALLED;
 
 enum Mode : uint32_t { kFused = 0, kChecked = 1, kReject = 2 };
+
+// Adds status bits to the call's status word and its error bits to the
+// workspace history.
+__device__ __forceinline__ void ReportStatus(Control* ctrl, uint32_t bits) {
+  if (!bits) return;
+  atomicOr(&ctrl->status, bits);
+  if (bits & kHistoryBits) atomicOr(&ctrl->history, bits & kHistoryBits);
+}
 
 // Bounds domain: kBoundSlots x {W, M, V, unused} as non-negative float bits.
 struct Bounds { uint32_t v[kBoundSlots][4]; };
@@ -100,6 +121,11 @@ int Check(hipError_t e, const char* what);
 #define EPS_HIP_LAUNCHED(what) EPS_HIP_TRY(::eps_hip::Check(hipGetLastError(), what))
 
 inline hipStream_t AsStream(void* s) { return static_cast<hipStream_t>(s); }
+
+// Fills count u32 words with value on the stream (a kernel, no memset node
+// under graph capture), leaving word `keep` as it is.
+int LaunchFill(uint32_t* target, uint32_t value, uint64_t count, hipStream_t stream,
+               uint64_t keep = ~0ull);
 
 // ---- device helpers ----
 // Every buffer this library reads or writes is global memory (device memory,

@@ -229,10 +229,11 @@ __global__ void NormalizeMeanKernel(float* output, const uint64_t* lengths, uint
   }
 }
 
-__global__ void FillKernel(uint32_t* target, uint32_t value, uint64_t count) {
+// target[i] = value for i < count, except i == keep (kept as it is).
+__global__ void FillKernel(uint32_t* target, uint32_t value, uint64_t count, uint64_t keep) {
   for (uint64_t i = uint64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < count;
        i += uint64_t(blockDim.x) * gridDim.x)
-    target[i] = value;
+    if (i != keep) target[i] = value;
 }
 
 __device__ __forceinline__ uint64_t Mix(uint64_t x) {
@@ -366,10 +367,10 @@ int CheckTable(const eps_hip_table* t) {
 
 }  // namespace
 
-int LaunchFill(uint32_t* target, uint32_t value, uint64_t count, hipStream_t stream) {
+int LaunchFill(uint32_t* target, uint32_t value, uint64_t count, hipStream_t stream, uint64_t keep) {
   if (!count) return EPS_HIP_OK;
   hipLaunchKernelGGL(FillKernel, dim3(GridFor(count, 4096)), dim3(kBlock), 0, stream, target,
-                     value, count);
+                     value, count, keep);
   EPS_HIP_LAUNCHED("fill");
   return EPS_HIP_OK;
 }

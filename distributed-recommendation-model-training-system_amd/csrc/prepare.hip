@@ -24,8 +24,6 @@
 
 namespace eps_hip {
 
-int LaunchFill(uint32_t* target, uint32_t value, uint64_t count, hipStream_t stream);
-
 namespace {
 
 constexpr uint32_t kFlagAggregate = 1u << 30;
@@ -673,8 +671,9 @@ int eps_hip_prepare(const eps_hip_table* tables, uint32_t table_count,
   auto* ws = static_cast<uint8_t*>(workspace);
   auto* ctrl = reinterpret_cast<Control*>(ws);
   const hipStream_t s = AsStream(stream);
-  // Control block, histograms and look-back flags start at zero.
-  EPS_HIP_TRY(LaunchFill(reinterpret_cast<uint32_t*>(ws), 0, L.keys_a / 4, s));
+  // Control block (but its status history), histograms and look-back flags
+  // start at zero.
+  EPS_HIP_TRY(LaunchFill(reinterpret_cast<uint32_t*>(ws), 0, L.keys_a / 4, s, kHistoryWord));
   if (!plan.occurrences) return EPS_HIP_OK;
 
   PrepArgs args{};

@@ -29,8 +29,9 @@ STATUS_REDUCE_OVERFLOW = 0x4
 STATUS_ADAM_OVERFLOW = 0x8
 STATUS_REJECTED = 0x10
 STATUS_STALLED = 0x20
+STATUS_BAD_SCALE = 0x40
 STATUS_CHECKED_PATH = 0x100
-STATUS_ERRORS = 0xF | STATUS_STALLED
+STATUS_ERRORS = 0xF | STATUS_REJECTED | STATUS_STALLED | STATUS_BAD_SCALE
 MAX_FEATURES = 32
 MAX_TABLES = 32
 MAX_GATHER_PARTS = 32
@@ -101,6 +102,8 @@ SYMBOLS = {
                                        C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64, C.c_uint64,
                                        C.c_void_p, C.c_void_p, C.c_void_p]),
     "eps_hip_status_word": (C.c_void_p, [C.c_void_p]),
+    "eps_hip_status_history_word": (C.c_void_p, [C.c_void_p]),
+    "eps_hip_debug_set_spin_limit": (C.c_int, [C.c_uint32]),
     "eps_hip_read_status": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p]),
     "eps_hip_fill_u32": (C.c_int, [C.c_void_p, C.c_uint32, C.c_uint64, C.c_void_p]),
 }
@@ -223,6 +226,10 @@ class DeviceShard:
     def reserve(self, occurrences):
         need = lib().eps_hip_push_workspace_bytes(int(occurrences))
         if need > self.ws_bytes:
+            if any(w is not None for w in self.wss):
+                # Work queued on any stream may still read the old workspaces:
+                # drain the device before their memory can be handed out again.
+                self.torch.cuda.synchronize()
             self.wss = [self.torch.zeros((need + 3) // 4, dtype=self.torch.int32, device=self.device)
                         for _ in self.wss]
             self.ws_bytes = need
@@ -316,8 +323,12 @@ class DeviceShard:
                                     _ptr(self.wss[slot]), self.ws_bytes, _stream(self.torch, stream)))
 
     def push(self, feats, stream=None, advance=True, events=None, slot=0):
-        """Fused aggregation + Adam of a prepared push (asynchronous).  Powers are
-        advanced optimistically; check status() after the stream drains.
+        """Fused aggregation + Adam of a prepared push.  With `advance` the call
+        waits for the push, and advances the optimizer powers of the pushed
+        tables only if it applied (a rejected update leaves them unchanged, as
+        ApplyLazyAdam does, src/update/lazy_adam.cpp:39-41); it returns the
+        status.  Callers that overlap pushes pass advance=False (asynchronous),
+        advance the powers themselves and check history() afterwards.
         `events` = (start, end) torch events recorded around the fused pass;
         `slot` = the workspace the batch was prepared in."""
         arr = self._push_args(feats)
@@ -334,13 +345,28 @@ class DeviceShard:
             events[1].record(stream)
         check(L.eps_hip_push_end(*args))
         if advance:
-            self.advance_powers([f.table for f in feats])
+            status = self.status(stream, slot=slot)
+            if status & STATUS_ERRORS == 0:
+                self.advance_powers([f.table for f in feats])
+            return status
+        return None
 
     def status(self, stream=None, workspace=None, slot=0):
         out = C.c_uint32()
         ws = self.wss[slot] if workspace is None else workspace
         check(lib().eps_hip_read_status(_ptr(ws), C.byref(out), _stream(self.torch, stream)))
         return out.value
+
+    def history(self, slot=0):
+        """Failure bits of every push run in workspace `slot` (waits for the device)."""
+        ws = self.wss[slot]
+        index = (lib().eps_hip_status_history_word(_ptr(ws)) - ws.data_ptr()) // 4
+        self.torch.cuda.synchronize()
+        return int(ws[index].item()) & 0xFFFFFFFF
+
+    def clear_history(self, slot=0, stream=None):
+        check(lib().eps_hip_fill_u32(lib().eps_hip_status_history_word(_ptr(self.wss[slot])), 0, 1,
+                                     _stream(self.torch, stream)))
 
     def unique(self, feats, stream=None):
         """(unique_slots, unique_tables, occurrence_to_unique, count) of a prepared push."""

@@ -225,6 +225,43 @@ class Ragged8(Workload):
             feats.append(Feature(i, i, WEIGHTED_SUM, keys, offsets, vlen, weights, grad))
         return feats
 
+    # ---- cache-tier row moves ----
+    MOVE_FRACTION = 0.05
+    MOVE_LAG = 3  # a row written back after step k is admitted again at step k + MOVE_LAG
+
+    def move_counts(self):
+        """Rows admitted (and written back) per step and table: 5% of the
+        expected touched rows."""
+        return [max(1, int(round(self.MOVE_FRACTION * z.expected_unique(8 * self.bags))))
+                for z in self.zipf]
+
+    def admissions(self, touched):
+        """Admission sets of a cycle of batches.  `touched[j][t]` = the unique
+        keys batch j touches in table t (the batches repeat with period
+        len(touched) >= MOVE_LAG).  Batch j admits A_j: a seeded sample of
+        move_counts()[t] keys of batch j that neither of the previous
+        MOVE_LAG - 1 batches touches.  The rows written back after batch j are
+        A_{j + MOVE_LAG}: they are resident at batch j (no pending admission
+        holds them), untouched while they sit in host memory, and admitted
+        back, with the state they were written back with, before the batch
+        that needs them."""
+        period = len(touched)
+        if period < self.MOVE_LAG:
+            raise ValueError("tier moves need at least MOVE_LAG batches in the cycle")
+        counts = self.move_counts()
+        out = []
+        for j in range(period):
+            rng = np.random.default_rng((6000 + self.seed) * 100003 + j)
+            per_table = []
+            for t, count in enumerate(counts):
+                recent = [touched[(j - d) % period][t] for d in range(1, self.MOVE_LAG)]
+                free = np.setdiff1d(touched[j][t], np.concatenate(recent), assume_unique=False)
+                if len(free) < count:
+                    raise ValueError(f"batch {j} table {t}: only {len(free)} admissible rows")
+                per_table.append(np.sort(rng.choice(free, count, replace=False)).astype(np.uint64))
+            out.append(per_table)
+        return out
+
 
 def algorithmic_bytes(tables, feats, unique_rows):
     """Compulsory HBM bytes of one pull + push step (per table: unique weight rows,

@@ -54,6 +54,9 @@ extern "C" {
 #define EPS_HIP_STATUS_ADAM_OVERFLOW 0x8u    /* lazy_adam.cpp:19-20 */
 #define EPS_HIP_STATUS_REJECTED 0x10u        /* nothing was written */
 #define EPS_HIP_STATUS_STALLED 0x20u         /* internal: a hot-row hand-over timed out */
+#define EPS_HIP_STATUS_BAD_SCALE 0x40u       /* a non-finite reference scale or per-id weight,
+                                                or a negative compact scale
+                                                (compact_gradients.cpp:21) */
 #define EPS_HIP_STATUS_CHECKED_PATH 0x100u   /* info: the two-pass path ran */
 
 /* Per-launch limits (descriptors travel as kernel arguments). */
@@ -226,12 +229,29 @@ int eps_hip_adam_compact(const eps_hip_table* table, const eps_hip_optimizer* op
                          uint64_t references, void* workspace, void* bounds, void* stream);
 
 /* ---- status ---- */
-/* Device address of the status word inside a push or update workspace. */
+/* Device address of the status word inside a push or update workspace.  A
+ * call's status is complete once its last enqueued kernel has run (a push:
+ * after eps_hip_push_end).  Any bit of 0x7f means the call failed: with every
+ * bit but EPS_HIP_STATUS_STALLED set, nothing was written.  A stall (a hot-row
+ * hand-over that exceeded its spin limit, which no correct run reaches)
+ * leaves the hot rows whose work units completed before it updated and every
+ * other row unchanged. */
 uint32_t* eps_hip_status_word(void* workspace);
+/* Device address of the workspace's status history: the OR of the failure
+ * bits of every push or update run in it since it was zeroed (a workspace
+ * must be zero-filled once when it is allocated; the calls themselves never
+ * clear this word).  For callers that enqueue many pushes without reading
+ * each status; clear it with eps_hip_fill_u32. */
+uint32_t* eps_hip_status_history_word(void* workspace);
 /* Waits for `stream` and copies the workspace status word to *status. */
 int eps_hip_read_status(void* workspace, uint32_t* status, void* stream);
 /* Fills count u32 words with value (a kernel, safe under graph capture). */
 int eps_hip_fill_u32(uint32_t* target, uint32_t value, uint64_t count, void* stream);
+
+/* Test hook: polls of an LDS hand-over wait of the hot-row kernel before it
+ * gives up (default 4194304; process-wide).  0 makes every such wait give up
+ * at once, so tests can drive the stall path from the host. */
+int eps_hip_debug_set_spin_limit(uint32_t polls);
 
 #ifdef __cplusplus
 }
