@@ -248,6 +248,10 @@ def profile_traffic(workload):
     return None
 
 
+def progress(message):
+    print(f"[bench] {message}", file=sys.stderr, flush=True)
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -286,6 +290,7 @@ def main(argv=None):
     wl = make_workload(W, cfg["workload"])
     batches = [wl.batch(i) for i in range(nbatch)]
     stats = [batch_stats(W, wl, b, pull) for b in batches]
+    progress(f"config {args.config} ({cfg['workload']}): {nbatch} batches generated")
     shard = H.DeviceShard(torch, wl.tables, max_occurrences=max(s["lookups"] for s in stats), workspaces=2)
     if cfg["workload"] == "movielens":
         for t, state in enumerate(wl.initial_state()):
@@ -306,6 +311,7 @@ def main(argv=None):
     for k in range(warmup):
         pipe.step(k)
     pipe.check()
+    progress(f"{warmup} warm-up steps done")
     # Timed steps carry only the two events around the fused update (its
     # roofline), on every FUSED_EVERY-th step: every timing event costs GPU
     # time on its stream, and many outstanding timing events can stall the
@@ -329,6 +335,7 @@ def main(argv=None):
         pipe.step(warmup + steps + k, phases=events[k])
     torch.cuda.synchronize()
     pipe.check()
+    progress(f"{steps} timed steps: {elapsed * 1e3 / steps:.4f} ms/step")
 
     ms = elapsed * 1e3 / steps
     used = [stats[(warmup + k) % len(stats)] for k in range(steps)]
@@ -406,6 +413,7 @@ def main(argv=None):
             base["all_cores"] = cpu_baseline(wl, batches, shards, cfg["cpu_fraction"], budget_s=10.0,
                                              max_steps=200 if args.config == 1 else 8, pull=pull)
         result["cpu_baseline"] = base
+        progress("cpu baseline done")
     print(json.dumps(result))
     return 0
 
