@@ -74,6 +74,13 @@ SYMBOLS = {
     "eps_hip_scatter_rows": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p,
                                        C.c_void_p]),
     "eps_hip_gather_rows": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p]),
+    "eps_hip_index_bytes": (C.c_uint64, [C.c_uint64]),
+    "eps_hip_index_clear": (C.c_int, [C.c_void_p, C.c_uint64, C.c_void_p]),
+    "eps_hip_index_insert": (C.c_int, [C.c_void_p, C.c_uint64, C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p,
+                                       C.c_void_p]),
+    "eps_hip_index_remove": (C.c_int, [C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint64, C.c_void_p, C.c_void_p]),
+    "eps_hip_resolve": (C.c_int, [C.c_void_p, C.c_uint64, C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64,
+                                  C.c_uint64, C.c_void_p, C.c_void_p, C.c_void_p]),
     "eps_hip_gather": (C.c_int, [C.c_void_p, C.c_uint32, C.c_void_p, C.c_void_p]),
     "eps_hip_add_contribution": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64,
                                            C.c_uint32, C.c_void_p]),

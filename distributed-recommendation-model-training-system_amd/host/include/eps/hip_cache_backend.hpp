@@ -5,8 +5,9 @@
 // (include/eps/cuda_cache_backend.hpp:5-37): same operations, options and
 // statistics, same error behaviour, one FIFO worker per backend.  Device work
 // goes through the C ABI of include/eps_hip.h (libeps_hip.so); this class owns
-// the AoS [w | m | v] tables, the slot free lists, the row generations and
-// update counters, pinned staging, one stream and the device-output budget.
+// the AoS [w | m | v] tables with a device key -> slot index each, the slot
+// stacks, the row generations and update counters, pinned staging, one stream
+// and the device-output budget.
 #pragma once
 
 #include <filesystem>
@@ -101,6 +102,20 @@ class HipCacheBackend final : public GpuCacheAgent {
   std::future<Result<SnapshotFile>> WriteSnapshot(std::filesystem::path file, SnapshotIdentity identity,
                                                   std::vector<SnapshotTable> tables,
                                                   std::vector<RowState> host_rows);
+
+  // Device restore from a shard snapshot file (formats 1 and 2): the plan's
+  // rows are read from the file (the reference's ReadSnapshot checks,
+  // src/store/snapshot.cpp:223-268: identity, schema, finite state,
+  // non-negative second moments, checksum, no trailing bytes) and admitted
+  // straight into HBM with their update counters, as Load admits rows
+  // (src/cuda/cache_backend.cu:390-462: same plan checks, slot reserve and
+  // LIFO slots, all-or-nothing).  `identity` names the checkpoint (the file's
+  // run, shard, shard count and epoch must equal it); each plan row's table
+  // must be defined here as the file defines it.  The reference restores into
+  // its CPU store and moves GPU rows back with Load, 64 rows per request.
+  std::future<Result<std::vector<LocatedRow>>> RestoreSnapshot(std::filesystem::path file,
+                                                               SnapshotIdentity identity,
+                                                               MigrationPlan plan);
 
  private:
   struct Impl;

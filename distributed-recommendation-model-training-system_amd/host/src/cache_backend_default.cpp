@@ -1,30 +1,29 @@
 // cache_backend_default.cpp -- the interface's default ApplyCompact.
 //
-// Reference: src/cache/host_backend.cpp:12-16.  Part of the standalone
-// library only; a build beside the reference links the reference's own
-// definition instead of this file.
+// Reference: src/cache/host_backend.cpp:12-16 (the default expands the packet
+// on the host and applies it as ApplyHost).  Part of the standalone library
+// only; a build beside the reference links the reference's own definition
+// instead of this file.
 #include <future>
 #include <new>
 #include <utility>
 
 #include "eps/cache_backend.hpp"
-#include "executor.hpp"
+#include "job_queue.hpp"
+#include "packet.hpp"
 
 namespace eps {
 
-// Expands the CSR on the host and applies it as ApplyHost.
 std::future<Result<Ack>> CacheBackend::ApplyCompact(UpdateContext context, CompactGradients packet) {
+  std::promise<Result<Ack>> refused;
   try {
-    return ApplyHost(std::move(context), hip_detail::ExpandCompact(packet));
-  } catch (const hip_detail::Failure& f) {
-    std::promise<Result<Ack>> p;
-    p.set_value(f.error());
-    return p.get_future();
+    return ApplyHost(std::move(context), hipbk::ExpandPacket(packet));
+  } catch (const hipbk::Fault& f) {
+    refused.set_value(f.error);
   } catch (const std::bad_alloc&) {
-    std::promise<Result<Ack>> p;
-    p.set_value(Error{Error::Code::capacity_exceeded, "compact gradient allocation failed"});
-    return p.get_future();
+    refused.set_value(Error{Error::Code::capacity_exceeded, "compact packet expansion ran out of memory"});
   }
+  return refused.get_future();
 }
 
 }  // namespace eps

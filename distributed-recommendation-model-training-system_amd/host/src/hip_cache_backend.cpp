@@ -1,711 +1,838 @@
-// hip_cache_backend.cpp -- eps::HipCacheBackend over the gfx950 kernel library.
+// hip_cache_backend.cpp -- eps::HipCacheBackend: the GPU cache agent of a
+// parameter shard on one MI355X, over the kernel library's C ABI.
 //
-// Behaviour follows the reference CudaCacheBackend (src/cuda/cache_backend.cu)
-// operation by operation -- validation before mutation, the same error codes
-// and messages' meaning, LIFO slot reuse, row generations, atomic Load with
-// rollback, device outputs that outlive the backend -- while the device work is
-// the C ABI of include/eps_hip.h:
-//   GatherHost / GatherDevice -> eps_hip_gather (all features in one launch)
-//   ApplyHost                 -> eps_hip_adam_rows (guarded single pass)
-//   ApplyCompact              -> eps_hip_adam_compact (CSR reduce fused with Adam)
-//   Load / ReadBack           -> eps_hip_scatter_rows / eps_hip_gather_rows
-//   AssembleFeatures          -> eps_hip_fill_u32, eps_hip_add_contribution,
-//                                eps_hip_normalize_mean
-//   PushDevice                -> eps_hip_prepare + eps_hip_push (device gradients)
-//   WriteSnapshot             -> eps_hip_gather_rows into pinned staging, double buffered
-// Occurrence slots are resolved once per unique row (the reference looks the
-// row up in a hash map once per occurrence, src/cuda/cache_backend.cu:279-291).
+// Operation          device work (include/eps_hip.h)
+//   Define           device table + key index (eps_hip_index_clear)
+//   Load             eps_hip_scatter_rows, eps_hip_index_insert
+//   GatherHost/Device eps_hip_resolve (key index), eps_hip_gather
+//   ApplyHost        eps_hip_adam_rows
+//   ApplyCompact     eps_hip_adam_compact
+//   ReadBack         eps_hip_gather_rows
+//   CommitEviction   eps_hip_index_remove
+//   AssembleFeatures eps_hip_fill_u32, eps_hip_add_contribution, eps_hip_normalize_mean
+//   PushDevice       eps_hip_resolve, eps_hip_prepare, eps_hip_push
+//   WriteSnapshot    eps_hip_gather_rows into pinned staging, double buffered
+//   RestoreSnapshot  eps_hip_scatter_rows, eps_hip_index_insert
+//
+// The observable contract is the reference CudaCacheBackend's
+// (src/cuda/cache_backend.cu; include/eps/cache_backend.hpp:12-29): the same
+// checks before any state changes and the same error codes, slots handed out
+// from slot 0 and reused last-freed first, row generations and update counters
+// kept by the agent, atomic loads, device outputs that outlive the backend.
+// The design is this file's: every request is resolved against the host-side
+// residency of its unique rows only (generation, owner, counter checks: O(rows),
+// not O(occurrences)), its arrays are carved out of one pinned + device
+// transfer area and uploaded with one copy, and each key occurrence is turned
+// into a slot on the device by the table's key index, which also checks the
+// caller's occurrence map.  Gathers and pushes share that resolution and
+// build their kernel descriptors from it.
 #include "eps/hip_cache_backend.hpp"
 
 #include <hip/hip_runtime_api.h>
 
 #include <algorithm>
+#include <array>
 #include <atomic>
 #include <cmath>
+#include <cstring>
 #include <limits>
 #include <map>
-#include <numeric>
+#include <optional>
 #include <set>
 #include <unordered_map>
+#include <unordered_set>
 #include <utility>
 
 #include "eps_hip.h"
-#include "executor.hpp"
+#include "job_queue.hpp"
+#include "packet.hpp"
+#include "snapshot_reader.hpp"
 #include "snapshot_writer.hpp"
 
 namespace eps {
 namespace {
 
-using hip_detail::Failure;
-using hip_detail::Require;
+using hipbk::Expect;
+using hipbk::Raise;
+using Code = Error::Code;
 
-void Hip(hipError_t status) {
-  if (status != hipSuccess)
-    throw Failure({status == hipErrorOutOfMemory ? Error::Code::capacity_exceeded
-                                                 : Error::Code::run_failed,
-                   hipGetErrorString(status)});
+constexpr std::uint64_t kHole = ~0ull;
+constexpr std::size_t kQueueDepth = 128;
+constexpr std::uint32_t kFailureBits = 0x7f;
+
+void HipOk(hipError_t e, const char* what) {
+  if (e == hipSuccess) return;
+  Raise(e == hipErrorOutOfMemory ? Code::capacity_exceeded : Code::run_failed,
+        std::string(what) + ": " + hipGetErrorString(e));
 }
 
-// C ABI status: 0 ok, else Error::Code + 1.
-void Abi(int rc) {
+// A C ABI result (0, or Error::Code + 1).
+void AbiOk(int rc) {
   if (rc == EPS_HIP_OK) return;
-  const int code = rc >= EPS_HIP_INVALID_ARGUMENT && rc <= EPS_HIP_RUN_FAILED ? rc - 1
-                                                                              : int(Error::Code::run_failed);
-  throw Failure({Error::Code(code), eps_hip_last_error()});
+  const bool known = rc >= EPS_HIP_INVALID_ARGUMENT && rc <= EPS_HIP_RUN_FAILED;
+  Raise(known ? Code(rc - 1) : Code::run_failed, eps_hip_last_error());
 }
 
-struct Memory {
-  void* pointer = nullptr;
-  int device = 0;
-  bool pinned = false;
+std::uint64_t RoundUp(std::uint64_t x, std::uint64_t to) { return (x + to - 1) / to * to; }
+
+// ---------------------------------------------------------------------------
+// Memory the backend owns: device memory or pinned host memory.
+class Memory {
+ public:
   Memory() = default;
   Memory(const Memory&) = delete;
   Memory& operator=(const Memory&) = delete;
-  ~Memory() { Reset(); }
-  void Reset() noexcept {
-    if (!pointer) return;
-    (void)hipSetDevice(device);
-    if (pinned) (void)hipHostFree(pointer); else (void)hipFree(pointer);
-    pointer = nullptr;
-  }
-  void Allocate(std::uint64_t bytes, int ordinal, bool host = false) {
-    device = ordinal;
-    pinned = host;
-    Hip(hipSetDevice(device));
+  ~Memory() { Release(); }
+  void Acquire(int device, std::uint64_t bytes, bool pinned) {
+    Release();
+    device_ = device;
+    pinned_ = pinned;
+    bytes_ = bytes;
+    HipOk(hipSetDevice(device), "select device");
     if (!bytes) return;
-    if (host) Hip(hipHostMalloc(&pointer, bytes, hipHostMallocDefault));
-    else Hip(hipMalloc(&pointer, bytes));
+    if (pinned) HipOk(hipHostMalloc(&p_, bytes, hipHostMallocDefault), "pinned host allocation");
+    else HipOk(hipMalloc(&p_, bytes), "device allocation");
+  }
+  void Release() noexcept {
+    if (!p_) return;
+    (void)hipSetDevice(device_);
+    if (pinned_) (void)hipHostFree(p_);
+    else (void)hipFree(p_);
+    p_ = nullptr;
+  }
+  template <typename T = void>
+  T* Get() const { return static_cast<T*>(p_); }
+  std::uint64_t bytes() const { return bytes_; }
+
+ private:
+  void* p_ = nullptr;
+  int device_ = 0;
+  bool pinned_ = false;
+  std::uint64_t bytes_ = 0;
+};
+
+// ---------------------------------------------------------------------------
+// The staging of one request: a pinned host area and a device area of the
+// same size, carved front to back.  Inputs are written into the host side
+// and uploaded with one copy; device-only pieces (kernel outputs) follow them.
+class Transfer {
+ public:
+  template <typename T>
+  struct Piece {
+    T* host;
+    T* device;
+    std::uint64_t count;
+  };
+
+  void Open(int device, std::uint64_t bytes) {
+    host_.Acquire(device, bytes, true);
+    device_.Acquire(device, bytes, false);
+    capacity_ = bytes;
+  }
+  void Reset() { used_ = uploaded_ = 0; }
+  std::uint64_t capacity() const { return capacity_; }
+  std::uint64_t device_bytes() const { return device_.bytes(); }
+
+  template <typename T>
+  Piece<T> Take(std::uint64_t count) {
+    const std::uint64_t at = RoundUp(used_, 256);
+    Expect(count <= (capacity_ - std::min(at, capacity_)) / sizeof(T), "request exceeds the transfer staging",
+           Code::capacity_exceeded);
+    used_ = at + count * sizeof(T);
+    auto* h = reinterpret_cast<T*>(host_.Get<unsigned char>() + at);
+    auto* d = reinterpret_cast<T*>(device_.Get<unsigned char>() + at);
+    return {h, d, count};
   }
   template <typename T>
-  T* As() const { return static_cast<T*>(pointer); }
-};
-
-struct Stream {
-  hipStream_t value = nullptr;
-  int device;
-  explicit Stream(int d) : device(d) {
-    Hip(hipSetDevice(d));
-    Hip(hipStreamCreateWithFlags(&value, hipStreamNonBlocking));
+  Piece<T> Copy(const std::vector<T>& values) {
+    Piece<T> p = Take<T>(values.size());
+    if (!values.empty()) std::memcpy(p.host, values.data(), values.size() * sizeof(T));
+    return p;
   }
-  ~Stream() {
-    (void)hipSetDevice(device);
-    if (value) (void)hipStreamDestroy(value);
+  // Copies everything taken since the last upload to the device.
+  void Upload(hipStream_t stream) {
+    if (used_ > uploaded_)
+      HipOk(hipMemcpyAsync(device_.Get<unsigned char>() + uploaded_, host_.Get<unsigned char>() + uploaded_,
+                           used_ - uploaded_, hipMemcpyHostToDevice, stream),
+            "staging upload");
+    uploaded_ = used_;
   }
-};
-
-struct Event {
-  hipEvent_t value = nullptr;
-  int device;
-  explicit Event(int d) : device(d) {
-    Hip(hipSetDevice(d));
-    Hip(hipEventCreateWithFlags(&value, hipEventDisableTiming));
-  }
-  ~Event() {
-    (void)hipSetDevice(device);
-    if (value) (void)hipEventDestroy(value);
-  }
-};
-
-struct OutputBudget {
-  std::atomic<std::uint64_t> used{0};
-  std::atomic<std::uint64_t> allocations{0};
-  std::uint64_t limit = 0;
-};
-
-// One device output allocation, charged to the backend's budget until the last
-// view of it is released (possibly after the backend itself is gone).
-struct Allocation {
-  Memory memory;
-  Event ready;
-  std::shared_ptr<OutputBudget> budget;
-  std::uint64_t bytes;
-  Allocation(int device, std::uint64_t n, std::shared_ptr<OutputBudget> b)
-      : ready(device), budget(std::move(b)), bytes(n) {
-    Require(n <= budget->limit, "device output is too large", Error::Code::capacity_exceeded);
-    const auto before = budget->used.fetch_add(n);
-    if (before > budget->limit - n) {
-      budget->used.fetch_sub(n);
-      throw Failure({Error::Code::capacity_exceeded, "outstanding device output budget exhausted"});
-    }
-    try {
-      memory.Allocate(n, device);
-      ++budget->allocations;
-    } catch (...) {
-      budget->used.fetch_sub(n);
-      throw;
-    }
-  }
-  ~Allocation() {
-    memory.Reset();
-    budget->used.fetch_sub(bytes);
-  }
-};
-
-class TensorView final : public DeviceTensor {
- public:
-  TensorView(std::shared_ptr<Allocation> owner, std::uint64_t offset, std::uint64_t count)
-      : owner_(std::move(owner)), offset_(offset), count_(count) {}
-  void* data() const override {
-    return owner_->memory.pointer ? owner_->memory.As<float>() + offset_ : nullptr;
-  }
-  std::uint64_t elements() const override { return count_; }
-  int device() const override { return owner_->memory.device; }
-  void WaitOnStream(void* stream) const override {
-    Hip(hipSetDevice(device()));
-    Hip(hipStreamWaitEvent(static_cast<hipStream_t>(stream), owner_->ready.value, 0));
-  }
-  std::vector<float> CopyToHost() const override {
-    Hip(hipSetDevice(device()));
-    Hip(hipEventSynchronize(owner_->ready.value));
-    std::vector<float> values(count_);
-    if (count_) Hip(hipMemcpy(values.data(), data(), count_ * 4, hipMemcpyDeviceToHost));
-    return values;
+  // Marks what was taken so far as device-only (it is not uploaded).
+  void Skip() { uploaded_ = used_; }
+  template <typename T>
+  void Download(const Piece<T>& p, hipStream_t stream) {
+    if (p.count)
+      HipOk(hipMemcpyAsync(p.host, p.device, p.count * sizeof(T), hipMemcpyDeviceToHost, stream), "staging download");
   }
 
  private:
-  std::shared_ptr<Allocation> owner_;
+  Memory host_, device_;
+  std::uint64_t capacity_ = 0, used_ = 0, uploaded_ = 0;
+};
+
+// ---------------------------------------------------------------------------
+// Device outputs: one allocation per request, viewed by one tensor per
+// feature; the allocation lives while any view does (past the backend) and
+// is charged to the backend's outstanding-output budget meanwhile.
+struct OutputLedger {
+  std::atomic<std::uint64_t> used{0}, blocks{0};
+  std::uint64_t limit = 0;
+};
+
+class OutputBlock {
+ public:
+  OutputBlock(std::shared_ptr<OutputLedger> ledger, int device, std::uint64_t bytes)
+      : ledger_(std::move(ledger)), device_(device), bytes_(bytes) {
+    Expect(bytes <= ledger_->limit, "device output larger than the output budget", Code::capacity_exceeded);
+    std::uint64_t seen = ledger_->used.load();
+    do {
+      Expect(seen <= ledger_->limit - bytes, "outstanding device outputs exhaust the budget",
+             Code::capacity_exceeded);
+    } while (!ledger_->used.compare_exchange_weak(seen, seen + bytes));
+    try {
+      memory_.Acquire(device, bytes, false);
+      HipOk(hipEventCreateWithFlags(&ready_, hipEventDisableTiming), "output event");
+    } catch (...) {
+      memory_.Release();
+      ledger_->used.fetch_sub(bytes);
+      throw;
+    }
+    ledger_->blocks.fetch_add(1);
+  }
+  ~OutputBlock() {
+    memory_.Release();
+    if (ready_) {
+      (void)hipSetDevice(device_);
+      (void)hipEventDestroy(ready_);
+    }
+    ledger_->used.fetch_sub(bytes_);
+  }
+  float* data() const { return memory_.Get<float>(); }
+  hipEvent_t ready() const { return ready_; }
+  int device() const { return device_; }
+
+ private:
+  std::shared_ptr<OutputLedger> ledger_;
+  int device_;
+  std::uint64_t bytes_;
+  Memory memory_;
+  hipEvent_t ready_ = nullptr;
+};
+
+class OutputSlice final : public DeviceTensor {
+ public:
+  OutputSlice(std::shared_ptr<OutputBlock> block, std::uint64_t offset, std::uint64_t count)
+      : block_(std::move(block)), offset_(offset), count_(count) {}
+  void* data() const override { return block_->data() ? block_->data() + offset_ : nullptr; }
+  std::uint64_t elements() const override { return count_; }
+  int device() const override { return block_->device(); }
+  void WaitOnStream(void* stream) const override {
+    HipOk(hipSetDevice(block_->device()), "select device");
+    HipOk(hipStreamWaitEvent(static_cast<hipStream_t>(stream), block_->ready(), 0), "wait for device output");
+  }
+  std::vector<float> CopyToHost() const override {
+    HipOk(hipSetDevice(block_->device()), "select device");
+    HipOk(hipEventSynchronize(block_->ready()), "wait for device output");
+    std::vector<float> out(count_);
+    if (count_) HipOk(hipMemcpy(out.data(), data(), count_ * 4, hipMemcpyDeviceToHost), "device output copy");
+    return out;
+  }
+
+ private:
+  std::shared_ptr<OutputBlock> block_;
   std::uint64_t offset_, count_;
 };
 
-uint32_t PoolingCode(Pooling p) {
-  switch (p) {
-    case Pooling::sum: return EPS_HIP_POOL_SUM;
-    case Pooling::mean: return EPS_HIP_POOL_MEAN;
-    default: return EPS_HIP_POOL_SEQUENCE;
+// ---------------------------------------------------------------------------
+// One table on the device: the AoS [w | m | v] rows, the key index, the slot
+// stack (its back is the next slot handed out) and the residency of every
+// row the agent holds.
+struct Resident {
+  LocatedRow where;
+  std::uint64_t updates;
+};
+
+struct SlotTable {
+  TableDefinition definition;
+  eps_hip_table abi{};
+  Memory state, index;
+  std::uint64_t index_capacity = 0;
+  std::vector<std::uint64_t> free_slots;
+  std::unordered_map<Key, Resident> rows;
+
+  std::uint32_t dim() const { return definition.dimension; }
+  std::uint64_t TakeSlot() {
+    const std::uint64_t s = free_slots.back();
+    free_slots.pop_back();
+    return s;
   }
+};
+
+bool Finite(const std::vector<float>& v) {
+  return std::all_of(v.begin(), v.end(), [](float x) { return std::isfinite(x); });
 }
 
 }  // namespace
 
+// ---------------------------------------------------------------------------
 struct HipCacheBackend::Impl {
-  struct Entry {
-    LocatedRow location;
-    std::uint64_t updates;
-  };
-  struct Table {
-    TableDefinition definition;
-    Memory state;
-    std::vector<std::uint64_t> free;  // LIFO: slot 0 is handed out first
-    std::unordered_map<Key, Entry> rows;
-    eps_hip_table abi{};
-  };
-  struct GatherPart {
-    std::uint32_t feature;
-    Table* table;
-    Pooling pooling;
-    std::uint64_t slot_offset, offsets_offset, output_offset, rows;
-    const float* source;
-    std::uint64_t stride, source_rows;
-  };
-
-  explicit Impl(HipCacheOptions o)
-      : options(o), stream((Validate(o), o.device)), done(o.device),
-        output_budget(std::make_shared<OutputBudget>()) {
-    Abi(eps_hip_device_check(o.device));
-    output_budget->limit = o.outstanding_output_bytes;
-    host_values.Allocate(o.transfer_bytes, o.device, true);
-    host_indices.Allocate(o.transfer_bytes, o.device, true);
-    device_values.Allocate(o.transfer_bytes, o.device);
-    device_indices.Allocate(o.transfer_bytes, o.device);
-    device_transient.Allocate(o.transfer_bytes, o.device);
-    workspace.Allocate(eps_hip_update_workspace_bytes(), o.device);
-    bounds.Allocate(eps_hip_bounds_bytes(), o.device);
-    gather_status.Allocate(256, o.device);
-    Abi(eps_hip_bounds_reset(bounds.pointer, stream.value));
-    Finish();
-    worker = std::make_unique<hip_detail::Worker>(128);
+  explicit Impl(const HipCacheOptions& o) : options(o), ledger(std::make_shared<OutputLedger>()) {
+    Expect(o.output_alignment >= 4 && o.output_alignment <= 256 && (o.output_alignment & (o.output_alignment - 1)) == 0 &&
+               o.rows_per_table > 0 && o.rows_per_table <= (1ull << 31) && o.transfer_bytes >= 1024 &&
+               o.transfer_bytes <= (2ull << 30),
+           "invalid HIP cache options");
+    ledger->limit = o.outstanding_output_bytes;
+    AbiOk(eps_hip_device_check(o.device));
+    HipOk(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "create stream");
+    transfer.Open(o.device, o.transfer_bytes);
+    bounds.Acquire(o.device, eps_hip_bounds_bytes(), false);
+    AbiOk(eps_hip_bounds_reset(bounds.Get(), stream));
+    update_ws.Acquire(o.device, eps_hip_update_workspace_bytes(), false);
+    AbiOk(eps_hip_fill_u32(update_ws.Get<std::uint32_t>(), 0, update_ws.bytes() / 4, stream));
+    flags.Acquire(o.device, 256, false);
+    flags_host.Acquire(o.device, 256, true);
+    Await();
+    queue = std::make_unique<hipbk::JobQueue>(kQueueDepth);
   }
   ~Impl() {
-    worker.reset();
+    queue.reset();  // runs what was queued, then stops
     (void)hipSetDevice(options.device);
-    (void)hipStreamSynchronize(stream.value);
+    if (stream) {
+      (void)hipStreamSynchronize(stream);
+      (void)hipStreamDestroy(stream);
+    }
   }
 
-  // CudaCacheOptions limits (src/cuda/cache_backend.cu:208-214), widened for
-  // MI355X: 2^31 rows per table and 2 GiB of staging.
-  static void Validate(const HipCacheOptions& o) {
-    Require(o.output_alignment >= 4 && o.output_alignment <= 256 &&
-                (o.output_alignment & (o.output_alignment - 1)) == 0 && o.rows_per_table > 0 &&
-                o.rows_per_table <= (1ULL << 31) && o.transfer_bytes >= 1024 &&
-                o.transfer_bytes <= (2ULL << 30),
-            "invalid HIP cache limits");
-  }
+  void Activate() { HipOk(hipSetDevice(options.device), "select device"); }
+  void Await() { HipOk(hipStreamSynchronize(stream), "device work"); }
 
-  void Activate() { Hip(hipSetDevice(options.device)); }
-  void Finish() {
-    Hip(hipEventRecord(done.value, stream.value));
-    Hip(hipEventSynchronize(done.value));
-  }
-  Table& Get(TableId id) {
+  SlotTable& Table(TableId id) {
     auto it = tables.find(id);
-    Require(it != tables.end(), "unknown HIP cache table");
+    Expect(it != tables.end(), "table is not defined on this HIP agent");
     return *it->second;
   }
-  Entry& Find(const LocatedRow& loc) {
-    auto& t = Get(loc.row.table);
+
+  // The residency of a located row, which must be this agent's current copy.
+  Resident& Locate(const LocatedRow& loc) {
+    SlotTable& t = Table(loc.row.table);
     auto it = t.rows.find(loc.row.key);
-    Require(it != t.rows.end() && loc.agent == options.agent &&
-                it->second.location.generation == loc.generation &&
-                it->second.location.slot == loc.slot && it->second.location.home == loc.home,
-            "HIP cache generation mismatch", Error::Code::stale_generation);
+    const bool current = it != t.rows.end() && loc.agent == options.agent &&
+                         it->second.where.generation == loc.generation && it->second.where.slot == loc.slot &&
+                         it->second.where.home == loc.home;
+    Expect(current, "row is not resident at this generation on this HIP agent", Code::stale_generation);
     return it->second;
   }
-  void Limit(std::uint64_t bytes) const {
-    Require(bytes <= options.transfer_bytes, "HIP staging budget exceeded", Error::Code::capacity_exceeded);
-  }
-  void CopyIn(void* device, const void* host, std::uint64_t bytes) {
-    if (bytes) Hip(hipMemcpyAsync(device, host, bytes, hipMemcpyHostToDevice, stream.value));
+
+  // Status flags of one request: word 0 collects the resolution and index
+  // results; the push and update workspaces hold their own.
+  std::uint32_t* Flag() { return flags.Get<std::uint32_t>(); }
+  void ClearFlag() { AbiOk(eps_hip_fill_u32(Flag(), 0, 1, stream)); }
+  std::uint32_t ReadFlag(const std::uint32_t* device_word) {
+    HipOk(hipMemcpyAsync(flags_host.Get(), device_word, 4, hipMemcpyDeviceToHost, stream), "status copy");
+    Await();
+    return *flags_host.Get<std::uint32_t>();
   }
 
-  // Occurrence slots + bag offsets into the index staging, transferred unique
-  // vectors into the transient buffer (src/cuda/cache_backend.cu:251-308).
-  std::pair<std::vector<GatherPart>, std::uint64_t> PrepareGather(
-      const std::vector<AgentWork>& work, const std::vector<FeatureInput>& layouts) {
-    std::vector<GatherPart> parts;
-    parts.reserve(work.size());
-    std::uint64_t indices = 0, values = 0, transferred = 0;
-    auto* index = host_indices.As<std::uint64_t>();
-    std::vector<std::uint64_t> slot_of;
-    for (const auto& task : work) {
-      auto it = std::find_if(layouts.begin(), layouts.end(),
-                             [&](const FeatureInput& f) { return f.feature == task.feature; });
-      Require(it != layouts.end() && task.agent == options.agent &&
-                  (task.route == AccessRoute::resident_gpu ||
-                   task.route == AccessRoute::transfer_unique),
-              "invalid HIP gather work");
-      const FeatureInput& f = *it;
-      Table& table = Get(f.table);
-      const std::uint64_t dim = table.definition.dimension;
-      const bool transfer = task.route == AccessRoute::transfer_unique;
-      Require(transfer ? task.transferred_weights.size() == task.rows.size() * dim
-                       : task.transferred_weights.empty(),
-              "invalid HIP transferred weights");
-      const std::uint64_t transfer_offset = transferred;
-      if (transfer) {
-        Limit((transferred + task.transferred_weights.size()) * 4);
-        for (float value : task.transferred_weights)
-          Require(std::isfinite(value), "non-finite transferred weight");
-        std::copy(task.transferred_weights.begin(), task.transferred_weights.end(),
-                  host_values.As<float>() + transferred);
-        transferred += task.transferred_weights.size();
-      }
-      Require(task.occurrence_to_unique.size() == f.keys.size() && !f.offsets.empty() &&
-                  f.offsets.front() == 0 && f.offsets.back() == f.keys.size() &&
-                  std::is_sorted(f.offsets.begin(), f.offsets.end()),
-              "invalid HIP gather layout");
-      Limit((indices + f.keys.size() + f.offsets.size()) * 8);
-      const std::uint64_t slot_offset = indices;
-      constexpr std::uint64_t kUnresolved = std::numeric_limits<std::uint64_t>::max() - 1;
-      slot_of.assign(task.rows.size(), kUnresolved);
-      for (std::size_t i = 0; i < f.keys.size(); ++i) {
-        const std::uint64_t unique = task.occurrence_to_unique[i];
-        if (unique == UINT64_MAX) {
-          index[indices++] = UINT64_MAX;
-          continue;
-        }
-        Require(unique < task.rows.size() && task.rows[unique].row == RowKey{f.table, f.keys[i]},
-                "invalid HIP occurrence map");
-        if (slot_of[unique] == kUnresolved) {
-          if (transfer) {
-            Require(task.rows[unique].placement == Placement::cpu, "transferred row is not CPU-owned");
-            slot_of[unique] = unique;
-          } else {
-            slot_of[unique] = Find(task.rows[unique]).location.slot;
-          }
-        }
-        index[indices++] = slot_of[unique];
-      }
-      const std::uint64_t offsets_offset = indices;
-      std::copy(f.offsets.begin(), f.offsets.end(), index + indices);
-      indices += f.offsets.size();
-      const std::uint64_t rows = f.pooling == Pooling::sequence ? f.keys.size() : f.offsets.size() - 1;
-      Limit((values + rows * dim) * 4);
-      parts.push_back({f.feature, &table, f.pooling, slot_offset, offsets_offset, values, rows,
-                       transfer ? device_transient.As<float>() + transfer_offset : table.state.As<float>(),
-                       transfer ? dim : dim * 3, transfer ? task.rows.size() : options.rows_per_table});
-      values += rows * dim;
+  // Failure bits of an update -> the reference's error for the same case:
+  // non-finite inputs and overflow are request errors (invalid_argument,
+  // src/update/lazy_adam.cpp:7-23, src/access/batch_access.cpp:23-95); a bad
+  // slot or a stalled hand-over is this agent's own failure.
+  static void UpdateVerdict(std::uint32_t status) {
+    if (!(status & kFailureBits)) return;
+    if (status & (EPS_HIP_STATUS_STALLED | EPS_HIP_STATUS_BAD_INDEX))
+      Raise(Code::run_failed, "HIP update failed on the device");
+    if (status & EPS_HIP_STATUS_NONFINITE_GRAD) Raise(Code::invalid_argument, "non-finite gradient");
+    if (status & EPS_HIP_STATUS_BAD_SCALE) Raise(Code::invalid_argument, "invalid gradient scale");
+    Raise(Code::invalid_argument, "optimizer state would overflow");
+  }
+
+  eps_hip_optimizer Optimizer(const SlotTable& t, float lr, float b1p, float b2p) const {
+    const OptimizerConfig& o = t.definition.optimizer;
+    eps_hip_optimizer x{};
+    x.learning_rate = lr;
+    x.beta1 = o.beta1;
+    x.beta2 = o.beta2;
+    x.epsilon = o.epsilon;
+    x.beta1_power = b1p;
+    x.beta2_power = b2p;
+    x.bounded = o.weight_bounds ? 1 : 0;
+    x.weight_min = o.weight_bounds ? o.weight_bounds->minimum : 0.f;
+    x.weight_max = o.weight_bounds ? o.weight_bounds->maximum : 0.f;
+    return x;
+  }
+
+  static void CheckContext(const UpdateContext& c) {
+    // src/cuda/cache_backend.cu:321-325.
+    Expect(std::isfinite(c.learning_rate) && c.learning_rate > 0 && c.beta1_power >= 0 && c.beta1_power < 1 &&
+               c.beta2_power >= 0 && c.beta2_power < 1,
+           "invalid update context");
+  }
+
+  // Rows of one update: in the context's table, distinct, held here for the
+  // context's shard, counters not saturated.  Returns their residencies.
+  std::vector<Resident*> UpdateRows(const UpdateContext& c, SlotTable& t, const std::vector<RowKey>& rows) {
+    std::vector<Resident*> out;
+    out.reserve(rows.size());
+    std::unordered_set<Key> seen;
+    for (const RowKey& r : rows) {
+      auto it = t.rows.find(r.key);
+      Expect(r.table == c.table && seen.insert(r.key).second && it != t.rows.end() &&
+                 it->second.where.home == c.shard && it->second.updates != UINT64_MAX,
+             "update row is not a distinct row this agent holds for the shard");
+      out.push_back(&it->second);
     }
-    CopyIn(device_indices.pointer, host_indices.pointer, indices * 8);
-    CopyIn(device_transient.pointer, host_values.pointer, transferred * 4);
-    return {std::move(parts), values};
+    return out;
   }
 
-  // Unnormalised pooled sums (the mean divide happens once, at assembly or in
-  // the client), all parts of the call in launches of up to 16 features.
-  void LaunchGather(const std::vector<GatherPart>& parts, float* output) {
-    auto* status = gather_status.As<uint32_t>();
-    Abi(eps_hip_fill_u32(status, 0, 1, stream.value));
+  // ---- request resolution shared by gathers and pushes ----
+  struct Resolved {
+    const AgentWork* work;
+    const FeatureInput* layout;
+    SlotTable* table;
+    bool carried;            // transfer_unique: rows travel with the request
+    std::uint64_t rows;      // output rows (bags, or occurrences for sequence)
+    std::uint64_t occurrences;
+    std::uint64_t* slots;    // device: per occurrence slot (or unique index when carried), kHole elsewhere
+    std::uint64_t* offsets;  // device: bags + 1
+    std::uint64_t* lengths;  // device: bags
+    const float* carried_rows;  // device: unique rows x dim (carried only)
+    std::vector<const Resident*> unique;  // resident unique rows
+  };
+
+  std::vector<Resolved> ResolveWork(const std::vector<AgentWork>& work, const std::vector<FeatureInput>& layouts,
+                                    bool allow_carried) {
+    std::unordered_map<std::uint32_t, const FeatureInput*> by_feature;
+    for (const auto& f : layouts) by_feature.emplace(f.feature, &f);
+    std::unordered_set<std::uint32_t> served;
+    std::vector<Resolved> out;
+    out.reserve(work.size());
+    struct Staged {
+      Transfer::Piece<std::uint64_t> keys, occ, unique_keys;
+    };
+    std::vector<Staged> staged;
+    staged.reserve(work.size());
+    transfer.Reset();
+    for (const AgentWork& w : work) {
+      auto f = by_feature.find(w.feature);
+      const bool carried = w.route == AccessRoute::transfer_unique;
+      Expect(f != by_feature.end() && served.insert(w.feature).second && w.agent == options.agent &&
+                 (w.route == AccessRoute::resident_gpu || (allow_carried && carried)),
+             "invalid HIP agent work");
+      const FeatureInput& L = *f->second;
+      SlotTable& t = Table(L.table);
+      const std::uint32_t dim = t.dim();
+      const bool seq = L.pooling == Pooling::sequence;
+      // Mean pooling needs every bag's original length (its gradient scale).
+      bool layout_ok = w.occurrence_to_unique.size() == L.keys.size() && !L.offsets.empty() &&
+                       L.offsets.front() == 0 && L.offsets.back() == L.keys.size() &&
+                       std::is_sorted(L.offsets.begin(), L.offsets.end()) &&
+                       (L.pooling != Pooling::mean || L.valid_lengths.size() + 1 == L.offsets.size());
+      Expect(layout_ok, "invalid HIP lookup layout");
+      Resolved r{&w, &L, &t, carried, seq ? L.keys.size() : L.offsets.size() - 1, L.keys.size(),
+                 nullptr, nullptr, nullptr, nullptr, {}};
+      if (carried) {
+        Expect(w.transferred_weights.size() == w.rows.size() * std::uint64_t(dim),
+               "transferred weights do not match the work rows");
+        Expect(Finite(w.transferred_weights), "non-finite transferred weight");
+        for (const LocatedRow& loc : w.rows)
+          Expect(loc.placement == Placement::cpu && loc.row.table == L.table, "transferred row is not CPU-owned");
+      } else {
+        Expect(w.transferred_weights.empty(), "resident work carries weights");
+        r.unique.reserve(w.rows.size());
+        for (const LocatedRow& loc : w.rows) {
+          Expect(loc.row.table == L.table, "work row belongs to another table");
+          r.unique.push_back(&Locate(loc));
+        }
+      }
+      Staged s{transfer.Copy(L.keys), transfer.Copy(w.occurrence_to_unique), transfer.Take<std::uint64_t>(w.rows.size())};
+      for (std::size_t u = 0; u < w.rows.size(); ++u) s.unique_keys.host[u] = w.rows[u].row.key;
+      auto offsets = transfer.Copy(L.offsets);
+      auto lengths = transfer.Copy(L.valid_lengths);
+      r.offsets = offsets.device;
+      r.lengths = L.valid_lengths.empty() ? nullptr : lengths.device;
+      if (carried) r.carried_rows = transfer.Copy(w.transferred_weights).device;
+      staged.push_back(s);
+      out.push_back(std::move(r));
+    }
+    transfer.Upload(stream);
+    for (auto& r : out) r.slots = transfer.Take<std::uint64_t>(r.occurrences).device;
+    transfer.Skip();
+    ClearFlag();
+    for (std::size_t i = 0; i < out.size(); ++i) {
+      Resolved& r = out[i];
+      const Staged& s = staged[i];
+      AbiOk(eps_hip_resolve(r.carried ? nullptr : r.table->index.Get(), r.table->index_capacity, s.keys.device,
+                            s.occ.device, s.unique_keys.device, s.unique_keys.count, r.occurrences, r.slots, Flag(),
+                            stream));
+    }
+    return out;
+  }
+
+  // Pooled gather of resolved features into `output` (dim-wide rows, feature
+  // after feature at the given float offsets).
+  void Gather(const std::vector<Resolved>& parts, float* output, const std::vector<std::uint64_t>& at) {
     std::vector<eps_hip_gather_part> abi;
     abi.reserve(parts.size());
-    for (const auto& p : parts) {
-      if (!p.rows) continue;
+    for (std::size_t i = 0; i < parts.size(); ++i) {
+      const Resolved& r = parts[i];
+      const std::uint32_t dim = r.table->dim();
       eps_hip_gather_part g{};
-      g.source = p.source;
-      g.indices = device_indices.As<std::uint64_t>() + p.slot_offset;
-      g.offsets = device_indices.As<std::uint64_t>() + p.offsets_offset;
-      g.output = output + p.output_offset;
-      g.stride = p.stride;
-      g.rows = p.rows;
-      g.source_rows = p.source_rows;
-      g.dim = p.table->definition.dimension;
-      g.pooling = PoolingCode(p.pooling);
+      g.source = r.carried ? r.carried_rows : r.table->abi.state;
+      g.indices = r.occurrences ? r.slots : nullptr;
+      g.offsets = r.layout->pooling == Pooling::sequence ? nullptr : r.offsets;
+      g.output = output + at[i];
+      g.stride = r.carried ? dim : 3ull * dim;
+      g.rows = r.rows;
+      g.source_rows = r.carried ? r.work->rows.size() : options.rows_per_table;
+      g.dim = dim;
+      g.pooling = r.layout->pooling == Pooling::sum ? EPS_HIP_POOL_SUM
+                  : r.layout->pooling == Pooling::mean ? EPS_HIP_POOL_MEAN
+                                                       : EPS_HIP_POOL_SEQUENCE;
       abi.push_back(g);
     }
-    for (std::size_t i = 0; i < abi.size(); i += EPS_HIP_MAX_GATHER_PARTS) {
-      const auto n = std::min<std::size_t>(EPS_HIP_MAX_GATHER_PARTS, abi.size() - i);
-      Abi(eps_hip_gather(abi.data() + i, uint32_t(n), status, stream.value));
+    for (std::size_t b = 0; b < abi.size(); b += EPS_HIP_MAX_GATHER_PARTS) {
+      const auto n = std::uint32_t(std::min<std::size_t>(EPS_HIP_MAX_GATHER_PARTS, abi.size() - b));
+      AbiOk(eps_hip_gather(abi.data() + b, n, Flag(), stream));
     }
-  }
-  void CheckGatherStatus() {
-    uint32_t status = 0;
-    Hip(hipMemcpy(&status, gather_status.pointer, 4, hipMemcpyDeviceToHost));
-    Require(status == 0, "HIP gather met an out-of-range slot", Error::Code::run_failed);
   }
 
-  // src/cuda/cache_backend.cu:321-333.
-  Table& CheckContext(const UpdateContext& c) {
-    Table& t = Get(c.table);
-    Require(std::isfinite(c.learning_rate) && c.learning_rate > 0 && c.beta1_power >= 0 &&
-                c.beta1_power < 1 && c.beta2_power >= 0 && c.beta2_power < 1,
-            "invalid HIP update context");
-    return t;
+  void CheckResolution() {
+    Expect(!(ReadFlag(Flag()) & EPS_HIP_STATUS_BAD_INDEX), "occurrence map does not match the lookup");
   }
-  static void CheckOwner(const UpdateContext& c, const Entry& e) {
-    Require(e.location.home == c.shard && e.updates != UINT64_MAX, "invalid HIP gradient owner/counter");
+
+  // Grows the push workspace to `occurrences`; a fresh one is zero-filled.
+  void ReservePush(std::uint64_t occurrences) {
+    const std::uint64_t need = eps_hip_push_workspace_bytes(occurrences);
+    if (need <= push_ws.bytes()) return;
+    Await();
+    push_ws.Acquire(options.device, need, false);
+    AbiOk(eps_hip_fill_u32(push_ws.Get<std::uint32_t>(), 0, need / 4, stream));
   }
-  Table& ValidateUpdate(const UpdateContext& c, const std::vector<RowKey>& rows) {
-    Table& t = CheckContext(c);
-    Limit(rows.size() * std::uint64_t(t.definition.dimension) * 4);
-    std::set<Key> unique;
-    for (const auto& row : rows) {
-      auto it = t.rows.find(row.key);
-      Require(row.table == c.table && unique.insert(row.key).second && it != t.rows.end(),
-              "invalid HIP gradient owner/counter");
-      CheckOwner(c, it->second);
+
+  // Admits rows: allocates their slots (all or none), scatters their packed
+  // state, indexes their keys.  `pack(i, dst)` writes row i's [w | m | v].
+  // Rows stream through the transfer area in pieces; the residency is
+  // committed only after every piece landed, so a failure leaves no trace.
+  template <typename Pack>
+  std::vector<LocatedRow> Admit(const MigrationPlan& plan, const std::vector<std::uint64_t>& updates, Pack pack) {
+    std::map<TableId, std::vector<std::size_t>> by_table;
+    for (std::size_t i = 0; i < plan.rows.size(); ++i) by_table[plan.rows[i].row.table].push_back(i);
+    for (const auto& [id, members] : by_table) {
+      const SlotTable& t = Table(id);
+      Expect(plan.reserve_slots <= t.free_slots.size() && members.size() <= t.free_slots.size() - plan.reserve_slots,
+             "HIP cache slots or slot reserve exhausted", Code::capacity_exceeded);
+      const std::uint64_t per_row = 12ull * t.dim() + 16;
+      Expect(transfer.capacity() >= 3 * 256 + per_row, "admitted row exceeds the transfer staging",
+             Code::capacity_exceeded);
     }
-    return t;
+    std::vector<LocatedRow> result(plan.rows.size());
+    std::vector<std::pair<SlotTable*, std::uint64_t>> taken;
+    for (const auto& [id, members] : by_table) {
+      SlotTable& t = Table(id);
+      for (std::size_t i : members) {
+        const std::uint64_t slot = t.TakeSlot();
+        taken.emplace_back(&t, slot);
+        LocatedRow loc = plan.rows[i];
+        loc.slot = slot;
+        loc.agent = options.agent;
+        loc.placement = Placement::gpu;
+        result[i] = loc;
+      }
+    }
+    // Keys indexed so far, per table (removed again if the admission fails).
+    std::vector<std::pair<SlotTable*, std::vector<Key>>> indexed;
+    try {
+      ClearFlag();
+      for (const auto& [id, members] : by_table) {
+        SlotTable& t = Table(id);
+        const std::uint64_t width = 3ull * t.dim();
+        const std::uint64_t piece = (transfer.capacity() - 3 * 256) / (width * 4 + 16);
+        indexed.emplace_back(&t, std::vector<Key>());
+        for (std::size_t b = 0; b < members.size(); b += piece) {
+          const std::size_t n = std::min<std::size_t>(piece, members.size() - b);
+          Await();  // the previous piece's upload has left the host staging
+          transfer.Reset();
+          auto rows = transfer.Take<float>(n * width);
+          auto slots = transfer.Take<std::uint64_t>(n);
+          auto keys = transfer.Take<std::uint64_t>(n);
+          for (std::size_t j = 0; j < n; ++j) {
+            const std::size_t i = members[b + j];
+            pack(i, rows.host + j * width);
+            slots.host[j] = result[i].slot;
+            keys.host[j] = result[i].row.key;
+          }
+          transfer.Upload(stream);
+          AbiOk(eps_hip_scatter_rows(&t.abi, slots.device, rows.device, n, bounds.Get(), stream));
+          indexed.back().second.insert(indexed.back().second.end(), keys.host, keys.host + n);
+          AbiOk(eps_hip_index_insert(t.index.Get(), t.index_capacity, keys.device, slots.device, n, Flag(), stream));
+        }
+      }
+      Expect(!(ReadFlag(Flag()) & EPS_HIP_STATUS_BAD_INDEX), "HIP key index is full", Code::run_failed);
+    } catch (...) {
+      // Nothing of the admission stays: its keys leave the index (those that
+      // never made it in are simply not found) and its slots go back on top
+      // of their stacks in the order they were taken.
+      (void)hipStreamSynchronize(stream);
+      for (auto& [t, keys] : indexed) {
+        for (std::size_t b = 0; b < keys.size(); b += transfer.capacity() / 8) {
+          const std::size_t n = std::min<std::size_t>(transfer.capacity() / 8, keys.size() - b);
+          transfer.Reset();
+          auto piece = transfer.Take<std::uint64_t>(n);
+          std::memcpy(piece.host, keys.data() + b, n * 8);
+          transfer.Upload(stream);
+          (void)eps_hip_index_remove(t->index.Get(), t->index_capacity, piece.device, n, nullptr, stream);
+          (void)hipStreamSynchronize(stream);
+        }
+      }
+      for (auto it = taken.rbegin(); it != taken.rend(); ++it) it->first->free_slots.push_back(it->second);
+      throw;
+    }
+    for (std::size_t i = 0; i < result.size(); ++i)
+      Table(result[i].row.table).rows.emplace(result[i].row.key, Resident{result[i], updates[i]});
+    return result;
   }
-  eps_hip_optimizer Optimizer(const Table& t, const UpdateContext& c) const {
-    const auto& o = t.definition.optimizer;
-    eps_hip_optimizer opt{};
-    opt.learning_rate = c.learning_rate;
-    opt.beta1 = o.beta1;
-    opt.beta2 = o.beta2;
-    opt.epsilon = o.epsilon;
-    opt.beta1_power = c.beta1_power;
-    opt.beta2_power = c.beta2_power;
-    opt.bounded = o.weight_bounds ? 1 : 0;
-    opt.weight_min = o.weight_bounds ? o.weight_bounds->minimum : 0.f;
-    opt.weight_max = o.weight_bounds ? o.weight_bounds->maximum : 0.f;
-    return opt;
-  }
-  // All-or-nothing: the device status says whether anything was written.
-  void CheckStatus(void* ws) {
-    uint32_t status = 0;
-    Abi(eps_hip_read_status(ws, &status, stream.value));
-    Require((status & EPS_HIP_STATUS_NONFINITE_GRAD) == 0, "non-finite gradient");
-    Require((status & EPS_HIP_STATUS_REDUCE_OVERFLOW) == 0, "gradient reduction overflow");
-    Require((status & (EPS_HIP_STATUS_BAD_INDEX | EPS_HIP_STATUS_ADAM_OVERFLOW)) == 0,
-            "HIP optimizer state would overflow");
-    Require((status & EPS_HIP_STATUS_STALLED) == 0, "HIP hot-row update did not complete",
-            Error::Code::run_failed);
-  }
-  void FinishUpdate(Table& t, const std::vector<RowKey>& rows) {
-    CheckStatus(workspace.pointer);
-    for (const auto& row : rows) ++t.rows.at(row.key).updates;
-  }
-  // The device push workspace grows to the largest call seen (the stream is
-  // idle between operations, so the old one can go).
-  void ReservePush(std::uint64_t bytes) {
-    if (bytes <= push_bytes) return;
-    push_workspace.Reset();
-    push_bytes = 0;
-    push_workspace.Allocate(bytes, options.device);
-    push_bytes = bytes;
+
+  // The checks every admission applies before anything moves (Load's, with
+  // the row shapes checked by the caller): this agent, a GPU destination,
+  // distinct rows not held here yet, tables defined.
+  void CheckAdmission(const MigrationPlan& plan) {
+    Expect(plan.agent == options.agent && plan.destination == Placement::gpu, "invalid HIP admission plan");
+    std::set<std::pair<TableId, Key>> seen;
+    for (const LocatedRow& loc : plan.rows) {
+      const SlotTable& t = Table(loc.row.table);
+      Expect(seen.emplace(loc.row.table, loc.row.key).second && !t.rows.count(loc.row.key),
+             "admitted row is duplicated or already held here");
+    }
   }
 
   HipCacheOptions options;
-  Stream stream;
-  Event done;
-  Memory host_values, host_indices, device_values, device_indices, device_transient, workspace,
-      bounds, gather_status, push_workspace;
-  std::uint64_t push_bytes = 0;
-  std::map<TableId, std::unique_ptr<Table>> tables;
-  std::uint64_t allocated_state = 0;
-  std::shared_ptr<OutputBudget> output_budget;
-  std::unique_ptr<hip_detail::Worker> worker;
+  hipStream_t stream = nullptr;
+  Transfer transfer;
+  Memory bounds, update_ws, push_ws, flags, flags_host;
+  std::shared_ptr<OutputLedger> ledger;
+  std::map<TableId, std::unique_ptr<SlotTable>> tables;
+  std::uint64_t state_charged = 0;
+  std::unique_ptr<hipbk::JobQueue> queue;
 };
 
+// ---------------------------------------------------------------------------
 HipCacheBackend::HipCacheBackend(HipCacheOptions options) : impl_(std::make_unique<Impl>(options)) {}
-HipCacheBackend::~HipCacheBackend() { impl_->worker->Stop(); }
+HipCacheBackend::~HipCacheBackend() { impl_->queue->Close(); }
 
 std::future<Result<Ack>> HipCacheBackend::Define(TableDefinition d) {
-  return impl_->worker->Submit<Ack>([this, d] {
-    if (d.optimizer.weight_bounds) {
-      const auto b = *d.optimizer.weight_bounds;
-      Require(std::isfinite(b.minimum) && std::isfinite(b.maximum) && b.minimum <= b.maximum,
-              "invalid optimizer weight bounds");
-    }
-    impl_->Activate();
-    Require(d.dimension > 0 && d.dimension <= 65536, "invalid HIP dimension");
-    if (auto it = impl_->tables.find(d.id); it != impl_->tables.end()) {
-      Require(it->second->definition == d, "HIP table configuration mismatch");
+  return impl_->queue->Post<Ack>([this, d] {
+    Impl& I = *impl_;
+    I.Activate();
+    // ValidateWeightBounds (src/common/optimizer_bounds.hpp:7-13).
+    if (const auto& b = d.optimizer.weight_bounds)
+      Expect(std::isfinite(b->minimum) && std::isfinite(b->maximum) && b->minimum <= b->maximum,
+             "invalid optimizer weight bounds");
+    Expect(d.dimension >= 1 && d.dimension <= 65536, "invalid HIP table dimension");
+    if (auto it = I.tables.find(d.id); it != I.tables.end()) {
+      Expect(it->second->definition == d, "HIP table is already defined differently");
       return Ack{};
     }
-    const std::uint64_t rows = impl_->options.rows_per_table;
-    const std::uint64_t bytes = rows * (std::uint64_t(d.dimension) * 12 + 8);
-    Require(bytes <= impl_->options.state_bytes - impl_->allocated_state,
-            "HIP table state budget exhausted", Error::Code::capacity_exceeded);
-    auto t = std::make_unique<Impl::Table>();
+    // The state budget counts 12 bytes per element and 8 per row, as the
+    // reference's (src/cuda/cache_backend.cu:372-374).
+    const std::uint64_t rows = I.options.rows_per_table;
+    const std::uint64_t charge = rows * (std::uint64_t(d.dimension) * 12 + 8);
+    Expect(charge <= I.options.state_bytes - std::min(I.state_charged, I.options.state_bytes),
+           "HIP table state budget exhausted", Code::capacity_exceeded);
+    auto t = std::make_unique<SlotTable>();
     t->definition = d;
-    t->state.Allocate(rows * std::uint64_t(d.dimension) * 12, impl_->options.device);
-    t->free.resize(rows);
-    std::iota(t->free.rbegin(), t->free.rend(), 0);
-    t->abi = eps_hip_table{t->state.As<float>(), rows, d.dimension, d.id};
-    impl_->tables.emplace(d.id, std::move(t));
-    impl_->allocated_state += bytes;
+    t->state.Acquire(I.options.device, rows * d.dimension * 12ull, false);
+    t->abi = eps_hip_table{t->state.Get<float>(), rows, d.dimension, d.id};
+    t->index_capacity = 64;
+    while (t->index_capacity < 2 * rows) t->index_capacity <<= 1;
+    t->index.Acquire(I.options.device, eps_hip_index_bytes(t->index_capacity), false);
+    AbiOk(eps_hip_index_clear(t->index.Get(), t->index_capacity, I.stream));
+    t->free_slots.reserve(rows);
+    for (std::uint64_t s = rows; s-- > 0;) t->free_slots.push_back(s);  // slot 0 first
+    I.Await();
+    I.tables.emplace(d.id, std::move(t));
+    I.state_charged += charge;
     return Ack{};
   });
 }
 
 std::future<Result<std::uint64_t>> HipCacheBackend::FreeSlots(TableId id) {
-  return impl_->worker->Submit<std::uint64_t>(
-      [this, id] { return std::uint64_t(impl_->Get(id).free.size()); });
+  return impl_->queue->Post<std::uint64_t>([this, id] { return std::uint64_t(impl_->Table(id).free_slots.size()); });
 }
 
-std::future<Result<std::vector<LocatedRow>>> HipCacheBackend::Load(MigrationPlan plan,
-                                                                   std::vector<RowState> states) {
-  return impl_->worker->Submit<std::vector<LocatedRow>>(
-      [this, plan = std::move(plan), states = std::move(states)] {
-        impl_->Activate();
-        Require(plan.agent == impl_->options.agent && plan.rows.size() == states.size() &&
-                    plan.destination == Placement::gpu,
-                "invalid HIP load plan");
-        std::map<TableId, std::vector<std::size_t>> groups;
-        std::set<std::pair<TableId, Key>> unique;
-        std::uint64_t bytes = 0;
-        for (std::size_t i = 0; i < states.size(); ++i) {
-          const auto& row = states[i];
-          auto& t = impl_->Get(row.row.table);
-          const auto dim = t.definition.dimension;
-          Require(row.row == plan.rows[i].row && !t.rows.count(row.row.key) &&
-                      unique.emplace(row.row.table, row.row.key).second,
-                  "duplicate/existing HIP load row");
-          Require(row.weights.size() == dim && row.first_moment.size() == dim &&
-                      row.second_moment.size() == dim,
-                  "HIP load shape mismatch");
-          for (const auto* v : {&row.weights, &row.first_moment, &row.second_moment})
-            for (float x : *v) Require(std::isfinite(x), "non-finite HIP load state");
-          for (float x : row.second_moment) Require(x >= 0, "negative HIP second moment");
-          bytes += std::uint64_t(dim) * 12;
-          groups[row.row.table].push_back(i);
-        }
-        impl_->Limit(bytes);
-        impl_->Limit(states.size() * 8);
-        for (const auto& [id, rows] : groups) {
-          auto& t = impl_->Get(id);
-          Require(plan.reserve_slots <= t.free.size() && rows.size() <= t.free.size() - plan.reserve_slots,
-                  "HIP cache slots or reserve exhausted", Error::Code::capacity_exceeded);
-          t.rows.reserve(t.rows.size() + rows.size());
-        }
-        std::vector<LocatedRow> result(states.size());
-        std::vector<std::pair<TableId, Key>> inserted;
-        inserted.reserve(states.size());
-        struct Group { Impl::Table* table; std::uint64_t values, slots, count; };
-        std::vector<Group> copies;
-        std::uint64_t value_offset = 0, slot_offset = 0;
-        try {
-          for (const auto& [id, rows] : groups) {
-            auto& t = impl_->Get(id);
-            const auto dim = t.definition.dimension;
-            copies.push_back({&t, value_offset, slot_offset, rows.size()});
-            for (auto i : rows) {
-              const std::uint64_t slot = t.free.back();
-              LocatedRow loc = plan.rows[i];
-              loc.slot = slot;
-              loc.agent = impl_->options.agent;
-              loc.placement = Placement::gpu;
-              t.rows.emplace(loc.row.key, Impl::Entry{loc, states[i].row_updates});
-              t.free.pop_back();
-              inserted.emplace_back(id, loc.row.key);
-              result[i] = loc;
-              impl_->host_indices.As<std::uint64_t>()[slot_offset++] = slot;
-              for (const auto* v : {&states[i].weights, &states[i].first_moment, &states[i].second_moment}) {
-                std::copy(v->begin(), v->end(), impl_->host_values.As<float>() + value_offset);
-                value_offset += dim;
-              }
-            }
-          }
-          impl_->CopyIn(impl_->device_values.pointer, impl_->host_values.pointer, bytes);
-          impl_->CopyIn(impl_->device_indices.pointer, impl_->host_indices.pointer, slot_offset * 8);
-          for (const auto& c : copies) {
-            if (!c.count) continue;
-            Abi(eps_hip_scatter_rows(&c.table->abi, impl_->device_indices.As<std::uint64_t>() + c.slots,
-                                     impl_->device_values.As<float>() + c.values, c.count,
-                                     impl_->bounds.pointer, impl_->stream.value));
-          }
-          impl_->Finish();
-          return result;
-        } catch (...) {
-          (void)hipStreamSynchronize(impl_->stream.value);
-          for (auto [id, key] : inserted) {
-            auto& t = impl_->Get(id);
-            t.free.push_back(t.rows.at(key).location.slot);
-            t.rows.erase(key);
-          }
-          throw;
-        }
-      });
+std::future<Result<std::vector<LocatedRow>>> HipCacheBackend::Load(MigrationPlan plan, std::vector<RowState> states) {
+  return impl_->queue->Post<std::vector<LocatedRow>>([this, plan = std::move(plan), states = std::move(states)] {
+    Impl& I = *impl_;
+    I.Activate();
+    Expect(plan.rows.size() == states.size(), "invalid HIP admission plan");
+    I.CheckAdmission(plan);
+    std::vector<std::uint64_t> updates(states.size());
+    for (std::size_t i = 0; i < states.size(); ++i) {
+      const RowState& s = states[i];
+      const std::uint32_t dim = I.Table(s.row.table).dim();
+      Expect(s.row == plan.rows[i].row, "admitted state does not match its plan row");
+      Expect(s.weights.size() == dim && s.first_moment.size() == dim && s.second_moment.size() == dim,
+             "admitted state has the wrong shape");
+      Expect(Finite(s.weights) && Finite(s.first_moment) && Finite(s.second_moment), "admitted state is not finite");
+      Expect(std::all_of(s.second_moment.begin(), s.second_moment.end(), [](float v) { return v >= 0.f; }),
+             "admitted second moment is negative");
+      updates[i] = s.row_updates;
+    }
+    return I.Admit(plan, updates, [&](std::size_t i, float* dst) {
+      const RowState& s = states[i];
+      const std::size_t dim = s.weights.size();
+      std::memcpy(dst, s.weights.data(), dim * 4);
+      std::memcpy(dst + dim, s.first_moment.data(), dim * 4);
+      std::memcpy(dst + 2 * dim, s.second_moment.data(), dim * 4);
+    });
+  });
 }
 
-std::future<Result<std::vector<TensorBlock>>> HipCacheBackend::GatherHost(
-    std::vector<AgentWork> work, std::vector<FeatureInput> layouts) {
-  return impl_->worker->Submit<std::vector<TensorBlock>>(
-      [this, work = std::move(work), layouts = std::move(layouts)] {
-        impl_->Activate();
-        auto [parts, values] = impl_->PrepareGather(work, layouts);
-        impl_->LaunchGather(parts, impl_->device_values.As<float>());
-        if (values)
-          Hip(hipMemcpyAsync(impl_->host_values.pointer, impl_->device_values.pointer, values * 4,
-                             hipMemcpyDeviceToHost, impl_->stream.value));
-        impl_->Finish();
-        impl_->CheckGatherStatus();
-        std::vector<TensorBlock> out;
-        out.reserve(parts.size());
-        for (const auto& p : parts) {
-          const std::uint64_t dim = p.table->definition.dimension;
-          const float* begin = impl_->host_values.As<float>() + p.output_offset;
-          out.push_back({p.feature, {p.rows, dim}, {begin, begin + p.rows * dim}});
-        }
-        return out;
-      });
+std::future<Result<std::vector<TensorBlock>>> HipCacheBackend::GatherHost(std::vector<AgentWork> work,
+                                                                          std::vector<FeatureInput> layouts) {
+  return impl_->queue->Post<std::vector<TensorBlock>>([this, work = std::move(work), layouts = std::move(layouts)] {
+    Impl& I = *impl_;
+    I.Activate();
+    auto parts = I.ResolveWork(work, layouts, true);
+    std::vector<std::uint64_t> at;
+    std::uint64_t floats = 0;
+    for (const auto& r : parts) {
+      at.push_back(floats);
+      floats += r.rows * r.table->dim();
+    }
+    auto out = I.transfer.Take<float>(floats);
+    I.transfer.Skip();
+    I.Gather(parts, out.device, at);
+    I.transfer.Download(out, I.stream);
+    I.CheckResolution();
+    std::vector<TensorBlock> blocks;
+    blocks.reserve(parts.size());
+    for (std::size_t i = 0; i < parts.size(); ++i) {
+      const std::uint64_t dim = parts[i].table->dim(), n = parts[i].rows * dim;
+      blocks.push_back({parts[i].layout->feature, {parts[i].rows, dim}, {out.host + at[i], out.host + at[i] + n}});
+    }
+    return blocks;
+  });
 }
 
-std::future<Result<std::vector<DeviceTensorBlock>>> HipCacheBackend::GatherDevice(
-    std::vector<AgentWork> work, std::vector<FeatureInput> layouts) {
-  return impl_->worker->Submit<std::vector<DeviceTensorBlock>>(
-      [this, work = std::move(work), layouts = std::move(layouts)] {
-        impl_->Activate();
-        auto [parts, values] = impl_->PrepareGather(work, layouts);
-        auto allocation = std::make_shared<Allocation>(impl_->options.device, values * 4, impl_->output_budget);
-        std::vector<DeviceTensorBlock> out;
-        out.reserve(parts.size());
-        for (const auto& p : parts) {
-          const std::uint64_t dim = p.table->definition.dimension;
-          out.push_back({p.feature, {p.rows, dim},
-                         std::make_shared<TensorView>(allocation, p.output_offset, p.rows * dim)});
-        }
-        impl_->LaunchGather(parts, allocation->memory.As<float>());
-        Hip(hipEventRecord(allocation->ready.value, impl_->stream.value));
-        impl_->Finish();  // index staging is reusable once the launch is done
-        impl_->CheckGatherStatus();
-        return out;
-      });
+std::future<Result<std::vector<DeviceTensorBlock>>> HipCacheBackend::GatherDevice(std::vector<AgentWork> work,
+                                                                                  std::vector<FeatureInput> layouts) {
+  return impl_->queue->Post<std::vector<DeviceTensorBlock>>([this, work = std::move(work),
+                                                             layouts = std::move(layouts)] {
+    Impl& I = *impl_;
+    I.Activate();
+    auto parts = I.ResolveWork(work, layouts, true);
+    std::vector<std::uint64_t> at;
+    std::uint64_t floats = 0;
+    for (const auto& r : parts) {
+      at.push_back(floats);
+      floats += r.rows * r.table->dim();
+    }
+    auto block = std::make_shared<OutputBlock>(I.ledger, I.options.device, floats * 4);
+    I.Gather(parts, block->data(), at);
+    HipOk(hipEventRecord(block->ready(), I.stream), "output ready event");
+    I.CheckResolution();  // also drains the staging's users
+    std::vector<DeviceTensorBlock> out;
+    out.reserve(parts.size());
+    for (std::size_t i = 0; i < parts.size(); ++i) {
+      const std::uint64_t dim = parts[i].table->dim();
+      out.push_back({parts[i].layout->feature, {parts[i].rows, dim},
+                     std::make_shared<OutputSlice>(block, at[i], parts[i].rows * dim)});
+    }
+    return out;
+  });
 }
 
 std::future<Result<Ack>> HipCacheBackend::ApplyHost(UpdateContext context, RowGradients g) {
-  return impl_->worker->Submit<Ack>([this, context, g = std::move(g)] {
-    impl_->Activate();
-    auto& t = impl_->ValidateUpdate(context, g.rows);
-    const std::uint64_t dim = t.definition.dimension;
-    Require(g.values.size() == g.rows.size() * dim, "invalid HIP gradient shape");
-    impl_->Limit(g.rows.size() * 8);
-    if (g.rows.empty()) return Ack{};
-    auto* slots = impl_->host_indices.As<std::uint64_t>();
-    for (std::size_t i = 0; i < g.rows.size(); ++i) slots[i] = t.rows.at(g.rows[i].key).location.slot;
-    std::copy(g.values.begin(), g.values.end(), impl_->host_values.As<float>());
-    impl_->CopyIn(impl_->device_values.pointer, impl_->host_values.pointer, g.values.size() * 4);
-    impl_->CopyIn(impl_->device_indices.pointer, slots, g.rows.size() * 8);
-    const eps_hip_optimizer opt = impl_->Optimizer(t, context);
-    Abi(eps_hip_adam_rows(&t.abi, &opt, impl_->device_indices.As<std::uint64_t>(),
-                          impl_->device_values.As<float>(), g.rows.size(), impl_->workspace.pointer,
-                          impl_->bounds.pointer, impl_->stream.value));
-    impl_->FinishUpdate(t, g.rows);
+  return impl_->queue->Post<Ack>([this, context, g = std::move(g)] {
+    Impl& I = *impl_;
+    I.Activate();
+    Impl::CheckContext(context);
+    SlotTable& t = I.Table(context.table);
+    auto rows = I.UpdateRows(context, t, g.rows);
+    Expect(g.values.size() == rows.size() * std::uint64_t(t.dim()), "gradient values do not match the rows");
+    if (rows.empty()) return Ack{};
+    I.transfer.Reset();
+    auto slots = I.transfer.Take<std::uint64_t>(rows.size());
+    for (std::size_t i = 0; i < rows.size(); ++i) slots.host[i] = rows[i]->where.slot;
+    auto values = I.transfer.Copy(g.values);
+    I.transfer.Upload(I.stream);
+    const eps_hip_optimizer o = I.Optimizer(t, context.learning_rate, context.beta1_power, context.beta2_power);
+    AbiOk(eps_hip_adam_rows(&t.abi, &o, slots.device, values.device, rows.size(), I.update_ws.Get(),
+                            I.bounds.Get(), I.stream));
+    Impl::UpdateVerdict(I.ReadFlag(eps_hip_status_word(I.update_ws.Get())));
+    for (Resident* r : rows) ++r->updates;
     return Ack{};
   });
 }
 
 std::future<Result<Ack>> HipCacheBackend::ApplyCompact(UpdateContext context, CompactGradients p) {
-  return impl_->worker->Submit<Ack>([this, context, p = std::move(p)] {
-    impl_->Activate();
-    hip_detail::ValidateCompact(p);
-    auto& t = impl_->ValidateUpdate(context, p.rows);
-    const std::uint64_t dim = t.definition.dimension;
-    Require(p.dimension == dim, "compact HIP table dimension mismatch");
-    const std::uint64_t slots_offset = p.row_offsets.size() + p.source_rows.size();
-    const std::uint64_t index_count = slots_offset + p.rows.size();
-    const std::uint64_t value_count = p.source_values.size() + p.scales.size();
-    impl_->Limit(index_count * 8);
-    impl_->Limit(value_count * 4);
-    if (p.rows.empty()) return Ack{};
-    auto* indices = impl_->host_indices.As<std::uint64_t>();
-    std::copy(p.row_offsets.begin(), p.row_offsets.end(), indices);
-    std::copy(p.source_rows.begin(), p.source_rows.end(), indices + p.row_offsets.size());
-    for (std::size_t i = 0; i < p.rows.size(); ++i)
-      indices[slots_offset + i] = t.rows.at(p.rows[i].key).location.slot;
-    auto* values = impl_->host_values.As<float>();
-    std::copy(p.source_values.begin(), p.source_values.end(), values);
-    std::copy(p.scales.begin(), p.scales.end(), values + p.source_values.size());
-    impl_->CopyIn(impl_->device_transient.pointer, values, value_count * 4);
-    impl_->CopyIn(impl_->device_indices.pointer, indices, index_count * 8);
-    const auto* dev_index = impl_->device_indices.As<std::uint64_t>();
-    const auto* dev_value = impl_->device_transient.As<float>();
-    const eps_hip_optimizer opt = impl_->Optimizer(t, context);
-    Abi(eps_hip_adam_compact(&t.abi, &opt, dev_index + slots_offset, p.rows.size(), dev_index,
-                             dev_index + p.row_offsets.size(), dev_value + p.source_values.size(),
-                             dev_value, p.source_values.size() / dim, p.source_rows.size(),
-                             impl_->workspace.pointer, impl_->bounds.pointer, impl_->stream.value));
-    impl_->FinishUpdate(t, p.rows);
+  return impl_->queue->Post<Ack>([this, context, p = std::move(p)] {
+    Impl& I = *impl_;
+    I.Activate();
+    hipbk::CheckPacket(p);
+    Impl::CheckContext(context);
+    SlotTable& t = I.Table(context.table);
+    auto rows = I.UpdateRows(context, t, p.rows);
+    Expect(p.dimension == t.dim(), "compact packet dimension differs from the table's");
+    if (rows.empty()) return Ack{};
+    I.transfer.Reset();
+    auto slots = I.transfer.Take<std::uint64_t>(rows.size());
+    for (std::size_t i = 0; i < rows.size(); ++i) slots.host[i] = rows[i]->where.slot;
+    auto offsets = I.transfer.Copy(p.row_offsets);
+    auto sources = I.transfer.Copy(p.source_rows);
+    auto scales = I.transfer.Copy(p.scales);
+    auto values = I.transfer.Copy(p.source_values);
+    I.transfer.Upload(I.stream);
+    const eps_hip_optimizer o = I.Optimizer(t, context.learning_rate, context.beta1_power, context.beta2_power);
+    AbiOk(eps_hip_adam_compact(&t.abi, &o, slots.device, rows.size(), offsets.device, sources.device, scales.device,
+                               values.device, p.source_values.size() / p.dimension, p.source_rows.size(),
+                               I.update_ws.Get(), I.bounds.Get(), I.stream));
+    Impl::UpdateVerdict(I.ReadFlag(eps_hip_status_word(I.update_ws.Get())));
+    for (Resident* r : rows) ++r->updates;
     return Ack{};
   });
 }
 
 std::future<Result<std::vector<RowState>>> HipCacheBackend::ReadBack(MigrationPlan plan) {
-  return impl_->worker->Submit<std::vector<RowState>>([this, plan = std::move(plan)] {
-    impl_->Activate();
-    std::map<TableId, std::vector<std::size_t>> groups;
-    std::uint64_t bytes = 0;
-    std::vector<RowState> out(plan.rows.size());
+  return impl_->queue->Post<std::vector<RowState>>([this, plan = std::move(plan)] {
+    Impl& I = *impl_;
+    I.Activate();
+    std::vector<const Resident*> held;
+    std::map<TableId, std::vector<std::size_t>> by_table;
     for (std::size_t i = 0; i < plan.rows.size(); ++i) {
-      const auto& loc = plan.rows[i];
-      auto& entry = impl_->Find(loc);
-      const std::uint64_t dim = impl_->Get(loc.row.table).definition.dimension;
-      out[i] = {loc.row, std::vector<float>(dim), std::vector<float>(dim), std::vector<float>(dim),
-                entry.updates};
-      groups[loc.row.table].push_back(i);
-      bytes += dim * 12;
+      held.push_back(&I.Locate(plan.rows[i]));
+      by_table[plan.rows[i].row.table].push_back(i);
     }
-    impl_->Limit(bytes);
-    impl_->Limit(plan.rows.size() * 8);
-    struct Part { Impl::Table* table; std::uint64_t values, slots, count; };
+    I.transfer.Reset();
+    struct Part {
+      SlotTable* t;
+      Transfer::Piece<std::uint64_t> slots;
+      const std::vector<std::size_t>* members;
+    };
     std::vector<Part> parts;
-    std::uint64_t values = 0, slots = 0;
-    for (const auto& [id, members] : groups) {
-      auto& t = impl_->Get(id);
-      parts.push_back({&t, values, slots, members.size()});
-      for (auto i : members) {
-        impl_->host_indices.As<std::uint64_t>()[slots++] = impl_->Find(plan.rows[i]).location.slot;
-        values += std::uint64_t(t.definition.dimension) * 3;
-      }
+    for (const auto& [id, members] : by_table) {
+      Part part{&I.Table(id), I.transfer.Take<std::uint64_t>(members.size()), &members};
+      for (std::size_t j = 0; j < members.size(); ++j) part.slots.host[j] = held[members[j]]->where.slot;
+      parts.push_back(part);
     }
-    impl_->CopyIn(impl_->device_indices.pointer, impl_->host_indices.pointer, slots * 8);
-    for (const auto& p : parts) {
-      if (!p.count) continue;
-      Abi(eps_hip_gather_rows(&p.table->abi, impl_->device_indices.As<std::uint64_t>() + p.slots,
-                              impl_->device_values.As<float>() + p.values, p.count, impl_->stream.value));
+    I.transfer.Upload(I.stream);
+    std::vector<Transfer::Piece<float>> packed;
+    for (const Part& part : parts) packed.push_back(I.transfer.Take<float>(part.slots.count * 3ull * part.t->dim()));
+    I.transfer.Skip();
+    for (std::size_t k = 0; k < parts.size(); ++k) {
+      AbiOk(eps_hip_gather_rows(&parts[k].t->abi, parts[k].slots.device, packed[k].device, parts[k].slots.count,
+                                I.stream));
+      I.transfer.Download(packed[k], I.stream);
     }
-    if (bytes)
-      Hip(hipMemcpyAsync(impl_->host_values.pointer, impl_->device_values.pointer, bytes,
-                         hipMemcpyDeviceToHost, impl_->stream.value));
-    impl_->Finish();
-    std::uint64_t offset = 0;
-    for (const auto& [id, members] : groups) {
-      const std::uint64_t dim = impl_->Get(id).definition.dimension;
-      for (auto i : members) {
-        for (auto* v : {&out[i].weights, &out[i].first_moment, &out[i].second_moment}) {
-          std::copy_n(impl_->host_values.As<float>() + offset, dim, v->begin());
-          offset += dim;
-        }
+    I.Await();
+    std::vector<RowState> out(plan.rows.size());
+    for (std::size_t k = 0; k < parts.size(); ++k) {
+      const std::size_t dim = parts[k].t->dim();
+      for (std::size_t j = 0; j < parts[k].members->size(); ++j) {
+        const std::size_t i = (*parts[k].members)[j];
+        const float* src = packed[k].host + j * 3 * dim;
+        out[i] = RowState{plan.rows[i].row, {src, src + dim}, {src + dim, src + 2 * dim}, {src + 2 * dim, src + 3 * dim},
+                          held[i]->updates};
       }
     }
     return out;
@@ -713,443 +840,379 @@ std::future<Result<std::vector<RowState>>> HipCacheBackend::ReadBack(MigrationPl
 }
 
 std::future<Result<Ack>> HipCacheBackend::CommitEviction(MigrationPlan plan) {
-  return impl_->worker->Submit<Ack>([this, plan = std::move(plan)] {
-    std::set<std::pair<TableId, Key>> unique;
-    for (const auto& loc : plan.rows) {
-      impl_->Find(loc);
-      Require(unique.emplace(loc.row.table, loc.row.key).second, "duplicate HIP eviction row");
+  return impl_->queue->Post<Ack>([this, plan = std::move(plan)] {
+    Impl& I = *impl_;
+    I.Activate();
+    std::set<std::pair<TableId, Key>> seen;
+    std::map<TableId, std::vector<Key>> by_table;
+    for (const LocatedRow& loc : plan.rows) {
+      I.Locate(loc);
+      Expect(seen.emplace(loc.row.table, loc.row.key).second, "evicted row is named twice");
+      by_table[loc.row.table].push_back(loc.row.key);
     }
-    for (const auto& loc : plan.rows) {
-      auto& t = impl_->Get(loc.row.table);
-      t.free.push_back(loc.slot);
+    I.transfer.Reset();
+    std::vector<std::pair<SlotTable*, Transfer::Piece<std::uint64_t>>> removals;
+    for (const auto& [id, keys] : by_table) removals.emplace_back(&I.Table(id), I.transfer.Copy(keys));
+    I.transfer.Upload(I.stream);
+    I.ClearFlag();
+    for (auto& [t, keys] : removals)
+      AbiOk(eps_hip_index_remove(t->index.Get(), t->index_capacity, keys.device, keys.count, I.Flag(), I.stream));
+    Expect(!(I.ReadFlag(I.Flag()) & EPS_HIP_STATUS_BAD_INDEX), "HIP key index lost a resident row", Code::run_failed);
+    for (const LocatedRow& loc : plan.rows) {
+      SlotTable& t = I.Table(loc.row.table);
+      t.free_slots.push_back(loc.slot);
       t.rows.erase(loc.row.key);
     }
     return Ack{};
   });
 }
 
-// Device feature assembly (src/cuda/cache_backend.cu:600-697): a zeroed output
-// per feature, host partial sums added (scattered to sequence positions when
-// projected), device contributions added after their producers' events, then
-// one mean divide by the original bag lengths.
-std::future<Result<std::vector<DeviceTensorBlock>>> HipCacheBackend::AssembleFeatures(
-    DeviceAssemblyRequest request) {
-  return impl_->worker->Submit<std::vector<DeviceTensorBlock>>([this, request = std::move(request)] {
-    impl_->Activate();
-    const auto& o = impl_->options;
-    Require(request.host.size() == request.layouts.size() && !request.host.empty(),
-            "invalid device assembly features");
-    struct Target {
-      std::uint64_t offset, rows, compact_rows;
-      std::uint32_t dim;
+std::future<Result<std::vector<DeviceTensorBlock>>> HipCacheBackend::AssembleFeatures(DeviceAssemblyRequest request) {
+  return impl_->queue->Post<std::vector<DeviceTensorBlock>>([this, request = std::move(request)] {
+    Impl& I = *impl_;
+    I.Activate();
+    const std::uint64_t cap = I.options.transfer_bytes;
+    Expect(!request.host.empty() && request.host.size() == request.layouts.size(), "invalid device assembly");
+    std::unordered_map<std::uint32_t, const SequenceProjection*> projection;
+    for (const auto& p : request.projections)
+      Expect(projection.emplace(p.feature, &p).second, "feature projected twice");
+    // One output per feature: its rows before and after projection, its
+    // offset in the shared allocation.
+    struct Out {
+      std::uint64_t at, rows, compact, dim;
       const SequenceProjection* projection;
     };
-    struct Source {
+    std::vector<Out> outs;
+    std::unordered_map<std::uint32_t, std::size_t> slot_of;
+    const std::uint64_t align = I.options.output_alignment / 4;
+    std::uint64_t floats = 0;
+    for (std::size_t i = 0; i < request.host.size(); ++i) {
+      const TensorBlock& h = request.host[i];
+      const FeatureInput& L = request.layouts[i];
+      Expect(h.feature == L.feature && h.shape.size() == 2 && h.shape[1] >= 1 && h.shape[1] <= UINT32_MAX &&
+                 slot_of.emplace(h.feature, i).second,
+             "device assembly host part does not match its layout");
+      const std::uint64_t dim = h.shape[1];
+      const std::uint64_t compact = L.pooling == Pooling::sequence ? L.keys.size() : L.valid_lengths.size();
+      Expect(h.shape[0] == compact && compact <= cap / (4 * dim) && h.values.size() == compact * dim,
+             "device assembly host part has the wrong shape");
+      const SequenceProjection* p = nullptr;
+      if (auto it = projection.find(h.feature); it != projection.end()) {
+        p = it->second;
+        bool ok = L.pooling == Pooling::sequence && p->positions.size() == compact;
+        for (std::size_t j = 0; ok && j < p->positions.size(); ++j)
+          ok = p->positions[j] < p->rows && (j == 0 || p->positions[j - 1] < p->positions[j]);
+        Expect(ok, "invalid sequence projection");
+      }
+      const std::uint64_t rows = p ? p->rows : compact;
+      Expect(rows <= cap / (4 * dim), "device assembly output exceeds the transfer limit", Code::capacity_exceeded);
+      floats = RoundUp(floats, align);
+      outs.push_back({floats, rows, compact, dim, p});
+      floats += rows * dim;
+    }
+    for (const auto& [feature, p] : projection) Expect(slot_of.count(feature), "projection of an unknown feature");
+    // Device contributions and where their rows land.
+    struct Add {
       const DeviceTensor* tensor;
-      std::size_t target;
+      std::size_t out;
       std::vector<std::uint64_t> positions;
     };
-    std::map<std::uint32_t, const SequenceProjection*> projections;
-    for (const auto& p : request.projections)
-      Require(projections.emplace(p.feature, &p).second, "duplicate device output projection");
-    std::vector<Target> targets;
-    std::map<std::uint32_t, std::size_t> indices;
-    std::uint64_t total = 0;
-    for (std::size_t i = 0; i < request.host.size(); ++i) {
-      const auto& host = request.host[i];
-      const auto& layout = request.layouts[i];
-      Require(layout.pooling == Pooling::sum || layout.pooling == Pooling::mean ||
-                  layout.pooling == Pooling::sequence,
-              "invalid device assembly pooling");
-      Require(host.feature == layout.feature && host.shape.size() == 2 && host.shape[1] > 0 &&
-                  host.shape[1] <= UINT32_MAX && indices.emplace(host.feature, i).second,
-              "invalid device assembly schema");
-      const std::uint64_t rows =
-          layout.pooling == Pooling::sequence ? layout.keys.size() : layout.valid_lengths.size();
-      Require(host.shape[0] == rows && rows <= o.transfer_bytes / (4 * host.shape[1]) &&
-                  host.values.size() == rows * host.shape[1],
-              "device assembly host shape mismatch");
-      const SequenceProjection* p = nullptr;
-      if (projections.count(host.feature)) {
-        p = projections.at(host.feature);
-        Require(layout.pooling == Pooling::sequence && p->positions.size() == rows,
-                "invalid sequence output projection");
-        for (std::size_t j = 0; j < p->positions.size(); ++j)
-          Require(p->positions[j] < p->rows && (!j || p->positions[j - 1] < p->positions[j]),
-                  "invalid output sequence position");
-        impl_->Limit(p->positions.size() * 8);
-      }
-      const std::uint64_t output_rows = p ? p->rows : rows;
-      const std::uint64_t alignment = o.output_alignment / 4;
-      total = (total + alignment - 1) / alignment * alignment;
-      Require(output_rows <= o.transfer_bytes / (4 * host.shape[1]), "device assembly output exceeds limit",
-              Error::Code::capacity_exceeded);
-      impl_->Limit((total + output_rows * host.shape[1]) * 4);
-      targets.push_back({total, output_rows, rows, std::uint32_t(host.shape[1]), p});
-      total += output_rows * host.shape[1];
-      if (layout.pooling == Pooling::mean) impl_->Limit(layout.valid_lengths.size() * 8);
-    }
-    for (const auto& [id, p] : projections)
-      Require(indices.count(id) > 0, "unknown device output projection");
-    std::vector<Source> sources;
-    sources.reserve(request.device.size());
-    for (const auto& contribution : request.device) {
-      const auto& block = contribution.block;
-      Require(indices.count(block.feature) && bool(block.tensor), "unknown/null device contribution");
-      const std::size_t ti = indices.at(block.feature);
-      const Target& target = targets[ti];
-      Require(block.shape.size() == 2 && block.shape[1] == target.dim &&
-                  block.shape[0] <= o.transfer_bytes / (4ULL * target.dim) &&
-                  block.tensor->elements() == block.shape[0] * target.dim &&
-                  block.tensor->device() == o.device,
-              "native contribution device/layout mismatch");
-      Source source{block.tensor.get(), ti, {}};
-      if (contribution.projected) {
-        Require(request.layouts[ti].pooling == Pooling::sequence &&
-                    contribution.positions.size() == block.shape[0],
-                "invalid projected device contribution");
-        source.positions.reserve(contribution.positions.size());
-        for (std::size_t j = 0; j < contribution.positions.size(); ++j) {
-          const std::uint64_t position = contribution.positions[j];
-          Require(position < target.compact_rows && (!j || contribution.positions[j - 1] < position),
-                  "invalid device contribution position");
-          source.positions.push_back(target.projection ? target.projection->positions[position] : position);
-        }
+    std::vector<Add> adds;
+    for (const DeviceContribution& c : request.device) {
+      auto it = slot_of.find(c.block.feature);
+      Expect(it != slot_of.end() && c.block.tensor, "device contribution of an unknown feature");
+      const Out& o = outs[it->second];
+      const DeviceTensorBlock& b = c.block;
+      Expect(b.shape.size() == 2 && b.shape[1] == o.dim && b.shape[0] <= cap / (4 * o.dim) &&
+                 b.tensor->elements() == b.shape[0] * o.dim && b.tensor->device() == I.options.device,
+             "device contribution layout or device mismatch");
+      Add a{b.tensor.get(), it->second, {}};
+      if (c.projected) {
+        bool ok = request.layouts[it->second].pooling == Pooling::sequence && c.positions.size() == b.shape[0];
+        for (std::size_t j = 0; ok && j < c.positions.size(); ++j)
+          ok = c.positions[j] < o.compact && (j == 0 || c.positions[j - 1] < c.positions[j]);
+        Expect(ok, "invalid projected device contribution");
+        for (std::uint64_t q : c.positions) a.positions.push_back(o.projection ? o.projection->positions[q] : q);
       } else {
-        Require(contribution.positions.empty() && block.shape[0] == target.compact_rows,
-                "device contribution row mismatch");
-        if (target.projection) source.positions = target.projection->positions;
+        Expect(c.positions.empty() && b.shape[0] == o.compact, "device contribution row count mismatch");
+        if (o.projection) a.positions = o.projection->positions;
       }
-      impl_->Limit(source.positions.size() * 8);
-      sources.push_back(std::move(source));
+      adds.push_back(std::move(a));
     }
-    auto allocation = std::make_shared<Allocation>(o.device, total * 4, impl_->output_budget);
-    std::vector<DeviceTensorBlock> output;
-    output.reserve(targets.size());
-    for (std::size_t i = 0; i < targets.size(); ++i) {
-      const Target& target = targets[i];
-      output.push_back({request.host[i].feature, {target.rows, target.dim},
-                        std::make_shared<TensorView>(allocation, target.offset, target.rows * target.dim)});
-    }
-    hipStream_t s = impl_->stream.value;
-    float* base = allocation->memory.As<float>();
+    auto block = std::make_shared<OutputBlock>(I.ledger, I.options.device, floats * 4);
+    float* base = block->data();
     try {
-      if (total) Abi(eps_hip_fill_u32(reinterpret_cast<uint32_t*>(base), 0, total, s));
-      for (std::size_t i = 0; i < targets.size(); ++i) {
-        const Target& target = targets[i];
-        const auto& host = request.host[i];
-        if (host.values.empty()) continue;
-        float* destination = base + target.offset;
-        if (!target.projection) {
-          Hip(hipMemcpyAsync(destination, host.values.data(), host.values.size() * 4,
-                             hipMemcpyHostToDevice, s));
-        } else {
-          Hip(hipMemcpyAsync(impl_->device_values.pointer, host.values.data(), host.values.size() * 4,
-                             hipMemcpyHostToDevice, s));
-          Hip(hipMemcpyAsync(impl_->device_indices.pointer, target.projection->positions.data(),
-                             target.projection->positions.size() * 8, hipMemcpyHostToDevice, s));
-          Abi(eps_hip_add_contribution(destination, impl_->device_values.As<float>(),
-                                       impl_->device_indices.As<std::uint64_t>(), host.values.size(),
-                                       target.dim, s));
-        }
+      // Stage what the kernels read: projected host parts and their
+      // positions, contribution positions, mean lengths.
+      I.transfer.Reset();
+      struct HostAdd {
+        Transfer::Piece<float> values;
+        Transfer::Piece<std::uint64_t> positions;
+      };
+      std::vector<std::optional<HostAdd>> host_adds(outs.size());
+      std::vector<Transfer::Piece<std::uint64_t>> add_positions, lengths(outs.size());
+      for (std::size_t i = 0; i < outs.size(); ++i)
+        if (outs[i].projection && !request.host[i].values.empty())
+          host_adds[i] = HostAdd{I.transfer.Copy(request.host[i].values), I.transfer.Copy(outs[i].projection->positions)};
+      for (const Add& a : adds) add_positions.push_back(I.transfer.Copy(a.positions));
+      for (std::size_t i = 0; i < outs.size(); ++i)
+        if (request.layouts[i].pooling == Pooling::mean) lengths[i] = I.transfer.Copy(request.layouts[i].valid_lengths);
+      I.transfer.Upload(I.stream);
+      if (floats) AbiOk(eps_hip_fill_u32(reinterpret_cast<std::uint32_t*>(base), 0, floats, I.stream));
+      // Host parts: a plain part is copied over the zeroed output, a
+      // projected one is added at its positions (src/cuda/cache_backend.cu:664-676).
+      for (std::size_t i = 0; i < outs.size(); ++i) {
+        const auto& values = request.host[i].values;
+        if (values.empty()) continue;
+        float* dst = base + outs[i].at;
+        if (host_adds[i])
+          AbiOk(eps_hip_add_contribution(dst, host_adds[i]->values.device, host_adds[i]->positions.device,
+                                         values.size(), std::uint32_t(outs[i].dim), I.stream));
+        else
+          HipOk(hipMemcpyAsync(dst, values.data(), values.size() * 4, hipMemcpyHostToDevice, I.stream), "host part");
       }
-      for (const auto& source : sources) {
-        const std::uint64_t n = source.tensor->elements();
+      // Device contributions, after their producers' work.
+      for (std::size_t k = 0; k < adds.size(); ++k) {
+        const Add& a = adds[k];
+        const std::uint64_t n = a.tensor->elements();
         if (!n) continue;
-        const Target& target = targets[source.target];
-        source.tensor->WaitOnStream(s);
-        const std::uint64_t* positions = nullptr;
-        if (!source.positions.empty()) {
-          Hip(hipMemcpyAsync(impl_->device_indices.pointer, source.positions.data(),
-                             source.positions.size() * 8, hipMemcpyHostToDevice, s));
-          positions = impl_->device_indices.As<std::uint64_t>();
-        }
-        Abi(eps_hip_add_contribution(base + target.offset, static_cast<const float*>(source.tensor->data()),
-                                     positions, n, target.dim, s));
+        a.tensor->WaitOnStream(I.stream);
+        AbiOk(eps_hip_add_contribution(base + outs[a.out].at, static_cast<const float*>(a.tensor->data()),
+                                       a.positions.empty() ? nullptr : add_positions[k].device, n,
+                                       std::uint32_t(outs[a.out].dim), I.stream));
       }
-      for (std::size_t i = 0; i < targets.size(); ++i) {
-        if (request.layouts[i].pooling != Pooling::mean) continue;
-        const Target& target = targets[i];
-        if (!target.rows) continue;
-        const auto& lengths = request.layouts[i].valid_lengths;
-        Hip(hipMemcpyAsync(impl_->device_indices.pointer, lengths.data(), lengths.size() * 8,
-                           hipMemcpyHostToDevice, s));
-        Abi(eps_hip_normalize_mean(base + target.offset, impl_->device_indices.As<std::uint64_t>(),
-                                   target.rows, target.dim, s));
-      }
-      Hip(hipEventRecord(allocation->ready.value, s));
-      impl_->Finish();
+      // Means divide once by the original bag lengths.
+      for (std::size_t i = 0; i < outs.size(); ++i)
+        if (request.layouts[i].pooling == Pooling::mean && outs[i].rows)
+          AbiOk(eps_hip_normalize_mean(base + outs[i].at, lengths[i].device, outs[i].rows, std::uint32_t(outs[i].dim),
+                                       I.stream));
+      HipOk(hipEventRecord(block->ready(), I.stream), "output ready event");
+      I.Await();
     } catch (...) {
-      (void)hipStreamSynchronize(s);
+      (void)hipStreamSynchronize(I.stream);
       throw;
     }
-    return output;
+    std::vector<DeviceTensorBlock> result;
+    result.reserve(outs.size());
+    for (std::size_t i = 0; i < outs.size(); ++i)
+      result.push_back({request.host[i].feature, {outs[i].rows, outs[i].dim},
+                        std::make_shared<OutputSlice>(block, outs[i].at, outs[i].rows * outs[i].dim)});
+    return result;
   });
 }
 
-// Device-resident push.  Host work is the slot translation of the lookup's
-// occurrence maps (once per unique row, as in PrepareGather) and the owner and
-// counter checks of ValidateUpdate (src/cuda/cache_backend.cu:321-333); the
-// gradients never leave the device.  eps_hip_prepare sorts the occurrences by
-// (table, slot) and eps_hip_push runs ReduceGradients
-// (src/access/batch_access.cpp:54-97: non-finite inputs rejected, scale
-// 1/valid_length for mean, sums in (feature, bag, position) order, overflow of
-// a sum rejected) fused with LazyAdam (src/update/lazy_adam.cpp:7-42), writing
-// nothing unless the whole call is valid.
-std::future<Result<Ack>> HipCacheBackend::PushDevice(std::vector<UpdateContext> contexts,
-                                                     std::vector<AgentWork> work,
+std::future<Result<Ack>> HipCacheBackend::PushDevice(std::vector<UpdateContext> contexts, std::vector<AgentWork> work,
                                                      std::vector<FeatureInput> layouts,
                                                      std::vector<DeviceTensorBlock> gradients) {
-  return impl_->worker->Submit<Ack>([this, contexts = std::move(contexts), work = std::move(work),
-                                     layouts = std::move(layouts), gradients = std::move(gradients)] {
+  return impl_->queue->Post<Ack>([this, contexts = std::move(contexts), work = std::move(work),
+                                  layouts = std::move(layouts), gradients = std::move(gradients)] {
     Impl& I = *impl_;
     I.Activate();
-    struct PushTable {
-      Impl::Table* table;
-      const UpdateContext* context;
-      std::uint32_t index;
-      std::vector<Key> rows;  // unique rows touched, first-touch order
-      std::unordered_map<Key, std::uint64_t> slots;
-    };
-    std::map<TableId, PushTable> tables;
+    // One context per pushed table; one gradient block per pushed feature.
+    std::map<TableId, const UpdateContext*> context_of;
     for (const auto& c : contexts) {
-      Impl::Table& t = I.CheckContext(c);
-      Require(tables.emplace(c.table, PushTable{&t, &c, UINT32_MAX, {}, {}}).second,
-              "duplicate HIP update context");
+      Impl::CheckContext(c);
+      Expect(context_of.emplace(c.table, &c).second, "two update contexts for one table");
     }
-    std::map<std::uint32_t, const DeviceTensorBlock*> gradient_of;
-    for (const auto& g : gradients)
-      Require(gradient_of.emplace(g.feature, &g).second, "duplicate gradient feature");
-    Require(gradients.size() == work.size(), "gradient feature count mismatch");
-    Require(work.size() <= EPS_HIP_MAX_FEATURES, "too many features for one HIP push",
-            Error::Code::capacity_exceeded);
-    struct Part {
-      PushTable* table;
-      const FeatureInput* layout;
-      const DeviceTensor* gradient;
-      std::uint64_t slots, offsets, lengths;
-    };
-    std::vector<Part> parts;
-    parts.reserve(work.size());
-    auto* index = I.host_indices.As<std::uint64_t>();
-    std::uint64_t used = 0, occurrences = 0;
-    std::uint32_t table_count = 0;
-    std::set<std::uint32_t> features;
-    for (const auto& task : work) {
-      auto it = std::find_if(layouts.begin(), layouts.end(),
-                             [&](const FeatureInput& f) { return f.feature == task.feature; });
-      Require(features.insert(task.feature).second, "duplicate HIP push feature");
-      Require(it != layouts.end() && task.agent == I.options.agent &&
-                  task.route == AccessRoute::resident_gpu && task.transferred_weights.empty(),
-              "invalid HIP push work");
-      const FeatureInput& f = *it;
-      auto pt = tables.find(f.table);
-      Require(pt != tables.end(), "missing HIP update context");
-      PushTable& target = pt->second;
-      const std::uint64_t dim = target.table->definition.dimension;
-      Require(task.occurrence_to_unique.size() == f.keys.size() && !f.offsets.empty() &&
-                  f.offsets.front() == 0 && f.offsets.back() == f.keys.size() &&
-                  std::is_sorted(f.offsets.begin(), f.offsets.end()) &&
-                  f.valid_lengths.size() + 1 == f.offsets.size(),
-              "invalid HIP push layout");
-      auto g = gradient_of.find(f.feature);
-      Require(g != gradient_of.end(), "missing feature gradient");
-      const DeviceTensorBlock& block = *g->second;
-      const std::uint64_t rows = f.pooling == Pooling::sequence ? f.keys.size() : f.valid_lengths.size();
-      Require(block.tensor && block.shape == std::vector<std::uint64_t>{rows, dim} &&
-                  block.tensor->elements() == rows * dim && block.tensor->device() == I.options.device &&
-                  (rows == 0 || block.tensor->data() != nullptr),
-              "gradient tensor layout mismatch");
-      I.Limit((used + f.keys.size() + f.offsets.size() + f.valid_lengths.size()) * 8);
-      if (target.index == UINT32_MAX) target.index = table_count++;
-      Part part{&target, &f, block.tensor.get(), used, 0, 0};
-      constexpr std::uint64_t kUnresolved = std::numeric_limits<std::uint64_t>::max() - 1;
-      std::vector<std::uint64_t> slot_of(task.rows.size(), kUnresolved);
-      for (std::size_t i = 0; i < f.keys.size(); ++i) {
-        const std::uint64_t unique = task.occurrence_to_unique[i];
-        if (unique == UINT64_MAX) {
-          index[used++] = UINT64_MAX;
-          continue;
-        }
-        Require(unique < task.rows.size() && task.rows[unique].row == RowKey{f.table, f.keys[i]},
-                "invalid HIP occurrence map");
-        if (slot_of[unique] == kUnresolved) {
-          const Impl::Entry& e = I.Find(task.rows[unique]);
-          Impl::CheckOwner(*target.context, e);
-          slot_of[unique] = e.location.slot;
-          if (target.slots.emplace(f.keys[i], e.location.slot).second) target.rows.push_back(f.keys[i]);
-        }
-        index[used++] = slot_of[unique];
+    std::unordered_map<std::uint32_t, const DeviceTensorBlock*> gradient_of;
+    for (const auto& g : gradients) Expect(gradient_of.emplace(g.feature, &g).second, "two gradients for one feature");
+    Expect(work.size() <= EPS_HIP_MAX_FEATURES, "too many features in one device push");
+    auto parts = I.ResolveWork(work, layouts, false);
+    // Call tables in first-use order; the push's per-table optimizers.
+    std::vector<TableId> order;
+    std::map<TableId, std::uint32_t> index_of;
+    std::vector<eps_hip_table> tables;
+    std::vector<eps_hip_optimizer> optimizers;
+    std::vector<eps_hip_push_feature> features;
+    std::uint64_t occurrences = 0;
+    for (const auto& r : parts) {
+      const FeatureInput& L = *r.layout;
+      auto c = context_of.find(L.table);
+      Expect(c != context_of.end(), "device push without a context for its table");
+      auto g = gradient_of.find(L.feature);
+      const std::uint64_t dim = r.table->dim();
+      Expect(g != gradient_of.end() && g->second->tensor && g->second->shape.size() == 2 &&
+                 g->second->shape[0] == r.rows && g->second->shape[1] == dim &&
+                 g->second->tensor->elements() == r.rows * dim && g->second->tensor->device() == I.options.device,
+             "device gradient does not match its feature");
+      auto [it, fresh] = index_of.emplace(L.table, std::uint32_t(tables.size()));
+      if (fresh) {
+        order.push_back(L.table);
+        tables.push_back(r.table->abi);
+        optimizers.push_back(I.Optimizer(*r.table, c->second->learning_rate, c->second->beta1_power,
+                                         c->second->beta2_power));
       }
-      occurrences += f.keys.size();
-      part.offsets = used;
-      std::copy(f.offsets.begin(), f.offsets.end(), index + used);
-      used += f.offsets.size();
-      part.lengths = used;
-      std::copy(f.valid_lengths.begin(), f.valid_lengths.end(), index + used);
-      used += f.valid_lengths.size();
-      parts.push_back(part);
-    }
-    if (!occurrences) return Ack{};
-    std::vector<eps_hip_table> abi_tables(table_count);
-    std::vector<eps_hip_optimizer> optimizers(table_count);
-    for (auto& [id, t] : tables) {
-      if (t.index == UINT32_MAX) continue;
-      abi_tables[t.index] = t.table->abi;
-      optimizers[t.index] = I.Optimizer(*t.table, *t.context);
-    }
-    const std::uint64_t bytes = eps_hip_push_workspace_bytes(occurrences);
-    I.ReservePush(bytes);
-    hipStream_t s = I.stream.value;
-    try {
-      I.CopyIn(I.device_indices.pointer, I.host_indices.pointer, used * 8);
-      const auto* device = I.device_indices.As<std::uint64_t>();
-      std::vector<eps_hip_push_feature> features;
-      features.reserve(parts.size());
-      for (const auto& p : parts) {
-        p.gradient->WaitOnStream(s);
-        const FeatureInput& f = *p.layout;
-        eps_hip_push_feature x{};
-        x.indices = device + p.slots;
-        x.offsets = device + p.offsets;
-        x.valid_lengths = f.pooling == Pooling::mean ? device + p.lengths : nullptr;
-        x.gradients = static_cast<const float*>(p.gradient->data());
-        x.occurrences = f.keys.size();
-        x.bags = f.valid_lengths.size();
-        x.table = p.table->index;
-        x.pooling = PoolingCode(f.pooling);
-        features.push_back(x);
+      g->second->tensor->WaitOnStream(I.stream);
+      eps_hip_push_feature f{};
+      f.indices = r.occurrences ? r.slots : nullptr;
+      f.offsets = r.offsets;
+      f.valid_lengths = r.lengths;
+      f.gradients = static_cast<const float*>(g->second->tensor->data());
+      f.occurrences = r.occurrences;
+      f.bags = L.pooling == Pooling::sequence ? 1 : r.rows;
+      f.table = it->second;
+      f.pooling = L.pooling == Pooling::sum ? EPS_HIP_POOL_SUM
+                  : L.pooling == Pooling::mean ? EPS_HIP_POOL_MEAN
+                                               : EPS_HIP_POOL_SEQUENCE;
+      if (L.pooling == Pooling::sequence) {  // one bag holding every occurrence
+        f.offsets = nullptr;
+        f.valid_lengths = nullptr;
       }
-      Abi(eps_hip_prepare(abi_tables.data(), table_count, features.data(), std::uint32_t(features.size()),
-                          I.push_workspace.pointer, bytes, s));
-      Abi(eps_hip_push(abi_tables.data(), optimizers.data(), table_count, features.data(),
-                       std::uint32_t(features.size()), I.push_workspace.pointer, bytes, I.bounds.pointer, s));
-      I.CheckStatus(I.push_workspace.pointer);
-    } catch (...) {
-      (void)hipStreamSynchronize(s);
-      throw;
+      features.push_back(f);
+      occurrences += r.occurrences;
     }
-    for (auto& [id, t] : tables)
-      for (Key key : t.rows) ++t.table->rows.at(key).updates;
+    Expect(tables.size() <= EPS_HIP_MAX_TABLES, "too many tables in one device push");
+    // Every unique row the push updates, once per table.
+    std::vector<Resident*> updated;
+    {
+      std::set<std::pair<TableId, Key>> seen;
+      for (const auto& r : parts)
+        for (const Resident* u : r.unique) {
+          Expect(u->updates != UINT64_MAX && u->where.home == context_of.at(u->where.row.table)->shard,
+                 "device push row is not this shard's");
+          if (seen.emplace(u->where.row.table, u->where.row.key).second) updated.push_back(const_cast<Resident*>(u));
+        }
+    }
+    I.CheckResolution();
+    if (features.empty()) return Ack{};
+    I.ReservePush(occurrences);
+    void* ws = I.push_ws.Get();
+    const std::uint64_t bytes = I.push_ws.bytes();
+    AbiOk(eps_hip_prepare(tables.data(), std::uint32_t(tables.size()), features.data(), std::uint32_t(features.size()),
+                          ws, bytes, I.stream));
+    AbiOk(eps_hip_push(tables.data(), optimizers.data(), std::uint32_t(tables.size()), features.data(),
+                       std::uint32_t(features.size()), ws, bytes, I.bounds.Get(), I.stream));
+    Impl::UpdateVerdict(I.ReadFlag(eps_hip_status_word(ws)));
+    for (Resident* r : updated) ++r->updates;
     return Ack{};
   });
 }
 
-// Snapshot writeback.  Rows are encoded in file order chunk by chunk: the
-// device rows of chunk c + 1 are gathered into one half of the pinned staging
-// (eps_hip_gather_rows writes host memory directly) while the host hashes and
-// writes chunk c from the other half.  The checksum, a byte-serial FNV-1a, is
-// the host's share and bounds the rate.
-std::future<Result<SnapshotFile>> HipCacheBackend::WriteSnapshot(std::filesystem::path file,
-                                                                 SnapshotIdentity identity,
+std::future<Result<SnapshotFile>> HipCacheBackend::WriteSnapshot(std::filesystem::path file, SnapshotIdentity identity,
                                                                  std::vector<SnapshotTable> tables,
                                                                  std::vector<RowState> host_rows) {
-  return impl_->worker->Submit<SnapshotFile>([this, file = std::move(file), identity = std::move(identity),
-                                              tables = std::move(tables),
-                                              host_rows = std::move(host_rows)] {
+  return impl_->queue->Post<SnapshotFile>([this, file = std::move(file), identity = std::move(identity),
+                                           tables = std::move(tables), host_rows = std::move(host_rows)] {
     Impl& I = *impl_;
     I.Activate();
     // The identity and schema checks the reference reader applies
     // (src/store/snapshot.cpp:201-206,230-245), so a written file restores.
-    Require(!identity.run.empty() && identity.run.size() <= 1024 && identity.shard_count > 0 &&
-                identity.shard < identity.shard_count && identity.epoch > 0 && tables.size() <= 1024,
-            "invalid snapshot identity");
+    Expect(!identity.run.empty() && identity.run.size() <= 1024 && identity.shard_count > 0 &&
+               identity.shard < identity.shard_count && identity.epoch > 0 && tables.size() <= 1024,
+           "invalid snapshot identity");
     std::map<std::pair<TableId, Key>, const RowState*> host;
     for (const auto& r : host_rows)
-      Require(host.emplace(std::make_pair(r.row.table, r.row.key), &r).second, "duplicate snapshot host row");
+      Expect(host.emplace(std::make_pair(r.row.table, r.row.key), &r).second, "a host row is given twice");
     std::set<TableId> ids;
     std::uint64_t device_rows = 0;
     for (const auto& t : tables) {
       const auto& d = t.definition;
-      Require(ids.insert(d.id).second && d.dimension > 0 && d.dimension <= 65536 &&
-                  d.shard_count == identity.shard_count && d.partition_epoch == identity.epoch &&
-                  t.beta1_power >= 0 && t.beta1_power < 1 && t.beta2_power >= 0 && t.beta2_power < 1,
-              "invalid snapshot table");
+      Expect(ids.insert(d.id).second && d.dimension > 0 && d.dimension <= 65536 &&
+                 d.shard_count == identity.shard_count && d.partition_epoch == identity.epoch &&
+                 t.beta1_power >= 0 && t.beta1_power < 1 && t.beta2_power >= 0 && t.beta2_power < 1,
+             "invalid snapshot table");
       auto it = I.tables.find(d.id);
-      Require(it == I.tables.end() || it->second->definition == d, "HIP table configuration mismatch");
-      std::set<Key> keys;
+      Expect(it == I.tables.end() || it->second->definition == d, "snapshot table is defined differently here");
+      std::unordered_set<Key> keys;
       for (Key key : t.keys) {
-        Require(keys.insert(key).second, "duplicate snapshot row");
+        Expect(keys.insert(key).second, "snapshot names a row twice");
         const bool resident = it != I.tables.end() && it->second->rows.count(key);
         auto h = host.find({d.id, key});
-        Require(resident != (h != host.end()), "snapshot row must be held by exactly one store");
+        Expect(resident != (h != host.end()), "a snapshot row must be held by exactly one store");
         if (resident) {
           ++device_rows;
         } else {
           const RowState& r = *h->second;
-          Require(r.weights.size() == d.dimension && r.first_moment.size() == d.dimension &&
-                      r.second_moment.size() == d.dimension,
-                  "snapshot host row shape mismatch");
+          Expect(r.weights.size() == d.dimension && r.first_moment.size() == d.dimension &&
+                     r.second_moment.size() == d.dimension,
+                 "snapshot host row has the wrong shape");
         }
       }
-      Require(it == I.tables.end() || 2 * std::uint64_t(d.dimension) * 12 <= I.options.transfer_bytes,
-              "snapshot row exceeds the staging buffer", Error::Code::capacity_exceeded);
+      Expect(it == I.tables.end() || I.options.transfer_bytes / 2 / 256 * 256 >= 256 + std::uint64_t(d.dimension) * 12 + 8,
+             "snapshot row exceeds the transfer staging", Code::capacity_exceeded);
     }
 
-    hip_detail::SnapshotWriter out(file);
-    hip_detail::WriteSnapshotHeader(out, identity, tables.size());
-    Event ready[2] = {Event(I.options.device), Event(I.options.device)};
-    const std::uint64_t half_bytes = I.options.transfer_bytes / 2;
-    for (const auto& t : tables) {
-      const auto& d = t.definition;
-      hip_detail::WriteSnapshotTable(out, t);
-      auto it = I.tables.find(d.id);
-      Impl::Table* table = it == I.tables.end() ? nullptr : it->second.get();
-      const std::uint64_t floats = std::uint64_t(d.dimension) * 3;
-      const std::uint64_t cap = table ? std::min(half_bytes / (floats * 4), half_bytes / 8) : 0;
-      // Chunks: [begin, end) of the key list holding at most `cap` device rows.
-      std::vector<std::pair<std::size_t, std::size_t>> chunks;
-      for (std::size_t b = 0; b < t.keys.size();) {
-        std::size_t e = b;
-        std::uint64_t n = 0;
-        while (e < t.keys.size() && (!table || !table->rows.count(t.keys[e]) || n < cap)) {
-          if (table && table->rows.count(t.keys[e])) ++n;
-          ++e;
-        }
-        chunks.emplace_back(b, e);
-        b = e;
+    hipbk::SnapshotWriter out(file);
+    hipbk::WriteSnapshotHeader(out, identity, tables.size());
+    // Device rows come back in chunks through two halves of the transfer
+    // area: the device fills one half while the host hashes the other.
+    hipEvent_t ready[2] = {nullptr, nullptr};
+    for (auto& e : ready) HipOk(hipEventCreateWithFlags(&e, hipEventDisableTiming), "snapshot event");
+    struct EventGuard {
+      hipEvent_t* e;
+      ~EventGuard() {
+        for (int i = 0; i < 2; ++i)
+          if (e[i]) (void)hipEventDestroy(e[i]);
       }
-      auto issue = [&](std::size_t c) {
-        const int h = int(c % 2);
-        auto* slots = I.host_indices.As<std::uint64_t>() + h * (half_bytes / 8);
-        std::uint64_t n = 0;
-        for (std::size_t i = chunks[c].first; i < chunks[c].second; ++i)
-          if (table)
-            if (auto r = table->rows.find(t.keys[i]); r != table->rows.end()) slots[n++] = r->second.location.slot;
-        if (n) {
-          auto* dslots = I.device_indices.As<std::uint64_t>() + h * (half_bytes / 8);
-          I.CopyIn(dslots, slots, n * 8);
-          Abi(eps_hip_gather_rows(&table->abi, dslots,
-                                  reinterpret_cast<float*>(I.host_values.As<unsigned char>() + h * half_bytes), n,
-                                  I.stream.value));
+    } guard{ready};
+    I.transfer.Reset();
+    const std::uint64_t half = I.transfer.capacity() / 2 / 256 * 256;
+    auto halves = std::array<Transfer::Piece<unsigned char>, 2>{I.transfer.Take<unsigned char>(half),
+                                                               I.transfer.Take<unsigned char>(half)};
+    try {
+      for (const auto& t : tables) {
+        const auto& d = t.definition;
+        hipbk::WriteSnapshotTable(out, t);
+        auto it = I.tables.find(d.id);
+        SlotTable* table = it == I.tables.end() ? nullptr : it->second.get();
+        const std::uint64_t width = 3ull * d.dimension;
+        // A chunk's slots (rounded up to 256 bytes) and rows fit in a half.
+        const std::uint64_t per_chunk = table ? (half - 256) / (width * 4 + 8) : 0;
+        auto resident = [&](Key key) -> const Resident* {
+          if (!table) return nullptr;
+          auto r = table->rows.find(key);
+          return r == table->rows.end() ? nullptr : &r->second;
+        };
+        // Chunks: [begin, end) of the key list with at most per_chunk device rows.
+        std::vector<std::pair<std::size_t, std::size_t>> chunks;
+        for (std::size_t b = 0; b < t.keys.size();) {
+          std::size_t e = b;
+          for (std::uint64_t n = 0; e < t.keys.size(); ++e) {
+            if (!resident(t.keys[e])) continue;
+            if (n == per_chunk) break;
+            ++n;
+          }
+          chunks.emplace_back(b, e);
+          b = e;
         }
-        Hip(hipEventRecord(ready[h].value, I.stream.value));
-      };
-      try {
+        auto issue = [&](std::size_t c) {
+          const auto& h = halves[c % 2];
+          auto* slots = reinterpret_cast<std::uint64_t*>(h.host);
+          auto* dslots = reinterpret_cast<std::uint64_t*>(h.device);
+          std::uint64_t n = 0;
+          for (std::size_t i = chunks[c].first; i < chunks[c].second; ++i)
+            if (const Resident* r = resident(t.keys[i])) slots[n++] = r->where.slot;
+          if (n) {
+            float* rows = reinterpret_cast<float*>(h.host + RoundUp(n * 8, 256));
+            HipOk(hipMemcpyAsync(dslots, slots, n * 8, hipMemcpyHostToDevice, I.stream), "snapshot slots");
+            AbiOk(eps_hip_gather_rows(&table->abi, dslots, rows, n, I.stream));
+          }
+          HipOk(hipEventRecord(ready[c % 2], I.stream), "snapshot event");
+        };
         if (!chunks.empty()) issue(0);
         for (std::size_t c = 0; c < chunks.size(); ++c) {
           if (c + 1 < chunks.size()) issue(c + 1);
-          const int h = int(c % 2);
-          Hip(hipEventSynchronize(ready[h].value));
-          const float* staged = reinterpret_cast<const float*>(I.host_values.As<unsigned char>() + h * half_bytes);
+          HipOk(hipEventSynchronize(ready[c % 2]), "snapshot rows");
+          const auto& h = halves[c % 2];
           std::uint64_t n = 0;
+          for (std::size_t i = chunks[c].first; i < chunks[c].second; ++i)
+            if (resident(t.keys[i])) ++n;
+          const float* rows = reinterpret_cast<const float*>(h.host + RoundUp(n * 8, 256));
+          std::uint64_t k = 0;
           for (std::size_t i = chunks[c].first; i < chunks[c].second; ++i) {
             const Key key = t.keys[i];
-            const Impl::Entry* entry = nullptr;
-            if (table)
-              if (auto r = table->rows.find(key); r != table->rows.end()) entry = &r->second;
-            if (entry) {
-              hip_detail::WriteSnapshotRow(out, key, entry->updates, staged + n * floats, d.dimension);
-              ++n;
+            if (const Resident* r = resident(key)) {
+              hipbk::WriteSnapshotRow(out, key, r->updates, rows + k * width, d.dimension);
+              ++k;
             } else {
-              hip_detail::WriteSnapshotRow(out, *host.at({d.id, key}));
+              hipbk::WriteSnapshotRow(out, *host.at({d.id, key}));
             }
           }
         }
-      } catch (...) {
-        (void)hipStreamSynchronize(I.stream.value);
-        throw;
       }
+    } catch (...) {
+      (void)hipStreamSynchronize(I.stream);
+      throw;
     }
     const std::uint64_t bytes = out.bytes() + 8;
     const std::uint64_t checksum = out.Publish();
@@ -1157,15 +1220,67 @@ std::future<Result<SnapshotFile>> HipCacheBackend::WriteSnapshot(std::filesystem
   });
 }
 
+std::future<Result<std::vector<LocatedRow>>> HipCacheBackend::RestoreSnapshot(std::filesystem::path file,
+                                                                              SnapshotIdentity identity,
+                                                                              MigrationPlan plan) {
+  return impl_->queue->Post<std::vector<LocatedRow>>([this, file = std::move(file), identity = std::move(identity),
+                                                      plan = std::move(plan)] {
+    Impl& I = *impl_;
+    I.Activate();
+    I.CheckAdmission(plan);
+    std::map<std::pair<TableId, Key>, std::size_t> wanted;
+    for (std::size_t i = 0; i < plan.rows.size(); ++i) wanted[{plan.rows[i].row.table, plan.rows[i].row.key}] = i;
+    hipbk::SnapshotReader in(file);
+    Expect(in.run == identity.run && in.shard == identity.shard && in.shard_count == identity.shard_count &&
+               in.epoch == identity.epoch && in.shard_count >= 1 && in.shard < in.shard_count && in.epoch >= 1,
+           "snapshot is not the named checkpoint");
+    // Every wanted row's state, read in file order (the checksum is checked
+    // before anything is admitted).
+    std::vector<std::vector<float>> states(plan.rows.size());
+    std::vector<std::uint64_t> updates(plan.rows.size());
+    std::vector<bool> found(plan.rows.size(), false);
+    std::set<TableId> tables_seen;
+    std::vector<float> scratch;
+    for (std::uint64_t k = 0; k < in.tables; ++k) {
+      const auto t = in.NextTable();
+      const TableId id = t.definition.id;
+      Expect(tables_seen.insert(id).second, "snapshot defines a table twice");
+      auto here = I.tables.find(id);
+      const bool used = std::any_of(plan.rows.begin(), plan.rows.end(), [&](const LocatedRow& r) { return r.row.table == id; });
+      if (used) Expect(here != I.tables.end() && here->second->definition == t.definition,
+                       "snapshot table is defined differently here");
+      scratch.resize(3ull * t.definition.dimension);
+      for (std::uint64_t j = 0; j < t.rows; ++j) {
+        Key key = 0;
+        std::uint64_t counter = 0;
+        in.Row(t.definition.dimension, key, counter, scratch.data());
+        auto w = wanted.find({id, key});
+        if (w == wanted.end()) continue;
+        Expect(!found[w->second], "snapshot holds a row twice");
+        found[w->second] = true;
+        states[w->second] = scratch;
+        updates[w->second] = counter;
+      }
+    }
+    in.Finish();
+    Expect(std::all_of(found.begin(), found.end(), [](bool f) { return f; }), "a planned row is not in the snapshot");
+    return I.Admit(plan, updates, [&](std::size_t i, float* dst) {
+      std::memcpy(dst, states[i].data(), states[i].size() * 4);
+    });
+  });
+}
+
 std::future<Result<HipMemoryStats>> HipCacheBackend::MemoryStats() {
-  return impl_->worker->Submit<HipMemoryStats>([this] {
-    std::uint64_t state = 0;
-    for (const auto& [id, table] : impl_->tables)
-      state += impl_->options.rows_per_table * std::uint64_t(table->definition.dimension) * 12;
-    const std::uint64_t staging = impl_->options.transfer_bytes * 3 + eps_hip_update_workspace_bytes() +
-                                  eps_hip_bounds_bytes() + 256 + impl_->push_bytes;
-    return HipMemoryStats{state, staging, impl_->output_budget->used.load(),
-                          impl_->output_budget->allocations.load()};
+  return impl_->queue->Post<HipMemoryStats>([this] {
+    const Impl& I = *impl_;
+    std::uint64_t state = 0, indexes = 0;
+    for (const auto& [id, t] : I.tables) {
+      state += I.options.rows_per_table * std::uint64_t(t->dim()) * 12;
+      indexes += t->index.bytes();
+    }
+    const std::uint64_t staging = I.transfer.device_bytes() + I.update_ws.bytes() + I.push_ws.bytes() +
+                                  I.bounds.bytes() + I.flags.bytes() + indexes;
+    return HipMemoryStats{state, staging, I.ledger->used.load(), I.ledger->blocks.load()};
   });
 }
 

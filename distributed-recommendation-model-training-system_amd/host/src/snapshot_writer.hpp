@@ -27,9 +27,9 @@
 #include <vector>
 
 #include "eps/hip_cache_backend.hpp"
-#include "executor.hpp"
+#include "job_queue.hpp"
 
-namespace eps::hip_detail {
+namespace eps::hipbk {
 
 static_assert(std::endian::native == std::endian::little,
               "snapshot rows are copied as little-endian bytes");
@@ -43,7 +43,7 @@ class SnapshotWriter {
     std::error_code ec;
     if (file_.has_parent_path()) std::filesystem::create_directories(file_.parent_path(), ec);
     fd_ = ::open(pending_.c_str(), O_WRONLY | O_CREAT | O_EXCL, 0600);
-    Require(fd_ >= 0, "cannot create snapshot staging file", Error::Code::unavailable);
+    Expect(fd_ >= 0, "cannot create snapshot staging file", Error::Code::unavailable);
     for (auto& b : buffers_) b.resize(kBuffer);
     io_ = std::thread([this] { Drain(); });
   }
@@ -77,20 +77,20 @@ class SnapshotWriter {
     Append(&checksum, 8);
     Hand();
     Stop();
-    Require(!io_failed_, "snapshot write failed", Error::Code::unavailable);
-    Require(::fsync(fd_) == 0, "snapshot fsync failed", Error::Code::unavailable);
+    Expect(!io_failed_, "snapshot write failed", Error::Code::unavailable);
+    Expect(::fsync(fd_) == 0, "snapshot fsync failed", Error::Code::unavailable);
     ::close(fd_);
     fd_ = -1;
-    Require(::link(pending_.c_str(), file_.c_str()) == 0,
+    Expect(::link(pending_.c_str(), file_.c_str()) == 0,
             "snapshot already exists or cannot be published", Error::Code::unavailable);
     published_ = true;
     ::unlink(pending_.c_str());
     const auto dir = file_.has_parent_path() ? file_.parent_path() : std::filesystem::path(".");
     const int d = ::open(dir.c_str(), O_RDONLY);
-    Require(d >= 0, "cannot open snapshot directory", Error::Code::unavailable);
+    Expect(d >= 0, "cannot open snapshot directory", Error::Code::unavailable);
     const int rc = ::fsync(d);
     ::close(d);
-    Require(rc == 0, "snapshot fsync failed", Error::Code::unavailable);
+    Expect(rc == 0, "snapshot fsync failed", Error::Code::unavailable);
     return checksum;
   }
 
@@ -115,7 +115,7 @@ class SnapshotWriter {
   void Hand() {
     std::unique_lock<std::mutex> lock(mutex_);
     idle_.wait(lock, [&] { return !busy_; });
-    Require(!io_failed_, "snapshot write failed", Error::Code::unavailable);
+    Expect(!io_failed_, "snapshot write failed", Error::Code::unavailable);
     ready_ = current_;
     ready_bytes_ = filled_;
     busy_ = true;
@@ -224,4 +224,4 @@ inline void WriteSnapshotRow(SnapshotWriter& out, const RowState& row) {
   out.Bytes(row.second_moment.data(), row.second_moment.size() * 4);
 }
 
-}  // namespace eps::hip_detail
+}  // namespace eps::hipbk

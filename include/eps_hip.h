@@ -144,6 +144,35 @@ int eps_hip_scatter_rows(const eps_hip_table* table, const uint64_t* slots,
 int eps_hip_gather_rows(const eps_hip_table* table, const uint64_t* slots, float* packed,
                         uint64_t count, void* stream);
 
+/* ---- device key -> slot index of a table ---- */
+/* The reference keeps a host hash map per table (CudaCacheBackend's
+ * Table::rows, src/cuda/cache_backend.cu:193-198) and looks every key
+ * occurrence up in it on the host before a gather (:279-291).  This index is
+ * an open-addressing hash table in device memory (16 bytes per bucket,
+ * `capacity` a power of two, at most half full for short probes) that
+ * admissions insert into and evictions remove from, so occurrences resolve on
+ * the device.  Keys of one insert or remove call must be distinct; a key must
+ * not be inserted twice.  Failures (a full index, removing a key that is not
+ * there) set EPS_HIP_STATUS_BAD_INDEX in `status` (device u32, may be NULL). */
+uint64_t eps_hip_index_bytes(uint64_t capacity);
+int eps_hip_index_clear(void* index, uint64_t capacity, void* stream);
+int eps_hip_index_insert(void* index, uint64_t capacity, const uint64_t* keys, const uint64_t* slots,
+                         uint64_t count, uint32_t* status, void* stream);
+int eps_hip_index_remove(void* index, uint64_t capacity, const uint64_t* keys, uint64_t count,
+                         uint32_t* status, void* stream);
+/* Slots of n key occurrences (the per-occurrence part of PrepareGather,
+ * :279-291).  With `occurrence_to_unique` (the lookup's AgentWork map): a
+ * UINT64_MAX entry stays a hole; otherwise occurrence i must name its unique
+ * row (keys[i] == unique_keys[occurrence_to_unique[i]]) and resolves through
+ * `index` to that row's slot, or, with no index, to the unique index itself
+ * (rows carried with the request).  Without a map, keys absent from the index
+ * become holes.  Any mismatch sets BAD_INDEX in `status` (the reference's
+ * "invalid occurrence map") and resolves to a hole. */
+int eps_hip_resolve(const void* index, uint64_t capacity, const uint64_t* keys,
+                    const uint64_t* occurrence_to_unique, const uint64_t* unique_keys,
+                    uint64_t unique_count, uint64_t n, uint64_t* slots, uint32_t* status,
+                    void* stream);
+
 /* ---- pull ---- */
 /* Pooled gather of up to EPS_HIP_MAX_GATHER_PARTS features in one launch.
  * Replaces LaunchGather/GatherKernel (:309-320,81-94) and fuses NormalizeMean

@@ -23,6 +23,7 @@
 #include <iostream>
 #include <limits>
 #include <map>
+#include <set>
 #include <stdexcept>
 #include <string>
 #include <vector>
@@ -614,24 +615,43 @@ void SnapshotWriteback() {
   Check(eps_or_snapshot_write(again.c_str(), run, shard, count, epoch, stores, ntables) == 0, "oracle writer");
   Check(FileBytes(again) == FileBytes(file), "snapshot bytes differ from the oracle writer's");
 
-  // Restore and resume (tests/core_tests.cpp:107-129): a fresh backend loaded
-  // with the snapshot's rows and the original take the same update and end
-  // bit-identical, counters included.
+  // Restore and resume (tests/core_tests.cpp:107-129): a fresh backend
+  // restores every row of the file straight into HBM (RestoreSnapshot) and
+  // takes the same update as the original; both end bit-identical, counters
+  // included.  Refused restores (another checkpoint, a row the file lacks, a
+  // damaged copy) admit nothing.
   {
     HipCacheBackend restored(o);
     Take(restored.Define(big));
-    std::vector<RowState> rows;
-    for (Key key : order) {
-      RowState r{{5, key}, std::vector<float>(16), std::vector<float>(16), std::vector<float>(16), 0};
-      Check(eps_or_read(stores[0], key, r.weights.data(), r.first_moment.data(), r.second_moment.data(),
-                        &r.row_updates) == 0,
-            "snapshot row");
-      rows.push_back(std::move(r));
+    MigrationPlan plan{"restore", 0, {}, Placement::gpu, 0};
+    for (Key key : order) plan.rows.push_back({{5, key}, 0, Placement::loading, 0, 1, 0});
+    Check(Fails(restored.RestoreSnapshot(file, {"other-run", 0, 1, 1}, plan), "restore of another checkpoint") ==
+              Error::Code::invalid_argument,
+          "wrong checkpoint code");
+    auto too_many = plan;
+    too_many.rows.push_back({{5, 5000}, 0, Placement::loading, 0, 1, 0});
+    Fails(restored.RestoreSnapshot(file, id, too_many), "restore of a row the file lacks");
+    const auto damaged = dir / "damaged.bin";
+    {
+      std::string bytes = FileBytes(file);
+      bytes[bytes.size() / 3] ^= 0x01;
+      std::ofstream(damaged, std::ios::binary) << bytes;
     }
+    Fails(restored.RestoreSnapshot(damaged, id, plan), "restore of a damaged file");
+    Check(Take(restored.FreeSlots(5)) == 4096, "a refused restore admitted rows");
     std::map<Key, LocatedRow> where_restored;
-    for (std::size_t b = 0; b < rows.size(); b += 300) {
-      std::vector<RowState> part(rows.begin() + b, rows.begin() + std::min(rows.size(), b + 300));
-      for (const auto& loc : Take(restored.Load(Plan(part), part))) where_restored[loc.row.key] = loc;
+    for (const auto& loc : Take(restored.RestoreSnapshot(file, id, plan))) where_restored[loc.row.key] = loc;
+    Check(where_restored.size() == order.size() && Take(restored.FreeSlots(5)) == 4096 - order.size(),
+          "restored rows");
+    for (std::size_t b = 0; b < order.size(); b += 300) {  // ReadBack is bounded by the staging
+      MigrationPlan some{"read", 0, {}, Placement::cpu, 0};
+      for (std::size_t i = b; i < std::min(order.size(), b + 300); ++i) some.rows.push_back(where_restored.at(order[i]));
+      for (const auto& r : Take(restored.ReadBack(some))) {
+        const RowState& want = expect.at({5, r.row.key});
+        Check(SameBits(r.weights, want.weights) && SameBits(r.first_moment, want.first_moment) &&
+                  SameBits(r.second_moment, want.second_moment) && r.row_updates == want.row_updates,
+              "restored row differs from the snapshot");
+      }
     }
     RowGradients g;
     MigrationPlan before{"read", 0, {}, Placement::cpu, 0}, after = before;
@@ -677,10 +697,412 @@ void SnapshotWriteback() {
   std::filesystem::remove_all(dir);
 }
 
+eps_or_table_def OracleDef(const TableDefinition& d) {
+  eps_or_table_def def{};
+  def.id = d.id;
+  def.dim = d.dimension;
+  def.shard = 0;
+  def.shard_count = 1;
+  def.learning_rate = d.optimizer.learning_rate;
+  def.beta1 = d.optimizer.beta1;
+  def.beta2 = d.optimizer.beta2;
+  def.epsilon = d.optimizer.epsilon;
+  def.initial_beta1_power = d.optimizer.initial_beta1_power;
+  def.initial_beta2_power = d.optimizer.initial_beta2_power;
+  def.bounded = d.optimizer.weight_bounds ? 1 : 0;
+  if (d.optimizer.weight_bounds) {
+    def.weight_min = d.optimizer.weight_bounds->minimum;
+    def.weight_max = d.optimizer.weight_bounds->maximum;
+  }
+  def.init_min = d.initialization_min;
+  def.init_max = d.initialization_max;
+  def.init_seed = d.initialization_seed;
+  return def;
+}
+
+eps_or_feature AsOracle(const FeatureInput& f) {
+  return {f.keys.data(), f.keys.size(), f.offsets.data(), f.valid_lengths.data(), nullptr,
+          f.valid_lengths.size(), uint32_t(f.pooling), f.feature};
+}
+
+// The feature restricted to the occurrences `keep` accepts: bags keep their
+// place and their original lengths (the mean scale), as a shard sees its part
+// of a lookup (src/access/prepared_lookup.cpp:47-83).
+template <typename Keep>
+FeatureInput Restrict(const FeatureInput& f, Keep keep) {
+  FeatureInput out{f.table, f.feature, f.pooling, {}, {0}, f.valid_lengths};
+  for (std::size_t b = 0; b + 1 < f.offsets.size(); ++b) {
+    for (std::uint64_t i = f.offsets[b]; i < f.offsets[b + 1]; ++i)
+      if (keep(f.keys[i])) out.keys.push_back(f.keys[i]);
+    out.offsets.push_back(out.keys.size());
+  }
+  return out;
+}
+
+// A push over rows of mixed ownership, as the shard service runs it
+// (src/server/service.cpp:236-331): one lookup ticket of three features over
+// two tables; keys k % 3 == 0 live in the shard's CPU store, the others on
+// this agent.  Every step the service reduces the ticket's gradients per
+// table, applies LazyAdam to its CPU rows and sends the agent its rows'
+// gradients, compact (CSR) when that is smaller than the expanded rows and
+// the expanded rows exceed 20 bytes per row + 8 (:279-295), else expanded;
+// the powers advance once per table.  Odd steps take the device-resident
+// route instead: PushDevice for the agent's rows (the CPU keys are holes) and
+// the CPU rows through the shard's own push.  After every step each row,
+// wherever it lives, and each table's powers equal one CPU shard that held
+// every row and took the same pushes.
+void MixedPush() {
+  HipCacheOptions o = SmallOptions(4096);
+  o.state_bytes = 64ull << 20;
+  o.transfer_bytes = 8ull << 20;
+  HipCacheBackend gpu(o);
+  const std::vector<TableDefinition> defs = {Table(21, 64), Table(22, 32)};
+  constexpr Key kKeys = 3000;
+  auto on_cpu = [](Key k) { return k % 3 == 0; };
+  std::vector<eps_or_store*> truth, cpu;
+  std::map<std::pair<TableId, Key>, LocatedRow> where;
+  for (const auto& d : defs) {
+    Take(gpu.Define(d));
+    const eps_or_table_def def = OracleDef(d);
+    truth.push_back(eps_or_create(&def));
+    cpu.push_back(eps_or_create(&def));
+    std::vector<RowState> agent_rows;
+    for (Key k = 0; k < kKeys; ++k) {
+      Check(eps_or_ensure(truth.back(), k) >= 0, "oracle first touch");
+      RowState r{{d.id, k}, std::vector<float>(d.dimension), std::vector<float>(d.dimension),
+                 std::vector<float>(d.dimension), 0};
+      Check(eps_or_read(truth.back(), k, r.weights.data(), r.first_moment.data(), r.second_moment.data(),
+                        &r.row_updates) == 0,
+            "oracle read");
+      if (on_cpu(k)) {
+        Check(eps_or_import(cpu.back(), k, r.weights.data(), r.first_moment.data(), r.second_moment.data(), 0) == 0,
+              "oracle import");
+      } else {
+        agent_rows.push_back(std::move(r));
+      }
+    }
+    for (const auto& loc : Take(gpu.Load(Plan(agent_rows), agent_rows))) where[{loc.row.table, loc.row.key}] = loc;
+  }
+  std::uint64_t state = 99;
+  auto next = [&]() {
+    state += 0x9e3779b97f4a7c15ull;
+    std::uint64_t z = state;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+  };
+  int compact_sends = 0, expanded_sends = 0;
+  for (int step = 0; step < 4; ++step) {
+    // The ticket: feature 0 (table 21, mean), 1 (table 21, sum), 2 (table 22, sum).
+    std::vector<FeatureInput> layouts;
+    std::vector<std::vector<float>> grads;
+    const std::pair<std::size_t, Pooling> spec[] = {{0, Pooling::mean}, {0, Pooling::sum}, {1, Pooling::sum}};
+    for (std::uint32_t fi = 0; fi < 3; ++fi) {
+      const TableDefinition& d = defs[spec[fi].first];
+      FeatureInput f{d.id, fi, spec[fi].second, {}, {0}, {}};
+      // Step 2's bags hold one id each: every agent row has its own source
+      // row, so the CSR is larger than the expanded rows and goes expanded.
+      const int bags = step == 2 ? 120 : 300;
+      for (int b = 0; b < bags; ++b) {
+        const std::uint64_t len = step == 2 ? 1 : 1 + next() % 12;
+        for (std::uint64_t i = 0; i < len; ++i) {
+          const double u = double(next() >> 11) * 0x1.0p-53;
+          f.keys.push_back(Key(double(kKeys) * u * u * u));
+        }
+        f.offsets.push_back(f.keys.size());
+        f.valid_lengths.push_back(len + (b % 5 == 0 ? 1 : 0));
+      }
+      std::vector<float> g(f.valid_lengths.size() * d.dimension);
+      for (auto& x : g) x = float(std::int64_t(next() % 2001) - 1000) * 2e-5f;
+      layouts.push_back(std::move(f));
+      grads.push_back(std::move(g));
+    }
+    std::vector<eps_or_feature> of;
+    std::vector<const float*> og;
+    std::vector<std::uint32_t> store_of;
+    for (std::size_t i = 0; i < layouts.size(); ++i) {
+      of.push_back(AsOracle(layouts[i]));
+      og.push_back(grads[i].data());
+      store_of.push_back(layouts[i].table == 21 ? 0 : 1);
+    }
+    // The context of each table: the shard's powers before this push.
+    std::vector<UpdateContext> contexts;
+    for (std::size_t t = 0; t < defs.size(); ++t) {
+      float b1 = 0, b2 = 0;
+      std::uint64_t seq = 0;
+      eps_or_powers(cpu[t], &b1, &b2, &seq);
+      contexts.push_back({{"mixed", 0, std::uint64_t(step), Phase::push}, 0, defs[t].id, seq, kLr, b1, b2});
+    }
+    Check(eps_or_push(truth.data(), 2, of.data(), store_of.data(), og.data(), 3) == 0, "oracle push (all rows)");
+    if (step % 2 == 0) {
+      for (std::size_t t = 0; t < defs.size(); ++t) {
+        const std::uint32_t dim = defs[t].dimension;
+        std::vector<eps_or_feature> tf;
+        std::vector<const float*> tg;
+        std::uint64_t n = 0;
+        for (std::size_t i = 0; i < layouts.size(); ++i)
+          if (store_of[i] == t) {
+            tf.push_back(of[i]);
+            tg.push_back(og[i]);
+            n += of[i].key_count;
+          }
+        std::vector<std::uint64_t> keys(n + 1);
+        std::vector<float> values((n + 1) * dim);
+        std::uint64_t count = 0;
+        Check(eps_or_reduce_gradients(truth[t], tf.data(), tg.data(), uint32_t(tf.size()), keys.data(), values.data(),
+                                      &count) == 0,
+              "oracle reduce");
+        std::vector<std::uint64_t> cpu_keys, gpu_keys;
+        std::vector<float> cpu_values, gpu_values;
+        for (std::uint64_t u = 0; u < count; ++u) {
+          auto& k = on_cpu(keys[u]) ? cpu_keys : gpu_keys;
+          auto& v = on_cpu(keys[u]) ? cpu_values : gpu_values;
+          k.push_back(keys[u]);
+          v.insert(v.end(), values.begin() + u * dim, values.begin() + (u + 1) * dim);
+        }
+        // The agent's packet (service.cpp:279-295).
+        const std::uint64_t expanded = gpu_values.size() * 4;
+        bool sent = false;
+        if (!gpu_keys.empty() && expanded > gpu_keys.size() * 20 + 8) {
+          std::vector<float> source(n * dim + 1);
+          std::vector<std::uint64_t> offsets(gpu_keys.size() + 1), refs(n + 1);
+          std::vector<float> scales(n + 1);
+          std::uint64_t sources = 0, references = 0;
+          if (eps_or_build_compact(tf.data(), tg.data(), uint32_t(tf.size()), dim, gpu_keys.data(), gpu_keys.size(),
+                                   source.data(), &sources, offsets.data(), refs.data(), scales.data(),
+                                   &references) == 0) {
+            const std::uint64_t bytes = eps_or_compact_bytes(gpu_keys.size(), sources, references) -
+                                        gpu_keys.size() * sizeof(RowKey);
+            if (bytes < expanded) {
+              CompactGradients packet{{}, dim, {source.begin(), source.begin() + sources}, offsets,
+                                      {refs.begin(), refs.begin() + references},
+                                      {scales.begin(), scales.begin() + references}};
+              for (Key k : gpu_keys) packet.rows.push_back({defs[t].id, k});
+              Take(gpu.ApplyCompact(contexts[t], packet));
+              sent = true;
+              ++compact_sends;
+            }
+          }
+        }
+        if (!sent && !gpu_keys.empty()) {
+          RowGradients rg{{}, gpu_values};
+          for (Key k : gpu_keys) rg.rows.push_back({defs[t].id, k});
+          Take(gpu.ApplyHost(contexts[t], rg));
+          ++expanded_sends;
+        }
+        // CPU rows last; the table's powers advance once, rows or not (:325).
+        Check(eps_or_validate_lazy_adam(cpu[t], cpu_keys.data(), cpu_values.data(), cpu_keys.size()) == 0,
+              "oracle validate");
+        eps_or_apply_lazy_adam(cpu[t], cpu_keys.data(), cpu_values.data(), cpu_keys.size());
+      }
+    } else {
+      std::vector<AgentWork> work;
+      for (const auto& f : layouts) {
+        AgentWork w{f.feature, AccessRoute::resident_gpu, 0, {}, std::vector<std::uint64_t>(f.keys.size()), {}};
+        std::map<Key, std::uint64_t> unique;
+        for (std::size_t i = 0; i < f.keys.size(); ++i) {
+          if (on_cpu(f.keys[i])) {
+            w.occurrence_to_unique[i] = UINT64_MAX;
+            continue;
+          }
+          auto [it, fresh] = unique.emplace(f.keys[i], w.rows.size());
+          if (fresh) w.rows.push_back(where.at({f.table, f.keys[i]}));
+          w.occurrence_to_unique[i] = it->second;
+        }
+        work.push_back(std::move(w));
+      }
+      std::vector<DeviceTensorBlock> blocks;
+      for (std::size_t i = 0; i < layouts.size(); ++i) {
+        const std::uint64_t dim = layouts[i].table == 21 ? 64 : 32;
+        blocks.push_back({layouts[i].feature, {layouts[i].valid_lengths.size(), dim},
+                          std::make_shared<DeviceBuffer>(grads[i])});
+      }
+      Take(gpu.PushDevice(contexts, work, layouts, blocks));
+      std::vector<FeatureInput> mine;
+      std::vector<eps_or_feature> cf;
+      for (const auto& f : layouts) mine.push_back(Restrict(f, on_cpu));
+      for (const auto& f : mine) cf.push_back(AsOracle(f));
+      Check(eps_or_push(cpu.data(), 2, cf.data(), store_of.data(), og.data(), 3) == 0, "oracle push (CPU rows)");
+    }
+    // Every row against the single-shard truth.
+    for (std::size_t t = 0; t < defs.size(); ++t) {
+      float b1 = 0, b2 = 0, c1 = 0, c2 = 0;
+      std::uint64_t s1 = 0, s2 = 0;
+      eps_or_powers(truth[t], &b1, &b2, &s1);
+      eps_or_powers(cpu[t], &c1, &c2, &s2);
+      Check(b1 == c1 && b2 == c2 && s1 == s2, "powers advanced other than once per push");
+      const std::uint32_t dim = defs[t].dimension;
+      MigrationPlan read{"read", 0, {}, Placement::cpu, 0};
+      for (Key k = 0; k < kKeys; ++k) {
+        std::vector<float> w(dim), m(dim), v(dim), cw(dim), cm(dim), cv(dim);
+        std::uint64_t updates = 0, cu = 0;
+        Check(eps_or_read(truth[t], k, w.data(), m.data(), v.data(), &updates) == 0, "truth row");
+        if (on_cpu(k)) {
+          Check(eps_or_read(cpu[t], k, cw.data(), cm.data(), cv.data(), &cu) == 0 && SameBits(w, cw) &&
+                    SameBits(m, cm) && SameBits(v, cv) && cu == updates,
+                "CPU row of the mixed push differs");
+        } else {
+          read.rows.push_back(where.at({defs[t].id, k}));
+        }
+      }
+      for (const auto& r : Take(gpu.ReadBack(read))) {
+        std::vector<float> w(dim), m(dim), v(dim);
+        std::uint64_t updates = 0;
+        Check(eps_or_read(truth[t], r.row.key, w.data(), m.data(), v.data(), &updates) == 0, "truth row");
+        Check(SameBits(r.weights, w) && SameBits(r.first_moment, m) && SameBits(r.second_moment, v) &&
+                  r.row_updates == updates,
+              "agent row of the mixed push differs (step " + std::to_string(step) + ", table " +
+                  std::to_string(defs[t].id) + ", key " + std::to_string(r.row.key) + ")");
+      }
+    }
+  }
+  Check(compact_sends > 0 && expanded_sends > 0, "the service's packet choice took only one form");
+  for (auto* s : truth) eps_or_destroy(s);
+  for (auto* s : cpu) eps_or_destroy(s);
+}
+
+// GatherDevice and PushDevice at the occurrence count of the 4 x 12.5M x 128
+// workload: 4 mean features of 262,144 bags x 32 ids (33.5 M occurrences),
+// Zipf(1.1) ids over 60,000 keys per table, of which this agent holds the
+// first 50,000 (the rest are served elsewhere: holes).  Every occurrence is
+// resolved to its slot on the device.  Checked against the oracle on 1,024
+// sampled bags of each feature (pull) and, after the push, on the 16 hottest
+// and 240 random held rows of each table (the oracle reduces every occurrence
+// of those keys, in order, with the full bags' mean scales).
+void LargeOccurrences() {
+  constexpr std::uint32_t kDim = 128, kBags = 262144, kLen = 32, kTables = 4;
+  constexpr Key kHeld = 50000, kIds = 60000;
+  HipCacheOptions o = SmallOptions(65536);
+  o.state_bytes = 8ull << 30;
+  o.transfer_bytes = 1ull << 30;
+  o.outstanding_output_bytes = 1ull << 30;
+  HipCacheBackend gpu(o);
+  std::vector<double> cdf(kIds);
+  double total = 0;
+  for (Key r = 0; r < kIds; ++r) cdf[r] = total += std::pow(double(r + 1), -1.1);
+  std::uint64_t state = 4;
+  auto next = [&]() {
+    state += 0x9e3779b97f4a7c15ull;
+    std::uint64_t z = state;
+    z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+    z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+    return z ^ (z >> 31);
+  };
+  std::vector<TableDefinition> defs;
+  std::map<std::pair<TableId, Key>, RowState> model;
+  std::map<std::pair<TableId, Key>, LocatedRow> where;
+  std::vector<FeatureInput> layouts;
+  std::vector<AgentWork> work;
+  std::vector<std::vector<float>> grads;
+  for (std::uint32_t t = 0; t < kTables; ++t) {
+    defs.push_back(Table(40 + t, kDim));
+    Take(gpu.Define(defs.back()));
+    for (Key b = 0; b < kHeld; b += 10000) {
+      std::vector<RowState> part;
+      for (Key k = b; k < b + 10000; ++k) part.push_back(model[{40 + t, k}] = MakeRow(40 + t, k, kDim));
+      for (const auto& loc : Take(gpu.Load(Plan(part), part))) where[{loc.row.table, loc.row.key}] = loc;
+    }
+    FeatureInput f{40 + t, t, Pooling::mean, std::vector<Key>(std::uint64_t(kBags) * kLen), {}, {}};
+    f.offsets.resize(kBags + 1);
+    f.valid_lengths.assign(kBags, kLen);
+    for (std::uint64_t b = 0; b <= kBags; ++b) f.offsets[b] = b * kLen;
+    // Rank -> key through a fixed odd multiplier, so the hot keys are spread.
+    for (auto& k : f.keys) {
+      const double u = double(next() >> 11) * 0x1.0p-53 * total;
+      const Key rank = Key(std::lower_bound(cdf.begin(), cdf.end(), u) - cdf.begin());
+      k = (std::min(rank, kIds - 1) * 7919 + 13) % kIds;
+    }
+    AgentWork w{t, AccessRoute::resident_gpu, 0, {}, std::vector<std::uint64_t>(f.keys.size()), {}};
+    std::vector<std::uint64_t> unique(kIds, UINT64_MAX);
+    for (std::size_t i = 0; i < f.keys.size(); ++i) {
+      const Key k = f.keys[i];
+      if (k >= kHeld) {
+        w.occurrence_to_unique[i] = UINT64_MAX;
+        continue;
+      }
+      if (unique[k] == UINT64_MAX) {
+        unique[k] = w.rows.size();
+        w.rows.push_back(where.at({40 + t, k}));
+      }
+      w.occurrence_to_unique[i] = unique[k];
+    }
+    std::vector<float> g(std::uint64_t(kBags) * kDim);
+    for (auto& x : g) x = float(std::int64_t(next() % 2001) - 1000) * 1e-5f;
+    layouts.push_back(std::move(f));
+    work.push_back(std::move(w));
+    grads.push_back(std::move(g));
+  }
+  auto pulled = Take(gpu.GatherDevice(work, layouts));
+  for (std::uint32_t t = 0; t < kTables; ++t) {
+    const FeatureInput& f = layouts[t];
+    const std::vector<float> got = pulled[t].tensor->CopyToHost();
+    Check(pulled[t].shape == std::vector<std::uint64_t>{kBags, kDim}, "large pull shape");
+    for (int s = 0; s < 1024; ++s) {
+      const std::uint64_t b = next() % kBags;
+      std::vector<float> want(kDim, 0.f);
+      for (std::uint64_t i = f.offsets[b]; i < f.offsets[b + 1]; ++i) {
+        if (f.keys[i] >= kHeld) continue;
+        const auto& w = model.at({40 + t, f.keys[i]}).weights;
+        for (std::uint32_t d = 0; d < kDim; ++d) want[d] = want[d] + w[d];
+      }
+      Check(std::memcmp(want.data(), got.data() + b * kDim, kDim * 4) == 0,
+            "large pull bag differs (table " + std::to_string(t) + ", bag " + std::to_string(b) + ")");
+    }
+  }
+  std::vector<UpdateContext> contexts;
+  std::vector<DeviceTensorBlock> blocks;
+  for (std::uint32_t t = 0; t < kTables; ++t) {
+    contexts.push_back({{"large", 0, 1, Phase::push}, 0, 40 + t, 0, kLr, 0.9f, 0.999f});
+    blocks.push_back({t, {kBags, kDim}, std::make_shared<DeviceBuffer>(grads[t])});
+  }
+  Take(gpu.PushDevice(contexts, work, layouts, blocks));
+  for (std::uint32_t t = 0; t < kTables; ++t) {
+    const FeatureInput& f = layouts[t];
+    std::vector<std::uint64_t> counts(kHeld, 0);
+    for (Key k : f.keys)
+      if (k < kHeld) ++counts[k];
+    std::vector<Key> by_count;
+    for (Key k = 0; k < kHeld; ++k)
+      if (counts[k]) by_count.push_back(k);
+    std::sort(by_count.begin(), by_count.end(), [&](Key a, Key b) { return counts[a] > counts[b]; });
+    std::set<Key> sample(by_count.begin(), by_count.begin() + 16);
+    while (sample.size() < 256) sample.insert(by_count[next() % by_count.size()]);
+    const FeatureInput part = Restrict(f, [&](Key k) { return sample.count(k) > 0; });
+    eps_or_table_def def = OracleDef(defs[t]);
+    eps_or_store* store = eps_or_create(&def);
+    const eps_or_feature of = AsOracle(part);
+    const float* og = grads[t].data();
+    std::vector<std::uint64_t> keys(part.keys.size() + 1);
+    std::vector<float> values((part.keys.size() + 1) * kDim);
+    std::uint64_t count = 0;
+    Check(eps_or_reduce_gradients(store, &of, &og, 1, keys.data(), values.data(), &count) == 0 && count == sample.size(),
+          "oracle reduce (large)");
+    eps_or_destroy(store);
+    MigrationPlan read{"read", 0, {}, Placement::cpu, 0};
+    for (std::uint64_t u = 0; u < count; ++u) {
+      RowState& r = model.at({40 + t, keys[u]});
+      Check(eps_or_adam_rows_ctx(r.weights.data(), r.first_moment.data(), r.second_moment.data(),
+                                 values.data() + u * kDim, 1, kDim, kBeta1, kBeta2, kEps, kLr, 0.9f, 0.999f, 0, 0, 0) == 0,
+            "oracle Adam (large)");
+      ++r.row_updates;
+      read.rows.push_back(where.at({40 + t, keys[u]}));
+    }
+    for (const auto& got : Take(gpu.ReadBack(read))) {
+      const RowState& want = model.at({got.row.table, got.row.key});
+      Check(SameBits(got.weights, want.weights) && SameBits(got.first_moment, want.first_moment) &&
+                SameBits(got.second_moment, want.second_moment) && got.row_updates == want.row_updates,
+            "large push row differs (table " + std::to_string(t) + ", key " + std::to_string(got.row.key) + ", " +
+                std::to_string(counts[got.row.key]) + " references)");
+    }
+  }
+}
+
 void Main() {
   AtomicReserve();
   SnapshotWriteback();
   DevicePushAtScale();
+  MixedPush();
+  LargeOccurrences();
   auto gpu = std::make_shared<HipCacheBackend>(SmallOptions(8));
   for (const auto& t : {Table(1, 128), Table(2, 64)}) Take(gpu->Define(t));
   Take(gpu->Define(Table(1, 128)));  // identical redefinition is accepted

@@ -5,7 +5,12 @@
 // content; the oracle's restatement of the reference's WriteSnapshot
 // (src/store/snapshot.cpp:159-194) writes the same content; the files must be
 // byte-identical.  Publication: an existing file is never replaced, and no
-// staging file is left behind on success or failure.  No GPU is used.
+// staging file is left behind on success or failure.  The reader that
+// HipCacheBackend::RestoreSnapshot streams files through (snapshot_reader.hpp)
+// reads that file back to the oracle's rows and clocks, reads the reference's
+// own format-1 fixture (tests/fixtures/snapshot-v1-unbounded.bin, copied to
+// tests/golden/), and refuses a flipped byte, a truncation and trailing bytes
+// as the reference's ReadSnapshot does.  No GPU is used.
 #include <unistd.h>
 
 #include <cmath>
@@ -17,6 +22,7 @@
 #include <vector>
 
 #include "eps_oracle.h"
+#include "snapshot_reader.hpp"
 #include "snapshot_writer.hpp"
 
 using namespace eps;
@@ -84,14 +90,14 @@ int main() {
     const auto ours = dir / "ours" / "shard-1.bin";
     std::uint64_t checksum = 0;
     {
-      hip_detail::SnapshotWriter out(ours);
-      hip_detail::WriteSnapshotHeader(out, id, tables.size());
+      hipbk::SnapshotWriter out(ours);
+      hipbk::WriteSnapshotHeader(out, id, tables.size());
       for (const auto& t : tables) {
         SnapshotTable st{t.definition, 0, 0, 0, {}};
         eps_or_powers(t.store, &st.beta1_power, &st.beta2_power, &st.optimizer_sequence);
         const std::uint64_t rows = eps_or_row_count(t.store);
         for (std::uint64_t r = 0; r < rows; ++r) st.keys.push_back(eps_or_key_at(t.store, r));
-        hip_detail::WriteSnapshotTable(out, st);
+        hipbk::WriteSnapshotTable(out, st);
         std::vector<float> wmv(3 * t.def.dim);
         for (std::size_t i = 0; i < st.keys.size(); ++i) {
           std::uint64_t updates = 0;
@@ -99,12 +105,12 @@ int main() {
                             wmv.data() + 2 * t.def.dim, &updates) == 0,
                 "oracle read");
           if (i % 2) {
-            hip_detail::WriteSnapshotRow(out, st.keys[i], updates, wmv.data(), t.def.dim);
+            hipbk::WriteSnapshotRow(out, st.keys[i], updates, wmv.data(), t.def.dim);
           } else {  // the CPU-store form of a row
             RowState row{{t.def.id, st.keys[i]}, {wmv.begin(), wmv.begin() + t.def.dim},
                          {wmv.begin() + t.def.dim, wmv.begin() + 2 * t.def.dim},
                          {wmv.begin() + 2 * t.def.dim, wmv.end()}, updates};
-            hip_detail::WriteSnapshotRow(out, row);
+            hipbk::WriteSnapshotRow(out, row);
           }
         }
       }
@@ -116,6 +122,78 @@ int main() {
     Check(eps_or_snapshot_write(theirs.c_str(), "format-run", 1, 3, 7, both, 2) == 0, "oracle writer");
     Check(Bytes(ours) == Bytes(theirs), "encoder bytes differ from the oracle writer's");
     const std::string data = Bytes(ours);
+
+    // The reader gives back every table clock and row of the stores.
+    {
+      hipbk::SnapshotReader in(ours);
+      Check(in.version == 2 && in.run == id.run && in.shard == 1 && in.shard_count == 3 && in.epoch == 7 &&
+                in.tables == 2,
+            "reader identity");
+      for (const auto& t : tables) {
+        const auto header = in.NextTable();
+        float b1 = 0, b2 = 0;
+        std::uint64_t seq = 0;
+        eps_or_powers(t.store, &b1, &b2, &seq);
+        Check(header.definition == t.definition && header.optimizer_sequence == seq && header.beta1_power == b1 &&
+                  header.beta2_power == b2 && header.rows == eps_or_row_count(t.store),
+              "reader table header");
+        std::vector<float> got(3 * t.def.dim), want(3 * t.def.dim);
+        for (std::uint64_t r = 0; r < header.rows; ++r) {
+          Key key = 0;
+          std::uint64_t updates = 0, want_updates = 0;
+          in.Row(t.def.dim, key, updates, got.data());
+          Check(key == eps_or_key_at(t.store, r), "reader row order");
+          Check(eps_or_read(t.store, key, want.data(), want.data() + t.def.dim, want.data() + 2 * t.def.dim,
+                            &want_updates) == 0 &&
+                    got == want && updates == want_updates,
+                "reader row");
+        }
+      }
+      in.Finish();
+    }
+    // The reference's format-1 fixture: run "legacy-unbounded", one row
+    // [0.25, 0.25 | 0, 0 | 0, 0] (tests/fixtures/README.md of the reference).
+    {
+      const auto fixture = std::filesystem::canonical("/proc/self/exe").parent_path() / ".." / ".." / "golden" /
+                           "snapshot-v1-unbounded.bin";
+      hipbk::SnapshotReader in(fixture);
+      Check(in.version == 1 && in.run == "legacy-unbounded" && in.tables == 1, "fixture identity");
+      const auto header = in.NextTable();
+      Check(header.rows == 1 && header.definition.dimension == 2 && !header.definition.optimizer.weight_bounds,
+            "fixture table");
+      std::vector<float> wmv(6);
+      Key key = 0;
+      std::uint64_t updates = 0;
+      in.Row(2, key, updates, wmv.data());
+      Check(wmv == std::vector<float>{0.25f, 0.25f, 0, 0, 0, 0}, "fixture row");
+      in.Finish();
+    }
+    // Damaged files are refused: a flipped byte, a truncation, trailing bytes.
+    auto refuses = [&](const std::string& bytes, Error::Code code, const char* what) {
+      const auto bad = dir / "damaged.bin";
+      std::filesystem::remove(bad);
+      std::ofstream(bad, std::ios::binary) << bytes;
+      bool refused = false;
+      try {
+        hipbk::SnapshotReader in(bad);
+        for (std::uint64_t t = 0; t < in.tables; ++t) {
+          const auto header = in.NextTable();
+          std::vector<float> wmv(3 * header.definition.dimension);
+          Key key;
+          std::uint64_t updates;
+          for (std::uint64_t r = 0; r < header.rows; ++r) in.Row(header.definition.dimension, key, updates, wmv.data());
+        }
+        in.Finish();
+      } catch (const hipbk::Fault& e) {
+        refused = e.error.code == code;
+      }
+      Check(refused, what);
+    };
+    std::string flipped = data;
+    flipped[data.size() / 2] ^= 0x10;
+    refuses(flipped, Error::Code::invalid_argument, "a flipped byte was accepted");
+    refuses(data.substr(0, data.size() - 3), Error::Code::unavailable, "a truncated snapshot was accepted");
+    refuses(data + "x", Error::Code::invalid_argument, "trailing bytes were accepted");
     Check(eps_or_fnv1a(14695981039346656037ull, data.data(), data.size() - 8) == checksum,
           "returned checksum");
     Check(!std::filesystem::exists(ours.string() + ".pending"), "staging file left after publish");
@@ -123,16 +201,16 @@ int main() {
     // A published file is never replaced; the refused attempt leaves no staging file.
     bool refused = false;
     try {
-      hip_detail::SnapshotWriter again(ours);
+      hipbk::SnapshotWriter again(ours);
       again.U64(1);
       again.Publish();
-    } catch (const hip_detail::Failure& e) {
-      refused = e.error().code == Error::Code::unavailable;
+    } catch (const hipbk::Fault& e) {
+      refused = e.error.code == Error::Code::unavailable;
     }
     Check(refused && Bytes(ours) == data && !std::filesystem::exists(ours.string() + ".pending"),
           "an existing snapshot was replaced");
     // A writer dropped before publication removes its staging file.
-    { hip_detail::SnapshotWriter dropped(dir / "dropped.bin"); dropped.U64(5); }
+    { hipbk::SnapshotWriter dropped(dir / "dropped.bin"); dropped.U64(5); }
     Check(!std::filesystem::exists(dir / "dropped.bin") &&
               !std::filesystem::exists((dir / "dropped.bin").string() + ".pending"),
           "unpublished snapshot left files");
