@@ -89,9 +89,10 @@ struct PushLayout {
   uint64_t hist, look, group_look, keys_a, keys_b, vals_a, vals_b, refscale, sorted_rs, flags,
       ranks, block_sums, long_list, total;
   // Capacity of each hot-row list (any one may hold every hot row).
-  uint64_t HotCapacity() const { return n / kLongRefs + 1; }
-  explicit PushLayout(uint64_t occurrences) {
-    n = occurrences;
+  constexpr uint64_t HotCapacity() const { return n / kLongRefs + 1; }
+  constexpr explicit PushLayout(uint64_t occurrences)
+      : n(occurrences), tiles(0), groups(0), hist(0), look(0), group_look(0), keys_a(0), keys_b(0), vals_a(0),
+        vals_b(0), refscale(0), sorted_rs(0), flags(0), ranks(0), block_sums(0), long_list(0), total(0) {
     tiles = (n + kSortTile - 1) / kSortTile;
     groups = (tiles + kGroupTiles - 1) / kGroupTiles;
     auto align = [](uint64_t x) { return (x + 255) & ~uint64_t(255); };

@@ -600,15 +600,13 @@ int PlanPush(const eps_hip_table* tables, uint32_t table_count,
   }
   plan.row_bits = std::max<uint32_t>(1, BitLength(max_rows - 1));
   // Table key indices ordered by dimension class, so each class is one
-  // contiguous range of the sorted keys.
-  std::vector<uint32_t> order(table_count);
-  for (uint32_t t = 0; t < table_count; ++t) order[t] = t;
-  std::stable_sort(order.begin(), order.end(), [&](uint32_t a, uint32_t b) {
-    return DimClass(tables[a].dim) < DimClass(tables[b].dim);
-  });
-  plan.key_index.assign(table_count, 0);
-  plan.table_of_key = order;
-  for (uint32_t k = 0; k < table_count; ++k) plan.key_index[order[k]] = k;
+  // contiguous range of the sorted keys (tables of a class in call order).
+  uint32_t keyed = 0;
+  for (uint32_t c = 0; c < kClasses; ++c)
+    for (uint32_t t = 0; t < table_count; ++t)
+      if (DimClass(tables[t].dim) == c) plan.table_of_key[keyed++] = t;
+  for (uint32_t i = 0; i < table_count; ++i) plan.key_index[plan.table_of_key[i]] = i;
+  const auto& order = plan.table_of_key;
   for (uint32_t c = 0; c <= kClasses; ++c) {
     uint32_t k = 0;
     while (k < table_count && DimClass(tables[order[k]].dim) < c) ++k;

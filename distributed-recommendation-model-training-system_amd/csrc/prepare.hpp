@@ -1,7 +1,6 @@
 // prepare.hpp -- host-side description of a push shared by prepare.hip and adam.hip.
 #pragma once
 #include <array>
-#include <vector>
 
 #include "common.hpp"
 
@@ -26,8 +25,9 @@ struct PushPlan {
   uint64_t occurrences = 0;           // total over features (holes included)
   uint32_t row_bits = 0, key_bits = 0, passes = 0;
   std::array<uint32_t, kMaxPasses> shift{}, bits{};
-  std::vector<uint32_t> key_index;    // call table index -> key index (class order)
-  std::vector<uint32_t> table_of_key; // key index -> call table index
+  // Fixed-size, so planning a push allocates nothing.
+  std::array<uint32_t, EPS_HIP_MAX_TABLES> key_index{};    // call table index -> key index (class order)
+  std::array<uint32_t, EPS_HIP_MAX_TABLES> table_of_key{}; // key index -> call table index
   std::array<uint32_t, kClasses + 1> class_start{};  // first key index of each class
   std::array<uint64_t, kClasses> class_occurrences{};  // upper bound of sorted positions
 };

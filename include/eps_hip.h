@@ -12,7 +12,8 @@
  *   - enqueues work on that stream and returns without synchronising, except
  *     eps_hip_read_status which waits for the stream;
  *   - never allocates device memory: scratch space is a caller-provided
- *     workspace sized by the matching *_workspace_bytes query.
+ *     workspace sized by the matching *_workspace_bytes query (or, for
+ *     eps_hip_push_static, a static array of the library).
  * Data-dependent outcomes (out-of-range row slots, non-finite gradients,
  * optimizer overflow) are reported in a device status word of the workspace,
  * read with eps_hip_read_status after the stream has drained.
@@ -240,6 +241,22 @@ int eps_hip_reduce(const eps_hip_table* tables, uint32_t table_count,
                    void* workspace, uint64_t workspace_bytes,
                    const uint64_t* occurrence_to_unique, float* values,
                    uint64_t row_stride, void* stream);
+
+/* A device push that allocates nothing.  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops).  Same as eps_hip_prepare + eps_hip_push on
+ * the same arguments, with the push workspace in a static device array of this
+ * library (about 12 MB per GPU, held from the library's load until the process
+ * ends) instead of a caller's buffer; pushes of more than
+ * EPS_HIP_STATIC_MAX_OCCURRENCES occurrences are refused with
+ * EPS_HIP_CAPACITY_EXCEEDED before anything is enqueued.  `status` (device
+ * memory, 2 u32, may be NULL) receives the push's status word and the array's
+ * status history once the push has run.  Every call on one GPU shares that
+ * GPU's array: calls that overlap on one GPU race. */
+#define EPS_HIP_STATIC_MAX_OCCURRENCES 262144u
+int eps_hip_push_static(const eps_hip_table* tables, const eps_hip_optimizer* optimizers,
+                        uint32_t table_count, const eps_hip_push_feature* features,
+                        uint32_t feature_count, void* bounds, uint32_t* status, void* stream);
 
 /* ---- backend updates with host-built layouts ---- */
 uint64_t eps_hip_update_workspace_bytes(void);
