@@ -27,6 +27,7 @@
 // or an out-of-range slot rejects the whole update before anything is written.
 #include "prepare.hpp"
 
+#include <algorithm>
 #include <atomic>
 #include <cfloat>
 #include <cmath>
@@ -1145,6 +1146,38 @@ uint64_t SpanBlocks(uint64_t count) {
   return (count + per - 1) / per;
 }
 
+// The hot-row kernel's side stream and fork/join events, per calling thread
+// and device (created on first use, default priority, never destroyed), so
+// concurrent callers never share an event.
+struct Overlap {
+  hipStream_t side = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+};
+int ThreadOverlap(Overlap** out) {
+  constexpr int kDevices = 64;
+  thread_local Overlap per_device[kDevices];
+  int device = 0;
+  EPS_HIP_TRY(Check(hipGetDevice(&device), "hipGetDevice"));
+  if (device < 0 || device >= kDevices) return Fail(EPS_HIP_UNAVAILABLE, "device ordinal out of range");
+  Overlap& o = per_device[device];
+  if (!o.side) {
+    EPS_HIP_TRY(Check(hipStreamCreateWithFlags(&o.side, hipStreamNonBlocking), "hot-row stream"));
+    EPS_HIP_TRY(Check(hipEventCreateWithFlags(&o.fork, hipEventDisableTiming), "hot-row fork event"));
+    EPS_HIP_TRY(Check(hipEventCreateWithFlags(&o.join, hipEventDisableTiming), "hot-row join event"));
+  }
+  *out = &o;
+  return EPS_HIP_OK;
+}
+
+// The hot-row kernel runs beside the row kernels (on the side stream) when
+// some table takes at least this many references in the push: its hottest
+// rows then hold serial chains long enough to keep the whole push waiting
+// (measured on MI355X: 65,536 pairs on one table, 167 -> 133 us a push; 4 x
+// 8.4 M references, 13.4 -> 11.6 ms).  With many tables of fewer references
+// each, the row kernels lose more occupancy beside it than they gain (26
+// tables of ~43,000: 283 -> 321 us), so they run after it.
+constexpr uint64_t kOverlapTableRefs = 1ull << 16;
+
 std::atomic<uint32_t> g_spin_limit{1u << 22};
 uint32_t SpinLimit() { return g_spin_limit.load(std::memory_order_relaxed); }
 
@@ -1198,6 +1231,8 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
   a.gs = GuardScalars{0, table_count};  // refs: the prepared valid count
   // The first kernel of the primary phase makes the guard decision.
   uint32_t role = kDecide;
+  bool overlap = false;  // hot rows on the side stream, joined before the checked apply
+  Overlap* ov = nullptr;
   for (uint32_t k = 0; k < table_count; ++k) {
     const uint32_t t = plan.table_of_key[k];
     eps_hip_optimizer o{};
@@ -1231,17 +1266,32 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
     uint64_t vector_occurrences = 0;
     for (uint32_t cls = 0; cls + 1 < kClasses; ++cls) vector_occurrences += plan.class_occurrences[cls];
     const uint64_t hot_units = (vector_occurrences / (kLongRefs + 1)) << va.slice_bits;
+    uint64_t table_refs[EPS_HIP_MAX_TABLES] = {};
+    for (uint32_t f = 0; f < feature_count; ++f) table_refs[features[f].table] += features[f].occurrences;
+    overlap = hot_units && *std::max_element(table_refs, table_refs + table_count) >= kOverlapTableRefs;
     if (phases & kPrimary) {
       // Grids are multiples of kXcds (the kernels split their work by XCD).
       auto xcd_grid = [](uint64_t b) { return (b + kXcds - 1) / kXcds * kXcds; };
       // Hot rows first, then the row runs of each class, in stream order: the
       // two run at full occupancy one after the other (side by side they
       // compete for the same registers and bandwidth and finish later).
+      // Pushes with very long hot rows run the hot-row kernel beside the row
+      // kernels instead: a few serial chains of up to a million references
+      // then no longer keep the rest of the push waiting.  Both sides make the
+      // guard decision themselves (they read the same inputs and decide the same).
       if (hot_units) {
         const uint64_t blocks = xcd_grid(std::min<uint64_t>(hot_units, kHotGrid));
         va.role = role;
-        EPS_HIP_TRY(LaunchVectorUpdate(0, true, unsigned(blocks), va, s));
-        role = kFollow;
+        if (overlap) {
+          EPS_HIP_TRY(ThreadOverlap(&ov));
+          EPS_HIP_TRY(Check(hipEventRecord(ov->fork, s), "hot-row fork"));
+          EPS_HIP_TRY(Check(hipStreamWaitEvent(ov->side, ov->fork, 0), "hot-row fork wait"));
+          EPS_HIP_TRY(LaunchVectorUpdate(0, true, unsigned(blocks), va, ov->side));
+          EPS_HIP_TRY(Check(hipEventRecord(ov->join, ov->side), "hot-row join"));
+        } else {
+          EPS_HIP_TRY(LaunchVectorUpdate(0, true, unsigned(blocks), va, s));
+          role = kFollow;
+        }
       }
       for (uint32_t cls = 0; cls + 1 < kClasses; ++cls) {
         if (!plan.class_occurrences[cls]) continue;
@@ -1272,6 +1322,7 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
       EPS_HIP_LAUNCHED("sorted update");
     }
   }
+  if (overlap && (phases & kPrimary)) EPS_HIP_TRY(Check(hipStreamWaitEvent(s, ov->join, 0), "hot-row join wait"));
   // The checked apply (after a validate-only pass) is one launch over every
   // class, one wavefront per row: it usually exits at once, and when it runs
   // it adds each row's references in the same order as the passes above.

@@ -56,6 +56,11 @@ class GatherPart(C.Structure):
                 ("pooling", C.c_uint32)]
 
 
+class RowBatch(C.Structure):
+    _fields_ = [("state", C.c_void_p), ("slots", C.c_void_p), ("packed", C.c_void_p), ("count", C.c_uint64),
+                ("dim", C.c_uint32), ("reserved", C.c_uint32)]
+
+
 class PushFeature(C.Structure):
     _fields_ = [("indices", C.c_void_p), ("offsets", C.c_void_p), ("valid_lengths", C.c_void_p),
                 ("weights", C.c_void_p), ("gradients", C.c_void_p), ("occurrences", C.c_uint64),
@@ -74,6 +79,7 @@ SYMBOLS = {
     "eps_hip_scatter_rows": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p,
                                        C.c_void_p]),
     "eps_hip_gather_rows": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p]),
+    "eps_hip_move_rows": (C.c_int, [C.c_void_p, C.c_uint32, C.c_int32, C.c_void_p, C.c_void_p]),
     "eps_hip_index_bytes": (C.c_uint64, [C.c_uint64]),
     "eps_hip_index_clear": (C.c_int, [C.c_void_p, C.c_uint64, C.c_void_p]),
     "eps_hip_index_insert": (C.c_int, [C.c_void_p, C.c_uint64, C.c_void_p, C.c_void_p, C.c_uint64, C.c_void_p,
@@ -265,6 +271,18 @@ class DeviceShard:
         check(lib().eps_hip_gather_rows(C.byref(self.tables[table]), _ptr(slots), _ptr(out),
                                         slots.numel(), _stream(self.torch, stream)))
         return out
+
+    def row_batches(self, parts):
+        """ctypes array of RowBatch for [(table, slots tensor, packed tensor), ...]."""
+        return (RowBatch * len(parts))(*[RowBatch(_ptr(self.state[t]), _ptr(slots), _ptr(packed), slots.numel(),
+                                                  self.specs[t].dim, 0) for t, slots, packed in parts])
+
+    def move_rows(self, batches, write_back, stream=None, bounds=True):
+        """Admit (write_back False) or write back the rows of a row_batches()
+        array.  bounds=False: an admission of values the bounds domain already
+        covers (rows this shard wrote back, unchanged) leaves it alone."""
+        check(lib().eps_hip_move_rows(batches, len(batches), 1 if write_back else 0,
+                                      _ptr(self.bounds) if bounds else None, _stream(self.torch, stream)))
 
     def optimizer(self, table):
         s = self.specs[table]

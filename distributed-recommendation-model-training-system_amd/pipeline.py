@@ -87,19 +87,25 @@ class TierMoves:
 
     Batch j (of a cycle) admits the rows `admissions[j]` (per table, see
     workloads.Ragged8.admissions): their packed [w | m | v] come from pinned
-    host memory and are scattered into their slots before the pull.  After the
-    push, the rows that batch j + lag admits are gathered out of their slots
-    and written back to pinned host memory.  The host link carries both
-    directions on two copy streams, overlapped with the steps:
+    host memory and land in their slots before the pull.  After the push, the
+    rows that batch j + lag admits are written back to pinned host memory.
+    One batched kernel per direction moves every table's rows straight between
+    the slots and the pinned buffers (it reads or writes host memory over the
+    host link itself: on this system a runtime copy of a pinned buffer costs
+    ~0.5 ms of host time a call).  Each direction has its own stream, so the
+    link carries both at once, and both overlap the steps:
 
-      * the write-back of step k is copied device -> host after step k;
-      * the admission of step k + 1 is copied host -> device (into one of two
-        device staging buffers) while step k runs; it is the write-back of step
-        k + 1 - lag, so it never waits for the step in flight.
+      * step k + 1's admission runs during step k (its rows are not touched by
+        step k: admissions avoid the rows of the previous lag - 1 batches);
+      * step k's write-back runs during step k + 1 (its rows are not touched
+        before their admission, lag steps later).
 
-    Row state between a write-back and its admission lives only in host
-    memory: `poison` (tests) overwrites the written-back slots so an admission
-    that did not happen cannot go unseen.
+    Re-admitted rows carry values this shard wrote back earlier, unchanged,
+    which the bounds domain already covers (it never decreases), so the
+    admissions leave it alone (a push's guard decision may be reading it
+    meanwhile).  Row state between a write-back and its admission lives only
+    in host memory: `poison` (tests) overwrites the written-back slots so an
+    admission that did not happen cannot go unseen.
     """
 
     def __init__(self, torch, shard, admissions, lag, poison=False):
@@ -117,86 +123,70 @@ class TierMoves:
         dev, f32 = "cuda", torch.float32
         self.slots = [[torch.from_numpy(np.ascontiguousarray(a).view(np.int64)).to(dev) for a in adm]
                       for adm in admissions]
-        self.adm_staging = [torch.empty(total, dtype=f32, device=dev) for _ in range(2)]
-        self.wb_staging = [torch.empty(total, dtype=f32, device=dev) for _ in range(2)]
-        # Host copy of the rows batch j admits, for j in flight (written back lag steps before).
+        # Host copy of the rows batch j admits (written back lag steps before).
         self.host = [torch.empty(total, dtype=f32, pin_memory=True) for _ in range(lag + 1)]
-        self.h2d, self.d2h = torch.cuda.Stream(), torch.cuda.Stream()
-        ev = torch.cuda.Event
-        self.staged = {}      # step -> admission copied to the device
-        self.scattered = {}   # step -> admission scattered (staging free again)
-        self.copied_out = {}  # step -> write-back in host memory
+        self.inbound, self.outbound = torch.cuda.Stream(), torch.cuda.Stream()
         self.stream = torch.cuda.current_stream()
-        self._ev = ev
-        self._poison_rows = None
+        self._tables = [t for t, c in enumerate(self.counts) if c]
+        self._args = {}  # (cycle batch, host buffer) -> batched move arguments
+        ring = 8  # events are reused round robin (a wait uses the latest record)
+        self._ev = {n: [torch.cuda.Event() for _ in range(ring)] for n in ("admitted", "pushed", "written")}
+        self._ring = ring
+        self._poison_args = None
         if poison:
             self._poison_rows = torch.full((total,), 7.0, dtype=f32, device=dev)
+            self._poison_args = {j: shard.row_batches([(t, self.slots[j][t], self._parts(self._poison_rows)[t])
+                                                       for t in self._tables]) for j in range(self.period)}
+
+    def _e(self, name, k):
+        return self._ev[name][k % self._ring]
 
     def _parts(self, buf):
         return [buf[int(self.offset[t]):int(self.offset[t + 1])] for t in range(len(self.counts))]
 
+    def _batches(self, j):
+        """Moves of the rows batch j admits, to or from host buffer j % (lag + 1)."""
+        key = (j % self.period, j % (self.lag + 1))
+        if key not in self._args:
+            host = self._parts(self.host[key[1]])
+            self._args[key] = self.shard.row_batches([(t, self.slots[key[0]][t], host[t]) for t in self._tables])
+        return self._args[key]
+
+    def _poison_slots(self, j, stream):
+        if self._poison_args is not None:
+            self.shard.move_rows(self._poison_args[j % self.period], False, stream=stream, bounds=False)
+
+    def _admit(self, k):
+        """Step k's admission, on the inbound stream: its host copy was written
+        back at step k - lag."""
+        if k >= self.lag:
+            self.inbound.wait_event(self._e("written", k - self.lag))
+        self.shard.move_rows(self._batches(k), False, stream=self.inbound, bounds=False)
+        self._e("admitted", k).record(self.inbound)
+
     def prime(self):
         """Before step 0: the rows batches 0 .. lag-1 admit start in host memory
-        (their current device state is written back), then the admission of
-        step 0 is staged."""
+        (their current device state is written back), then step 0's admission
+        is issued."""
         for j in range(self.lag):
-            buf = self.wb_staging[0]
-            for t, part in enumerate(self._parts(buf)):
-                if self.counts[t]:
-                    self.shard.read_rows(t, self.slots[j % self.period][t], out=part, stream=self.stream)
-            self._poison_slots(j % self.period)
-            self.torch.cuda.synchronize()
-            self.host[j % (self.lag + 1)].copy_(buf)
-        self._stage(0)
-
-    def _poison_slots(self, j):
-        if self._poison_rows is None:
-            return
-        for t, part in enumerate(self._parts(self._poison_rows)):
-            if self.counts[t]:
-                self.shard.load_rows(t, self.slots[j][t], part, stream=self.stream)
-
-    def _stage(self, k):
-        """Host -> device copy of step k's admission (copy stream)."""
-        with self.torch.cuda.stream(self.h2d):
-            if k - 2 in self.scattered:
-                self.h2d.wait_event(self.scattered.pop(k - 2))  # staging k % 2 is free
-            if k - self.lag in self.copied_out:  # the host copy of this admission is written
-                self.h2d.wait_event(self.copied_out[k - self.lag])
-            self.adm_staging[k % 2].copy_(self.host[k % (self.lag + 1)], non_blocking=True)
-            e = self._ev()
-            e.record(self.h2d)
-            self.staged[k] = e
+            self.shard.move_rows(self._batches(j), True, stream=self.stream)
+            self._poison_slots(j, self.stream)
+        self.torch.cuda.synchronize()
+        self._admit(0)
 
     def admit(self, k):
-        """Step k, before its pull: scatter the staged rows into their slots,
-        then start staging step k + 1's admission."""
-        self.stream.wait_event(self.staged.pop(k))
-        for t, part in enumerate(self._parts(self.adm_staging[k % 2])):
-            if self.counts[t]:
-                self.shard.load_rows(t, self.slots[k % self.period][t], part, stream=self.stream)
-        e = self._ev()
-        e.record(self.stream)
-        self.scattered[k] = e
-        self._stage(k + 1)
+        """Step k, before its pull: wait for step k's admission."""
+        self.stream.wait_event(self._e("admitted", k))
 
     def write_back(self, k):
-        """Step k, after its push: gather the rows batch k + lag admits into
-        staging, then copy them to host memory (copy stream)."""
-        j = (k + self.lag) % self.period
-        if k - 2 in self.copied_out:  # write-back staging k % 2 is free once copied out
-            self.stream.wait_event(self.copied_out[k - 2])
-        buf = self.wb_staging[k % 2]
-        for t, part in enumerate(self._parts(buf)):
-            if self.counts[t]:
-                self.shard.read_rows(t, self.slots[j][t], out=part, stream=self.stream)
-        self._poison_slots(j)
-        e = self._ev()
-        e.record(self.stream)
-        with self.torch.cuda.stream(self.d2h):
-            self.d2h.wait_event(e)
-            self.host[(k + self.lag) % (self.lag + 1)].copy_(buf, non_blocking=True)
-            done = self._ev()
-            done.record(self.d2h)
-            self.copied_out[k] = done
-        self.copied_out.pop(k - self.lag - 2, None)  # no later step waits for it
+        """Step k, after its push: issue step k + 1's admission, then (after the
+        push) the write-back of the rows batch k + lag admits, into the host
+        buffer step k - 1's admission read."""
+        self._e("pushed", k).record(self.stream)
+        self._admit(k + 1)
+        self.outbound.wait_event(self._e("pushed", k))
+        if k >= 1:
+            self.outbound.wait_event(self._e("admitted", k - 1))
+        self.shard.move_rows(self._batches(k + self.lag), True, stream=self.outbound)
+        self._poison_slots(k + self.lag, self.outbound)
+        self._e("written", k).record(self.outbound)

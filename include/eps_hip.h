@@ -145,6 +145,23 @@ int eps_hip_scatter_rows(const eps_hip_table* table, const uint64_t* slots,
 int eps_hip_gather_rows(const eps_hip_table* table, const uint64_t* slots, float* packed,
                         uint64_t count, void* stream);
 
+/* Row moves of up to EPS_HIP_MAX_TABLES tables in one launch: the tier moves
+ * of a step (Load's ScatterState and ReadBack's ReadStateKernel,
+ * src/cuda/cache_backend.cu:69-80,390-585, once per table there).  With
+ * write_back 0, batch b's packed rows [w|m|v] go to its slots (bounds updated,
+ * as eps_hip_scatter_rows); with write_back 1, its slots' rows go to `packed`
+ * (as eps_hip_gather_rows).  `packed` may be device or pinned host memory. */
+typedef struct eps_hip_row_batch {
+  float* state;          /* the table's state (16-byte aligned) */
+  const uint64_t* slots; /* count slots */
+  float* packed;         /* count x 3 x dim floats */
+  uint64_t count;
+  uint32_t dim;
+  uint32_t reserved;
+} eps_hip_row_batch;
+int eps_hip_move_rows(const eps_hip_row_batch* batches, uint32_t count, int32_t write_back,
+                      void* bounds, void* stream);
+
 /* ---- device key -> slot index of a table ---- */
 /* The reference keeps a host hash map per table (CudaCacheBackend's
  * Table::rows, src/cuda/cache_backend.cu:193-198) and looks every key
@@ -277,11 +294,13 @@ int eps_hip_adam_compact(const eps_hip_table* table, const eps_hip_optimizer* op
 /* ---- status ---- */
 /* Device address of the status word inside a push or update workspace.  A
  * call's status is complete once its last enqueued kernel has run (a push:
- * after eps_hip_push_end).  Any bit of 0x7f means the call failed: with every
- * bit but EPS_HIP_STATUS_STALLED set, nothing was written.  A stall (a hot-row
- * hand-over that exceeded its spin limit, which no correct run reaches)
- * leaves the hot rows whose work units completed before it updated and every
- * other row unchanged. */
+ * after eps_hip_push_end).  Any bit of 0x7f means the call failed; with any
+ * failure bit but EPS_HIP_STATUS_STALLED, nothing was written.  A stall (a
+ * hot-row hand-over that exceeded its spin limit, which no correct run
+ * reaches) writes none of the stalled work units' rows; rows of other work
+ * units of the same push may have been written (always so when the hot-row
+ * kernel ran beside the row kernels, as it does once a table takes 65,536 or
+ * more references), so the tables are to be restored, e.g. from a snapshot. */
 uint32_t* eps_hip_status_word(void* workspace);
 /* Device address of the workspace's status history: the OR of the failure
  * bits of every push or update run in it since it was zeroed (a workspace
