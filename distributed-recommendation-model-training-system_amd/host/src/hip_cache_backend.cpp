@@ -804,32 +804,32 @@ std::future<Result<std::vector<RowState>>> HipCacheBackend::ReadBack(MigrationPl
       by_table[plan.rows[i].row.table].push_back(i);
     }
     I.transfer.Reset();
-    struct Part {
+    struct TableRun {
       SlotTable* t;
       Transfer::Piece<std::uint64_t> slots;
       const std::vector<std::size_t>* members;
     };
-    std::vector<Part> parts;
+    std::vector<TableRun> runs;
     for (const auto& [id, members] : by_table) {
-      Part part{&I.Table(id), I.transfer.Take<std::uint64_t>(members.size()), &members};
-      for (std::size_t j = 0; j < members.size(); ++j) part.slots.host[j] = held[members[j]]->where.slot;
-      parts.push_back(part);
+      TableRun run{&I.Table(id), I.transfer.Take<std::uint64_t>(members.size()), &members};
+      for (std::size_t j = 0; j < members.size(); ++j) run.slots.host[j] = held[members[j]]->where.slot;
+      runs.push_back(run);
     }
     I.transfer.Upload(I.stream);
     std::vector<Transfer::Piece<float>> packed;
-    for (const Part& part : parts) packed.push_back(I.transfer.Take<float>(part.slots.count * 3ull * part.t->dim()));
+    for (const TableRun& run : runs) packed.push_back(I.transfer.Take<float>(run.slots.count * 3ull * run.t->dim()));
     I.transfer.Skip();
-    for (std::size_t k = 0; k < parts.size(); ++k) {
-      AbiOk(eps_hip_gather_rows(&parts[k].t->abi, parts[k].slots.device, packed[k].device, parts[k].slots.count,
+    for (std::size_t k = 0; k < runs.size(); ++k) {
+      AbiOk(eps_hip_gather_rows(&runs[k].t->abi, runs[k].slots.device, packed[k].device, runs[k].slots.count,
                                 I.stream));
       I.transfer.Download(packed[k], I.stream);
     }
     I.Await();
     std::vector<RowState> out(plan.rows.size());
-    for (std::size_t k = 0; k < parts.size(); ++k) {
-      const std::size_t dim = parts[k].t->dim();
-      for (std::size_t j = 0; j < parts[k].members->size(); ++j) {
-        const std::size_t i = (*parts[k].members)[j];
+    for (std::size_t k = 0; k < runs.size(); ++k) {
+      const std::size_t dim = runs[k].t->dim();
+      for (std::size_t j = 0; j < runs[k].members->size(); ++j) {
+        const std::size_t i = (*runs[k].members)[j];
         const float* src = packed[k].host + j * 3 * dim;
         out[i] = RowState{plan.rows[i].row, {src, src + dim}, {src + dim, src + 2 * dim}, {src + 2 * dim, src + 3 * dim},
                           held[i]->updates};

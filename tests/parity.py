@@ -3,7 +3,12 @@
 Floating-point results are held to the contract tolerance (1e-5 relative or
 1e-6 absolute per element) and their per-element ULP histogram is reported;
 integer results (slots, unique ids, occurrence maps) must be identical.
+With EPS_PARITY_REPORT set to a file path, every comparison also appends one
+JSON line (what, elements, histogram, worst ULP) to that file.
 """
+import json
+import os
+
 import numpy as np
 
 import oracle
@@ -29,6 +34,11 @@ def assert_close(got, want, what, strict_ulp=None):
     assert got.shape == want.shape, f"{what}: shape {got.shape} vs {want.shape}"
     hist, worst = ulp_histogram(got, want)
     print(f"{what}: ULP histogram {hist}")
+    report = os.environ.get("EPS_PARITY_REPORT")
+    if report:
+        with open(report, "a") as fh:
+            fh.write(json.dumps({"what": what, "elements": int(got.size), "ulp_histogram": hist,
+                                 "max_ulp": worst}) + "\n")
     ok = np.abs(got.astype(np.float64) - want) <= np.maximum(ATOL, RTOL * np.abs(want.astype(np.float64)))
     assert ok.all(), f"{what}: {int((~ok).sum())} elements outside 1e-5 rel / 1e-6 abs (max ULP {worst})"
     if strict_ulp is not None:

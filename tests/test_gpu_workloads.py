@@ -16,7 +16,9 @@ from parity import assert_close, expected_pull, oracle_store
 pytestmark = pytest.mark.gpu
 
 
-def run(torch, W, H, wl, steps, explicit_state=None, compare_every=1):
+def run(torch, W, H, wl, steps, explicit_state=None, compare_every=1, touched_only=False):
+    """`touched_only`: compare the rows the step touched at intermediate
+    compare steps (untouched rows change on neither side), every row at the end."""
     t0 = time.time()
     first = wl.batch(0)
     shard = H.DeviceShard(torch, wl.tables, max_occurrences=2 * sum(len(f.keys) for f in first))
@@ -48,6 +50,8 @@ def run(torch, W, H, wl, steps, explicit_state=None, compare_every=1):
         if step % compare_every == 0 or step == steps - 1:
             for t, s in enumerate(wl.tables):
                 keys = stores[t].keys()
+                if touched_only and step != steps - 1:
+                    keys = np.unique(np.concatenate([f.keys for f in feats if f.table == t]))
                 want, updates = stores[t].read_many(keys)
                 got = shard.read_rows(t, torch.from_numpy(keys.view(np.int64)).cuda()).cpu().numpy()
                 assert_close(got.reshape(want.shape), want, f"{wl.name} state step {step} table {t}",
@@ -71,14 +75,16 @@ def test_criteo26_full_size_step(torch_gpu, pkg):
 
 
 def test_dup10m_steps(torch_gpu, pkg):
-    """10,000,000 x 128, 65,536 pairs, Zipf(1.2) (about 82% duplicates), t = 1..3."""
+    """10,000,000 x 128, 65,536 pairs, Zipf(1.2) (about 82% duplicates), t = 1..50:
+    the pull and the step's touched rows every 5th step, and after the last step
+    all 247,234 rows the 50 steps touch."""
     W, H = pkg.workloads, pkg.eps_hip
     wl = W.Dup10M()
     feats = wl.batch(0)
     dup = 1 - len(np.unique(feats[0].keys)) / len(feats[0].keys)
     print(f"duplicate fraction {dup:.3f}")
     assert dup > 0.6
-    run(torch_gpu, W, H, wl, 3)
+    run(torch_gpu, W, H, wl, 50, compare_every=5, touched_only=True)
 
 
 def test_ragged8_weighted_steps(torch_gpu, pkg):

@@ -313,3 +313,28 @@ def test_reduce_first_occurrence_order_brute_force():
                 if keys[i] == k:
                     acc = (acc + (g[b] * scale).astype(F32)).astype(F32)
         assert np.array_equal(rv[u], acc)
+
+
+def test_mean_divide_closed_form():
+    """The client's mean (distributed_client.cpp:227-232): each value is
+    0.0f + partial, then divided by float(valid_length) when that is non-zero.
+    IEEE division is correctly rounded, so numpy's float32 quotient is the
+    closed form.  The cases fix the three ways to get it wrong: a reciprocal
+    multiply (values chosen where x * (1/len) rounds differently from x / len),
+    dividing an empty bag (len 0 leaves the value), and keeping -0.0 (the
+    +0.0f start turns it into +0.0)."""
+    x = np.array([[0.82161814, 0.3645724, 0.2941325, -1.3031572],
+                  [0.34558418, 0.82161814, 0.9053559, 5.0],
+                  [-0.0, 1.5, -2.25, 3.0e-38],
+                  [-0.0, 0.0, -7.0, 1.0e30]], np.float32)
+    lengths = np.array([3, 7, 0, 13], np.uint64)
+    got = oracle.mean_divide(x, lengths)
+    want = (np.float32(0.0) + x).astype(np.float32)
+    for b, n in enumerate(lengths):
+        if n:
+            want[b] = want[b] / np.float32(n)
+    assert got.tobytes() == want.tobytes()
+    recip = x[:2] * (np.float32(1) / lengths[:2, None].astype(np.float32))
+    assert np.any(recip != got[:2]), "the cases must separate divide from reciprocal multiply"
+    assert not np.signbit(got[2, 0]) and not np.signbit(got[3, 0])  # -0.0 comes out as +0.0
+    assert got[2, 1] == np.float32(1.5) and got[2, 3] == np.float32(3.0e-38)  # empty bag unchanged
