@@ -27,6 +27,12 @@ Adam rows/s, the step's algorithmic HBM bandwidth and its fraction of the
 its stream, every FUSED_EVERY-th timed step); `cpu_baseline` times the
 reference CPU shard (or the oracle's C restatement of it) on the host over a
 bounded sample, on one core and on the GPU's share of host cores.
+
+`--ceiling` instead measures what the memory system gives the fused update's
+access pattern (eps_hip_probe_row_rmw): the config's first batch's unique rows
+(sorted, one scratch table holding every table's rows) read and written back
+with one gradient row each, for several loads-in-flight and grid shapes, and
+the same count of consecutive rows; one JSON line per variant.
 """
 from __future__ import annotations
 
@@ -252,6 +258,61 @@ def progress(message):
     print(f"[bench] {message}", file=sys.stderr, flush=True)
 
 
+def ceiling(config):
+    """Row read-modify-write ceiling of a config with one dimension."""
+    import ctypes as C
+    import torch
+
+    cfg = CONFIGS[config]
+    pkg = package()
+    W, H = pkg.workloads, pkg.eps_hip
+    wl = make_workload(W, cfg["workload"])
+    dims = {t.dim for t in wl.tables}
+    if len(dims) != 1:
+        print(f"--ceiling needs one dimension; config {config} has {sorted(dims)}", file=sys.stderr)
+        return 2
+    dim = dims.pop()
+    base = np.concatenate([[0], np.cumsum([t.rows for t in wl.tables])]).astype(np.uint64)
+    batch = wl.batch(0)
+    slots = np.unique(np.concatenate([np.unique(f.keys) + base[f.table] for f in batch]))
+    n = len(slots)
+    grad_rows = sum(f.gradient.shape[0] for f in batch)
+    progress(f"ceiling config {config}: {n} unique rows of {int(base[-1])}, dim {dim}, {grad_rows} gradient rows")
+    state = torch.zeros(int(base[-1]) * 3 * dim, dtype=torch.float32, device="cuda")
+    grads = torch.randn(grad_rows * dim, dtype=torch.float32, device="cuda") * 1e-2
+    lists = {"sorted unique rows of the batch": torch.from_numpy(slots.view(np.int64)).cuda(),
+             "consecutive rows": torch.arange(n, dtype=torch.int64, device="cuda")}
+    fn = H.lib().eps_hip_probe_row_rmw
+    stream = torch.cuda.current_stream()
+    row_bytes = 2 * 3 * dim * 4 + dim * 4
+    full = (n * dim // 4 + 255) // 256
+    for what, dev_slots in lists.items():
+        for rows_per_group in (1, 2, 4):
+            for grid in sorted({1024, 2048, 4096, 8192, min(65536, max(1, full // rows_per_group))}):
+                def launch():
+                    rc = fn(C.c_void_p(state.data_ptr()), dim, C.c_void_p(dev_slots.data_ptr()), n,
+                            C.c_void_p(grads.data_ptr()), grad_rows, rows_per_group, grid,
+                            C.c_void_p(stream.cuda_stream))
+                    if rc:
+                        raise RuntimeError(H.lib().eps_hip_last_error().decode())
+                for _ in range(3):
+                    launch()
+                start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                reps = 20
+                start.record(stream)
+                for _ in range(reps):
+                    launch()
+                stop.record(stream)
+                torch.cuda.synchronize()
+                us = start.elapsed_time(stop) * 1e3 / reps
+                print(json.dumps({"probe": "row read-modify-write", "config": config, "rows": what,
+                                  "dim": dim, "n": n, "rows_per_group": rows_per_group, "grid": grid,
+                                  "us_per_launch": us, "rows_per_us": n / us,
+                                  "GBps": n * row_bytes / (us * 1e-6) / 1e9,
+                                  "bytes_per_row": row_bytes}), flush=True)
+    return 0
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -260,6 +321,8 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=None)
     ap.add_argument("--batches", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--ceiling", action="store_true",
+                    help="measure the row read-modify-write ceiling of the config instead")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first run three plain 1 GiB device copies (counter calibration)")
     args = ap.parse_args(argv)
@@ -267,6 +330,8 @@ def main(argv=None):
         print(f"bench.py measures one GPU only (asked for {args.gpus}): the parameter shard runs on a "
               "single MI355X here; multi-GPU sharding is designed, not built.", file=sys.stderr)
         return 2
+    if args.ceiling:
+        return ceiling(args.config)
     cfg = CONFIGS[args.config]
     steps = args.steps or cfg["steps"]
     warmup = cfg["warmup"] if args.warmup is None else args.warmup
@@ -291,7 +356,8 @@ def main(argv=None):
     batches = [wl.batch(i) for i in range(nbatch)]
     stats = [batch_stats(W, wl, b, pull) for b in batches]
     progress(f"config {args.config} ({cfg['workload']}): {nbatch} batches generated")
-    shard = H.DeviceShard(torch, wl.tables, max_occurrences=max(s["lookups"] for s in stats), workspaces=2)
+    shard = H.DeviceShard(torch, wl.tables, max_occurrences=max(s["lookups"] for s in stats),
+                          workspaces=P.WORKSPACES)
     if cfg["workload"] == "movielens":
         for t, state in enumerate(wl.initial_state()):
             shard.load_rows(t, torch.arange(state.shape[0], device="cuda"), torch.from_numpy(state).cuda())
@@ -343,6 +409,9 @@ def main(argv=None):
     gather_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in events]))
     prepare_ms = float(np.mean([e[5].elapsed_time(e[6]) for e in events]))  # side stream
     wait_ms = float(np.mean([e[1].elapsed_time(e[2]) for e in events]))
+    # How long before the end of the pull the batch's preparation had finished
+    # (positive: the main stream's wait for it found it done).
+    slack_ms = float(np.mean([e[6].elapsed_time(e[1]) for e in events]))
     fused_ms = float(np.mean([e[0].elapsed_time(e[1]) for e in fused if e]))
     push_ms = float(np.mean([e[2].elapsed_time(e[4]) for e in events]))
     step_bytes = mean["pull_bytes"] + mean["push_bytes"]
@@ -379,10 +448,13 @@ def main(argv=None):
         "step_algorithmic_GBps": step_bytes / (ms * 1e-3) / 1e9,
         "step_frac_of_hbm_peak": step_bytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBPS,
         "phases_ms": {"gather": gather_ms, "prepare": prepare_ms, "prepare_wait": wait_ms,
+                      "prepare_done_before_pull_end": slack_ms,
                       "push": push_ms, "fused_update": fused_ms,
                       "note": "gather/prepare/prepare_wait/push from untimed steps after the "
                       "timed ones (prepare runs on a side stream, ahead of the pull and push; gather "
-                      "includes the tier admissions of config 5); fused_update from every "
+                      "includes the tier admissions of config 5; prepare_done_before_pull_end > 0: "
+                      "the preparation had finished when the pull did, so prepare_wait is the cost "
+                      "of the cross-stream wait itself); fused_update from every "
                       f"{FUSED_EVERY}th timed step"},
         "roofline": {"kernel": "fused aggregation + sparse Adam (eps_hip_push_apply: "
                                "HotSliceKernel + RowRunKernel)", "bound": "hbm",

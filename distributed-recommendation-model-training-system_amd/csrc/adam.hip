@@ -475,12 +475,13 @@ __global__ void __launch_bounds__(kBlock) SortedUpdateKernel(FusedArgs a) {
 //    counters per tile (staged / added), so the waves never meet at a block
 //    barrier, and each producer keeps two chunks of rows in flight: the
 //    adding wave's serial chain is the critical path.
-//  * RowRunKernel: every other row.  A block owns kRunPositions sorted
-//    positions; it stages their keys and reference words (plus kLongRefs
-//    positions of look-ahead) in LDS with coalesced loads, finds the segment
-//    heads with a ballot, and a group of G = dim/4 lanes per row (lane = 4
-//    columns) loads the row's w, m, v together with its gradient rows, sums
-//    them in order and applies Adam.
+//  * RowRunKernel: every other row.  A block owns a window of sorted
+//    positions (RunPositions: 256, or 128 / 64 for 32- / 64-lane groups, so
+//    every group has a few rows per window whatever the width); it stages
+//    their keys and reference words (plus kLongRefs positions of look-ahead)
+//    in LDS with coalesced loads, finds the segment heads with a ballot, and a
+//    group of G = dim/4 lanes per row (lane = 4 columns) loads the row's w, m,
+//    v together with its gradient rows, sums them in order and applies Adam.
 constexpr uint32_t kHotBlock = 256;                       // threads of a hot-row block
 constexpr uint32_t kHotRing = 4;                          // chunks staged in LDS per block
 constexpr uint32_t kHotPitch = kHotChunk + 4;             // floats per tile row (one column)
@@ -489,7 +490,11 @@ constexpr uint32_t kHotRefsPerLoad = kWave / kHotQuads;   // references per row 
 constexpr uint32_t kHotLoads = kHotChunk / kHotRefsPerLoad;  // row loads per producer lane per chunk
 constexpr uint32_t kProducers = kHotBlock / kWave - 1;
 static_assert(kSlice == kWave && kHotChunk == kWave && kHotQuads == 16, "hot-row tile shape");
-constexpr uint32_t kRunPositions = 256;
+// Sorted positions per row-run window for groups of 2^log2g lanes: about 5
+// rows per group at the usual ~3 references per row.  Wider groups take
+// narrower windows, so a class of wide rows still spreads over many blocks.
+constexpr uint32_t RunPositions(uint32_t log2g) { return log2g <= 4 ? 256u : (log2g == 5 ? 128u : 64u); }
+constexpr uint32_t kRunPositions = RunPositions(2);  // the widest window
 static_assert(kRunPositions <= kBlock, "one thread per staged position finds the row heads");
 constexpr uint32_t kRefBatch = 4;                       // gradient rows in flight per group
 
@@ -898,13 +903,14 @@ __global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kLo
 RowRunKernel(VecArgs a) {
   constexpr uint32_t G = 1u << kLog2G;
   constexpr uint32_t ngroups = kBlock / G;
-  constexpr uint32_t kStaged = kRunPositions + kLongRefs;
+  constexpr uint32_t kWindow = RunPositions(kLog2G);
+  constexpr uint32_t kStaged = kWindow + kLongRefs;
   __shared__ TableDesc s_t[EPS_HIP_MAX_TABLES];
   __shared__ const float* s_grad[EPS_HIP_MAX_FEATURES];
   __shared__ uint32_t s_key[kStaged + 1];   // s_key[i + 1] = key at position p0 + i
   __shared__ const float* s_src[kStaged];   // gradient row of position p0 + i
   __shared__ float s_scale[kStaged];
-  __shared__ uint32_t s_heads[kRunPositions];
+  __shared__ uint32_t s_heads[kWindow];
   __shared__ uint32_t s_wave_heads[kBlock / kWave];
   __shared__ uint32_t s_next;               // next unclaimed row (head index) of the window
   __shared__ uint32_t s_mode;
@@ -923,13 +929,11 @@ RowRunKernel(VecArgs a) {
   // stay in that XCD's L2 for all their references.  Rows that straddle a cut
   // belong to the range holding their first position.
   const uint32_t xcd = blockIdx.x % kXcds, per_xcd = gridDim.x / kXcds;
-  const uint32_t span = ((end - begin + kXcds - 1) / kXcds + kRunPositions - 1) / kRunPositions *
-                        kRunPositions;
+  const uint32_t span = ((end - begin + kXcds - 1) / kXcds + kWindow - 1) / kWindow * kWindow;
   const uint32_t xbegin = min(begin + xcd * span, end), xend = min(xbegin + span, end);
   __syncthreads();
-  for (uint32_t p0 = xbegin + (blockIdx.x / kXcds) * kRunPositions; p0 < xend;
-       p0 += per_xcd * kRunPositions) {
-    const uint32_t p1 = min(p0 + kRunPositions, xend);
+  for (uint32_t p0 = xbegin + (blockIdx.x / kXcds) * kWindow; p0 < xend; p0 += per_xcd * kWindow) {
+    const uint32_t p1 = min(p0 + kWindow, xend);
     const uint32_t lim = min(p1 + kLongRefs, end);
     const uint32_t staged = lim - p0;
     __syncthreads();  // previous iteration's readers are done
@@ -1299,7 +1303,8 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
         va.role = role;
         role = kFollow;
         const uint64_t blocks = xcd_grid(std::min<uint64_t>(
-            std::max<uint64_t>(1, (plan.class_occurrences[cls] + kRunPositions - 1) / kRunPositions),
+            std::max<uint64_t>(1, (plan.class_occurrences[cls] + RunPositions(cls + 2) - 1) /
+                                      RunPositions(cls + 2)),
             kVectorGrid));
         EPS_HIP_TRY(LaunchVectorUpdate(cls, false, unsigned(blocks), va, s));
       }

@@ -165,10 +165,10 @@ __device__ __forceinline__ bool Finite(float x) { return AbsBits(x) < 0x7f800000
 // before this block, minus one.  One vector load and a ballot instead of a
 // chain of dependent kernel-argument loads.
 template <typename Part>
-__device__ __forceinline__ uint32_t PartOf(const Part* parts, uint32_t count) {
+__device__ __forceinline__ uint32_t PartOf(const Part* parts, uint32_t count, uint32_t unit = blockIdx.x) {
   const uint32_t lane = threadIdx.x & (kWave - 1);
   const uint32_t begin = lane < count ? parts[lane].block_begin : 0xffffffffu;
-  return uint32_t(__popcll(__ballot(begin <= blockIdx.x))) - 1u;
+  return uint32_t(__popcll(__ballot(begin <= unit))) - 1u;
 }
 
 // Maximum over the lanes of a wavefront (DPP/permute lowering by the compiler).

@@ -13,6 +13,7 @@
 // src/cuda/cache_backend.cu:134-139) is fused into the store.
 #include "common.hpp"
 
+#include <algorithm>
 #include <cfloat>
 #include <mutex>
 
@@ -330,68 +331,76 @@ __global__ void GatherRowsKernel(const float* state, uint32_t dim, const uint64_
 // Row moves of several tables in one launch (admissions: packed -> slots,
 // like ScatterRowsKernel; write-backs: slots -> packed, like
 // GatherRowsKernel).  A part's 16-byte pieces (scalar floats when dim % 4)
-// are dealt to its blocks in contiguous ranges.
+// form chunks of kBlock * kMovePerThread; the launch's blocks take the chunks
+// of all parts in turn (chunk c, c + gridDim.x, ...).  When one side is host
+// memory the grid is small: each block's loads wait microseconds on the host
+// link, and a few blocks keep enough bytes in flight for it without holding
+// wave slots the step's own kernels need.
 constexpr uint32_t kMovePerThread = 4;
+constexpr uint32_t kHostLinkGrid = 16;  // blocks of a move that crosses the host link (best of 8-64 on
+                                         // config 5: fewer slow the moves, more slow the step)
 struct MoveDesc {
   float* state;
   float* packed;
   const uint64_t* slots;
   uint64_t count;
-  uint32_t dim, block_begin;
+  uint32_t dim, block_begin;  // block_begin: the part's first chunk
 };
 struct MoveArgs {
   MoveDesc part[EPS_HIP_MAX_TABLES];
-  uint32_t count;
+  uint32_t count, chunks;
   uint32_t write_back;
   Bounds* bounds;
 };
 
 __global__ void __launch_bounds__(kBlock) MoveRowsKernel(MoveArgs a) {
-  const MoveDesc d = a.part[PartOf(a.part, a.count)];
-  const uint64_t width = uint64_t(d.dim) * 3;
-  const bool vec = (d.dim & 3) == 0;
-  const uint64_t per_row = vec ? width / 4 : width;
-  const uint64_t items = d.count * per_row;
-  const uint64_t first = uint64_t(blockIdx.x - d.block_begin) * kBlock * kMovePerThread;
   uint32_t bw = 0, bm = 0, bv = 0;
-  // Every load of the thread is issued before any store: one side may be
-  // host memory, microseconds away over the host link.
-  const float* src[kMovePerThread];
-  float* dst[kMovePerThread];
-  uint64_t col[kMovePerThread];
-  bool ok[kMovePerThread];
-#pragma unroll
-  for (uint32_t k = 0; k < kMovePerThread; ++k) {
-    const uint64_t e = first + uint64_t(k) * kBlock + threadIdx.x;
-    ok[k] = e < items;
-    const uint64_t row = ok[k] ? e / per_row : 0, piece = ok[k] ? e % per_row : 0;
-    col[k] = vec ? piece * 4 : piece;
-    float* slot_row = d.state + (ok[k] ? d.slots[row] : 0) * width + col[k];
-    float* packed = d.packed + row * width + col[k];
-    src[k] = a.write_back ? slot_row : packed;
-    dst[k] = a.write_back ? packed : slot_row;
-  }
-  if (vec) {
-    float4 x[kMovePerThread];
-#pragma unroll
-    for (uint32_t k = 0; k < kMovePerThread; ++k) x[k] = ok[k] ? Load4(src[k]) : make_float4(0.f, 0.f, 0.f, 0.f);
+  for (uint32_t chunk = blockIdx.x; chunk < a.chunks; chunk += gridDim.x) {
+    const MoveDesc d = a.part[PartOf(a.part, a.count, chunk)];
+    const uint64_t width = uint64_t(d.dim) * 3;
+    const bool vec = (d.dim & 3) == 0;
+    const uint64_t per_row = vec ? width / 4 : width;
+    const uint64_t items = d.count * per_row;
+    const uint64_t first = uint64_t(chunk - d.block_begin) * kBlock * kMovePerThread;
+    // Every load of the thread is issued before any store: one side may be
+    // host memory, microseconds away over the host link.
+    const float* src[kMovePerThread];
+    float* dst[kMovePerThread];
+    uint64_t col[kMovePerThread];
+    bool ok[kMovePerThread];
 #pragma unroll
     for (uint32_t k = 0; k < kMovePerThread; ++k) {
-      if (!ok[k]) continue;
-      Store4(dst[k], x[k]);
-      const uint32_t m = max(max(AbsBits(x[k].x), AbsBits(x[k].y)), max(AbsBits(x[k].z), AbsBits(x[k].w)));
-      if (col[k] < d.dim) bw = max(bw, m); else if (col[k] < 2 * d.dim) bm = max(bm, m); else bv = max(bv, m);
+      const uint64_t e = first + uint64_t(k) * kBlock + threadIdx.x;
+      ok[k] = e < items;
+      const uint64_t row = ok[k] ? e / per_row : 0, piece = ok[k] ? e % per_row : 0;
+      col[k] = vec ? piece * 4 : piece;
+      float* slot_row = d.state + (ok[k] ? d.slots[row] : 0) * width + col[k];
+      float* packed = d.packed + row * width + col[k];
+      src[k] = a.write_back ? slot_row : packed;
+      dst[k] = a.write_back ? packed : slot_row;
     }
-  } else {
-    float x[kMovePerThread];
+    if (vec) {
+      float4 x[kMovePerThread];
 #pragma unroll
-    for (uint32_t k = 0; k < kMovePerThread; ++k) x[k] = ok[k] ? LoadF(src[k]) : 0.f;
+      for (uint32_t k = 0; k < kMovePerThread; ++k) x[k] = ok[k] ? Load4(src[k]) : make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (uint32_t k = 0; k < kMovePerThread; ++k) {
-      if (!ok[k]) continue;
-      StoreF(dst[k], x[k]);
-      if (col[k] < d.dim) bw = max(bw, AbsBits(x[k])); else if (col[k] < 2 * d.dim) bm = max(bm, AbsBits(x[k]));
-      else bv = max(bv, AbsBits(x[k]));
+      for (uint32_t k = 0; k < kMovePerThread; ++k) {
+        if (!ok[k]) continue;
+        Store4(dst[k], x[k]);
+        const uint32_t m = max(max(AbsBits(x[k].x), AbsBits(x[k].y)), max(AbsBits(x[k].z), AbsBits(x[k].w)));
+        if (col[k] < d.dim) bw = max(bw, m); else if (col[k] < 2 * d.dim) bm = max(bm, m); else bv = max(bv, m);
+      }
+    } else {
+      float x[kMovePerThread];
+#pragma unroll
+      for (uint32_t k = 0; k < kMovePerThread; ++k) x[k] = ok[k] ? LoadF(src[k]) : 0.f;
+#pragma unroll
+      for (uint32_t k = 0; k < kMovePerThread; ++k) {
+        if (!ok[k]) continue;
+        StoreF(dst[k], x[k]);
+        if (col[k] < d.dim) bw = max(bw, AbsBits(x[k])); else if (col[k] < 2 * d.dim) bm = max(bm, AbsBits(x[k]));
+        else bv = max(bv, AbsBits(x[k]));
+      }
     }
   }
   if (!a.write_back) BoundMax(a.bounds, bw, bm, bv);
@@ -412,12 +421,13 @@ uint64_t HostMix(uint64_t x) {
 // Device-visible address of a row buffer: device memory as is, pinned host
 // memory through its mapped device pointer; pageable host memory is refused
 // (a kernel must never dereference an unmapped host address).
-int DeviceAddress(const void* p, const void** out) {
+int DeviceAddress(const void* p, const void** out, bool* host = nullptr) {
   hipPointerAttribute_t attr;
   if (hipPointerGetAttributes(&attr, p) != hipSuccess) {
     (void)hipGetLastError();
     return Fail(EPS_HIP_INVALID_ARGUMENT, "row buffer must be device memory or pinned host memory");
   }
+  if (host) *host = attr.type == hipMemoryTypeHost;
   if (attr.type == hipMemoryTypeHost) {
     if (!attr.devicePointer) return Fail(EPS_HIP_INVALID_ARGUMENT, "pinned host buffer is not mapped");
     *out = attr.devicePointer;
@@ -530,6 +540,7 @@ int eps_hip_move_rows(const eps_hip_row_batch* batches, uint32_t count, int32_t 
   args.write_back = write_back ? 1u : 0u;
   args.bounds = static_cast<Bounds*>(bounds);
   uint64_t blocks = 0;
+  bool host_link = false;
   for (uint32_t i = 0; i < count; ++i) {
     const eps_hip_row_batch& b = batches[i];
     if (!b.count) continue;
@@ -537,7 +548,9 @@ int eps_hip_move_rows(const eps_hip_row_batch* batches, uint32_t count, int32_t 
       return Fail(EPS_HIP_INVALID_ARGUMENT, "invalid row batch");
     if (reinterpret_cast<uintptr_t>(b.state) % 16) return Fail(EPS_HIP_INVALID_ARGUMENT, "table state must be 16-byte aligned");
     const void* packed = nullptr;
-    EPS_HIP_TRY(DeviceAddress(b.packed, &packed));
+    bool host = false;
+    EPS_HIP_TRY(DeviceAddress(b.packed, &packed, &host));
+    host_link = host_link || host;
     if ((b.dim & 3) == 0 && reinterpret_cast<uintptr_t>(packed) % 16)
       return Fail(EPS_HIP_INVALID_ARGUMENT, "packed rows must be 16-byte aligned");
     MoveDesc& d = args.part[args.count++];
@@ -552,7 +565,9 @@ int eps_hip_move_rows(const eps_hip_row_batch* batches, uint32_t count, int32_t 
     if (blocks >= (1ull << 31)) return Fail(EPS_HIP_CAPACITY_EXCEEDED, "row move grid too large");
   }
   if (!blocks) return EPS_HIP_OK;
-  hipLaunchKernelGGL(MoveRowsKernel, dim3(unsigned(blocks)), dim3(kBlock), 0, AsStream(stream), args);
+  args.chunks = uint32_t(blocks);
+  const uint64_t grid = std::min<uint64_t>(blocks, host_link ? kHostLinkGrid : 65536);
+  hipLaunchKernelGGL(MoveRowsKernel, dim3(unsigned(grid)), dim3(kBlock), 0, AsStream(stream), args);
   EPS_HIP_LAUNCHED("move rows");
   return EPS_HIP_OK;
 }

@@ -4,11 +4,15 @@ One step over a batch of features = the pooled pull of every feature on the
 main stream, then the push (gradient scan, fused aggregation + sparse Adam,
 checked apply) on the main stream.  The push's preparation (device dedup sort
 and hot-row lists) reads only the batch's ids, so it runs on a side stream
-ahead of the pull, alternating between two workspaces:
+ahead of the pull, rotating over the shard's W push workspaces (W >= 2):
 
-  * batch k's preparation waits for the push of batch k-2, the last reader of
+  * batch k's preparation waits for the push of batch k-W, the last reader of
     its workspace;
   * batch k's push waits for its preparation.
+
+With W = 3 a preparation has two steps' time to finish before its push needs
+it, so a preparation slowed by the steps it overlaps does not hold the main
+stream up.
 
 Pushes are issued without reading their status (that would stall the
 pipeline): optimizer powers are advanced when a push is issued and every
@@ -23,23 +27,26 @@ import numpy as np
 
 from . import eps_hip as H
 
+WORKSPACES = 3  # push workspaces the timed pipeline rotates over
+
 
 class StepPipeline:
     def __init__(self, torch, shard, batches, outputs, pull=True, moves=None):
-        """`shard` is an eps_hip.DeviceShard with two workspaces; `batches` a
+        """`shard` is an eps_hip.DeviceShard with two or more workspaces; `batches` a
         list of lists of DeviceFeature (cycled); `outputs` one pooled-output
         tensor per feature position.  `pull` False: the step is the push alone
         (duplicate-heavy gradient pairs).  `moves`: a TierMoves whose
         admissions run before the pull and whose write-backs run after the push."""
         if len(shard.wss) < 2:
-            raise ValueError("the pipeline alternates two push workspaces")
+            raise ValueError("the pipeline rotates over two or more push workspaces")
+        self.slots = len(shard.wss)
         self.torch, self.shard, self.batches, self.outputs = torch, shard, batches, outputs
         self.pull, self.moves = pull, moves
         self.stream = torch.cuda.current_stream()
         self.side = torch.cuda.Stream()
-        self.prepared = [torch.cuda.Event() for _ in range(2)]
-        self.pushed = [torch.cuda.Event() for _ in range(2)]
-        for slot in range(2):
+        self.prepared = [torch.cuda.Event() for _ in range(self.slots)]
+        self.pushed = [torch.cuda.Event() for _ in range(self.slots)]
+        for slot in range(self.slots):
             shard.clear_history(slot)
 
     def step(self, k, fused=None, phases=None):
@@ -47,7 +54,7 @@ class StepPipeline:
         events around the fused update; `phases` = seven events for a
         per-phase breakdown (see bench.py)."""
         feats = self.batches[k % len(self.batches)]
-        slot = k % 2
+        slot = k % self.slots
         stream, side, shard = self.stream, self.side, self.shard
         side.wait_event(self.pushed[slot])
         if phases:
@@ -75,9 +82,10 @@ class StepPipeline:
 
     def check(self):
         """Waits for the device; raises if any push of the run failed."""
-        bits = [self.shard.history(slot) for slot in range(2)]
+        bits = [self.shard.history(slot) for slot in range(self.slots)]
         if any(b & H.STATUS_ERRORS for b in bits):
-            raise RuntimeError(f"a pipelined push failed: status history {bits[0]:#x} / {bits[1]:#x}")
+            raise RuntimeError("a pipelined push failed: status history " +
+                               " / ".join(f"{b:#x}" for b in bits))
 
 
 class TierMoves:

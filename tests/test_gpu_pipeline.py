@@ -1,12 +1,12 @@
 """The benchmarked pipeline against the serial path and the oracle.
 
 bench.py times pipeline.StepPipeline: the push's preparation on a side stream
-one batch ahead, two alternating workspaces, and the push split into
+up to WORKSPACES - 1 batches ahead, WORKSPACES rotating workspaces, and the push split into
 begin/apply/end with timing events around the fused pass.  This runs that
 exact step for 8 steps of the 26 x 1,000,000 x 64 workload (4 batches cycled,
 as the bench does) and requires:
 
-  * no failure in either workspace's status history;
+  * no failure in any workspace's status history;
   * every table bit-identical to the serial path (prepare then push on one
     stream with one workspace, status read after every push), and the same
     optimizer powers;
@@ -38,7 +38,7 @@ def test_bench_pipeline_matches_serial_and_oracle(torch_gpu, pkg):
     dev = [[H.DeviceFeature(torch, f) for f in b] for b in batches]
     print(f"case: criteo26 pipeline, {STEPS} steps ({time.time() - t0:.1f}s)", flush=True)
 
-    piped = H.DeviceShard(torch, wl.tables, max_occurrences=most, workspaces=2)
+    piped = H.DeviceShard(torch, wl.tables, max_occurrences=most, workspaces=P.WORKSPACES)
     piped.init_rows()
     outputs = [torch.empty((wl.batch_size, t.dim), dtype=torch.float32, device="cuda") for t in wl.tables]
     pipe = P.StepPipeline(torch, piped, dev, outputs)

@@ -38,7 +38,7 @@ def test_ragged8_tier_moves_full_size(torch_gpu, pkg):
     print(f"case: ragged8 tier moves, {STEPS} steps, admitted rows per step {sum(counts)} "
           f"({time.time() - t0:.1f}s)", flush=True)
     most = max(sum(len(f.keys) for f in b) for b in batches)
-    shard = H.DeviceShard(torch, wl.tables, max_occurrences=most, workspaces=2)
+    shard = H.DeviceShard(torch, wl.tables, max_occurrences=most, workspaces=P.WORKSPACES)
     shard.init_rows()
     dev = [[H.DeviceFeature(torch, f) for f in b] for b in batches]
     outputs = [torch.empty((wl.bags, t.dim), dtype=torch.float32, device="cuda") for t in wl.tables]
