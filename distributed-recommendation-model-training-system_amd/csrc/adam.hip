@@ -465,16 +465,19 @@ __global__ void __launch_bounds__(kBlock) SortedUpdateKernel(FusedArgs a) {
 //  * HotSliceKernel: rows with more than kLongRefs references (listed at
 //    prepare time).  Work unit = (hot row, kSlice-column slice); a block
 //    works through a stream of units chunk by chunk (kHotChunk references).
-//    Wave 0 adds: lane c owns column col0 + c, adds the chunk's products in
-//    reference order (one dependent add per reference) and applies Adam
-//    after the unit's last chunk.  Waves 1..kProducers produce: producer p
-//    loads the gradient rows of every kProducers-th chunk (16 contiguous
-//    bytes per lane), multiplies them by their scales and stores the products
-//    into one of kHotRing LDS tiles [column][reference], with the unit's
-//    w, m, v when the chunk is its last.  Tiles change hands through two LDS
-//    counters per tile (staged / added), so the waves never meet at a block
-//    barrier, and each producer keeps two chunks of rows in flight: the
-//    adding wave's serial chain is the critical path.
+//    Wave 0 adds: lane c < kSlice owns column col0 + c, adds the chunk's
+//    products in reference order (one dependent add per reference) and
+//    applies Adam after the unit's last chunk.  Waves 1..kProducers produce:
+//    producer p loads the gradient rows of every kProducers-th chunk (16
+//    contiguous bytes per lane), multiplies them by their scales and stores
+//    the products into one of kHotRing LDS tiles [column][reference], with
+//    the unit's w, m, v when the chunk is its last.  Tiles change hands
+//    through two LDS counters per tile (staged / added), so the waves never
+//    meet at a block barrier, and each producer keeps two chunks of rows in
+//    flight.  The slices are narrow (16 columns) so that a hot row's chain
+//    data spreads over several CUs: a block's producers then move a quarter
+//    of a 64-column chunk's bytes through their CU per chunk, and the adding
+//    wave's serial chain, not the CU's memory pipeline, sets the rate.
 //  * RowRunKernel: every other row.  A block owns a window of sorted
 //    positions (RunPositions: 256, or 128 / 64 for 32- / 64-lane groups, so
 //    every group has a few rows per window whatever the width); it stages
@@ -489,7 +492,8 @@ constexpr uint32_t kHotQuads = kSlice / 4;                // lanes per reference
 constexpr uint32_t kHotRefsPerLoad = kWave / kHotQuads;   // references per row load
 constexpr uint32_t kHotLoads = kHotChunk / kHotRefsPerLoad;  // row loads per producer lane per chunk
 constexpr uint32_t kProducers = kHotBlock / kWave - 1;
-static_assert(kSlice == kWave && kHotChunk == kWave && kHotQuads == 16, "hot-row tile shape");
+static_assert(kHotChunk == kWave && kSlice <= kWave && kWave % kHotQuads == 0 && kHotLoads % 4 == 0,
+              "hot-row tile shape");
 // Sorted positions per row-run window for groups of 2^log2g lanes: about 5
 // rows per group at the usual ~3 references per row.  Wider groups take
 // narrower windows, so a class of wide rows still spreads over many blocks.
@@ -512,9 +516,10 @@ struct VecArgs {
 };
 
 // Position of (column c, reference r) in a hot-row tile.  Groups of four
-// references are rotated by the column's quarter (XOR), so the four stores of
-// a producer's row load hit 64 distinct banks, and the adding wave's 16-byte
-// reads of four consecutive references stay aligned.
+// references are rotated by the column's 16-column group (XOR; the identity
+// for slices of 16 columns), so a producer's stores of one row load hit
+// distinct banks, and the adding wave's 16-byte reads of four consecutive
+// references stay aligned.
 __device__ __forceinline__ uint32_t TileAt(uint32_t c, uint32_t r) {
   return c * kHotPitch + 4u * ((r >> 2) ^ (c >> 4)) + (r & 3u);
 }
@@ -688,11 +693,13 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
     HotSlot cn = after(c);       // chunk j + 1
     HotSlot cnn = after(cn);     // chunk j + 2
     float acc = 0.f;
-    auto read_tile = [&](uint32_t j, float4* x) {
+    auto read_tile = [&](uint32_t j, float4* x) {  // lanes past the slice read nothing
       const float* tile = s_tile[j % kHotRing];
+      if (lane < kSlice) {
 #pragma unroll
-      for (uint32_t g = 0; g < kHotChunk / 4; ++g)
-        x[g] = *reinterpret_cast<const float4*>(tile + TileAt(lane, 4 * g));
+        for (uint32_t g = 0; g < kHotChunk / 4; ++g)
+          x[g] = *reinterpret_cast<const float4*>(tile + TileAt(lane, 4 * g));
+      }
     };
     auto ready = [&](uint32_t j) {
       if (!stalled && !WaitCounter(&s_ready[j % kHotRing], j / kHotRing + 1, 0, a.spin_limit)) stalled = true;
@@ -705,7 +712,8 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
       __builtin_amdgcn_s_waitcnt(kLgkmZero);
       __builtin_amdgcn_sched_barrier(0);
       const uint32_t t = j % kHotRing;
-      float w = s_wmv[t][0][lane], m = s_wmv[t][1][lane], v = s_wmv[t][2][lane];
+      const uint32_t sl = lane % kSlice;  // lanes past the slice read a copy and drop it
+      float w = s_wmv[t][0][sl], m = s_wmv[t][1][sl], v = s_wmv[t][2][sl];
       const uint32_t peek = __hip_atomic_load(&s_ready[(j + 2) % kHotRing], __ATOMIC_RELAXED,
                                               __HIP_MEMORY_SCOPE_WORKGROUP);
       if (cn.ok) read_tile(j + 1, y);
@@ -729,7 +737,7 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
       __builtin_amdgcn_sched_barrier(0);
       if (c.cbase + kHotChunk >= c.end) {  // the unit's last chunk
         const TableDesc& T = s_t[c.key >> a.row_bits];
-        if (c.col0 + lane < T.dim && !stalled) {
+        if (lane < kSlice && c.col0 + lane < T.dim && !stalled) {
           AdamElement(T, acc, w, m, v, st);
           if (write) {
             float* row = T.state + uint64_t(c.key & row_mask) * T.dim * 3 + c.col0 + lane;
@@ -761,13 +769,11 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
   } else {
     // Producer p stages chunks p, p + kProducers, ... (its own chunks, counted
     // by o).  At own chunk o it stages rows(o), decodes the words of o + 2
-    // into its LDS reference slots, loads the words of o + 3 and then the
+    // into its LDS reference slots, loads the words of o + 4 and then the
     // rows of o + 2.  Loads complete in issue order, so each wait waits only
-    // for what it needs: the words loaded now are decoded one own chunk
-    // later, before the rows loaded now are staged.  Every chunk issues the
-    // same loads, also past the stream's end (then from the start of the
-    // reference words, never used), so the number of loads between any two
-    // points is fixed.
+    // for what it needs.  Every chunk issues the same loads, also past the
+    // stream's end (then from the start of the reference words, never used),
+    // so the number of loads between any two points is fixed.
     const uint32_t p = wave - 1;
     const uint32_t quad = lane % kHotQuads, sub = lane / kHotQuads;
     const float* idle = reinterpret_cast<const float*>(a.rs);
@@ -782,21 +788,25 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
         if (!cur.ok && total == ~0u) total = jc;
       }
     };
-    HotSlot wc{};  // chunk whose words are in `word`
+    // Reference words of one chunk in flight (lane l: reference l).
+    struct Words {
+      HotSlot c;
+      uint64_t word;
+    };
     HotSlot dc{};  // chunk whose references are in the LDS slots
-    uint64_t word = 0;
-    auto load_words = [&]() {
-      wc = cur;
+    auto load_words = [&](Words& w) {
+      w.c = cur;
       const uint32_t pos = cur.ok ? min(cur.cbase + lane, cur.end - 1) : 0u;
-      word = a.rs[pos];
+      w.word = a.rs[pos];
     };
     // Lane l decodes the word of reference l: its gradient row (from the
     // slice's first column) and scale.
-    auto decode = [&]() {
+    auto decode = [&](const Words& w) {
+      const HotSlot& wc = w.c;
       dc = wc;
       const TableDesc& T = s_t[wc.key >> a.row_bits];
       float scale;
-      const float* src = RefSource(s_grad, word, T.dim, wc.col0, scale);
+      const float* src = RefSource(s_grad, w.word, T.dim, wc.col0, scale);
       slots.src[lane % kHotRefsPerLoad][lane / kHotRefsPerLoad] = wc.ok ? src : idle;
       slots.scale[lane % kHotRefsPerLoad][lane / kHotRefsPerLoad] = scale;
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
@@ -825,7 +835,7 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
       }
 #pragma unroll
       for (uint32_t k = 0; k < kHotLoads; ++k) r.x[k] = Load4(src[k] + step);
-      const uint32_t wcol = dc.col0 + (dc.col0 + lane < dim ? lane : 0u);
+      const uint32_t wcol = dc.col0 + (lane < kSlice && dc.col0 + lane < dim ? lane : 0u);
       const float* row = dc.ok ? T.state + uint64_t(dc.key & row_mask) * dim * 3 + wcol : idle;
       const uint32_t ms = dc.ok ? dim : 0u;
       r.wmv[0] = LoadF(row); r.wmv[1] = LoadF(row + ms); r.wmv[2] = LoadF(row + 2 * ms);
@@ -834,14 +844,14 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
       const uint32_t t = j % kHotRing;
       if (!stalled && !WaitCounter(&s_used[t], j / kHotRing, 1, a.spin_limit)) stalled = true;
       if (stalled) return;  // nothing more is staged
-      // Load k writes (column 4*quad + i, reference 4k + sub) = TileAt(): the
-      // reference group k is rotated by the column's quarter quad / 4.
-      float* tile = s_tile[t] + 4 * quad * kHotPitch + sub;
+      // Load k brings columns 4*quad .. 4*quad+3 of reference
+      // kHotRefsPerLoad*k + sub; each lands at TileAt(column, reference).
+      float* tile = s_tile[t];
       if (r.c.cbase + kHotChunk <= r.c.end) {  // every reference inside the row
 #pragma unroll
         for (uint32_t k = 0; k < kHotLoads; ++k) {
           const float sv = r.s[k];
-          float* q = tile + 4u * (k ^ (quad >> 2));
+          float* q = tile + TileAt(4 * quad, kHotRefsPerLoad * k + sub);
           q[0] = r.x[k].x * sv;
           q[kHotPitch] = r.x[k].y * sv;
           q[2 * kHotPitch] = r.x[k].z * sv;
@@ -852,43 +862,54 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
         for (uint32_t k = 0; k < kHotLoads; ++k) {
           const bool in = r.c.cbase + kHotRefsPerLoad * k + sub < r.c.end;
           const float sv = r.s[k];
-          float* q = tile + 4u * (k ^ (quad >> 2));
+          float* q = tile + TileAt(4 * quad, kHotRefsPerLoad * k + sub);
           q[0] = in ? r.x[k].x * sv : -0.f;
           q[kHotPitch] = in ? r.x[k].y * sv : -0.f;
           q[2 * kHotPitch] = in ? r.x[k].z * sv : -0.f;
           q[3 * kHotPitch] = in ? r.x[k].w * sv : -0.f;
         }
       }
-      s_wmv[t][0][lane] = r.wmv[0];
-      s_wmv[t][1][lane] = r.wmv[1];
-      s_wmv[t][2][lane] = r.wmv[2];
+      if (lane < kSlice) {
+        s_wmv[t][0][lane] = r.wmv[0];
+        s_wmv[t][1][lane] = r.wmv[1];
+        s_wmv[t][2][lane] = r.wmv[2];
+      }
       PostCounter(&s_ready[t], j / kHotRing + 1);
     };
     HotRows ra, rb;
-    advance(p);
-    load_words();
-    decode();
-    advance(kProducers);
-    load_words();
-    load_rows(ra);
-    decode();
-    advance(kProducers);
-    load_words();
-    load_rows(rb);
-    // Own chunk o (chunk j = p + kProducers*o): stage rows(o) from buffer
-    // o % 2, decode words(o + 2), load words(o + 3), load rows(o + 2) into
-    // buffer o % 2.  Two own chunks per pass keep the buffers static.
-    auto own = [&](HotRows& r, uint32_t j) {
+    Words wa, wb;
+    // The prologue leaves the loads in the loop's own order (words(2),
+    // rows(0), words(3), rows(1)), so the compiler's load waits inside the
+    // loop can be exact.
+    advance(p);            // own chunk 0
+    load_words(wa);
+    decode(wa);
+    advance(kProducers);   // 1
+    load_words(wb);
+    advance(kProducers);   // 2
+    load_words(wa);
+    load_rows(ra);         // rows(0): the slots hold own chunk 0
+    decode(wb);
+    advance(kProducers);   // 3
+    load_words(wb);
+    load_rows(rb);         // rows(1)
+    // Own chunk o (chunk j = p + kProducers*o): stage rows(o) from row buffer
+    // o % 2, decode words(o + 2) from word buffer o % 2, load words(o + 4)
+    // into it and rows(o + 2) into the row buffer.  Words and rows both get
+    // two own chunks to arrive (the decode needs no wait of its own: its
+    // words were issued before the rows the stage waited for).  Two own
+    // chunks per pass keep the buffers static.
+    auto own = [&](HotRows& r, Words& w, uint32_t j) {
       stage(r, j);
-      decode();
+      decode(w);
       advance(kProducers);
-      load_words();
+      load_words(w);
       load_rows(r);
     };
     uint32_t j = p;
     for (; j + kProducers < total; j += 2 * kProducers) {  // one exit: both halves always run
-      own(ra, j);
-      own(rb, j + kProducers);
+      own(ra, wa, j);
+      own(rb, wb, j + kProducers);
     }
     if (j < total) stage(ra, j);
   }
