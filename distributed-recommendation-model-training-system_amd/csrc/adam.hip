@@ -487,11 +487,13 @@ __global__ void __launch_bounds__(kBlock) SortedUpdateKernel(FusedArgs a) {
 //    v together with its gradient rows, sums them in order and applies Adam.
 constexpr uint32_t kHotBlock = 256;                       // threads of a hot-row block
 constexpr uint32_t kHotRing = 4;                          // chunks staged in LDS per block
+constexpr uint32_t kUnitCache = 512;                      // unit headers a block stages in LDS
 constexpr uint32_t kHotPitch = kHotChunk + 4;             // floats per tile row (one column)
 constexpr uint32_t kHotQuads = kSlice / 4;                // lanes per reference in a row load
 constexpr uint32_t kHotRefsPerLoad = kWave / kHotQuads;   // references per row load
 constexpr uint32_t kHotLoads = kHotChunk / kHotRefsPerLoad;  // row loads per producer lane per chunk
 constexpr uint32_t kProducers = kHotBlock / kWave - 1;
+constexpr uint32_t kDepth = 2;  // own chunks each producer keeps in flight (4 measured no faster)
 static_assert(kHotChunk == kWave && kSlice <= kWave && kWave % kHotQuads == 0 && kHotLoads % 4 == 0,
               "hot-row tile shape");
 // Sorted positions per row-run window for groups of 2^log2g lanes: about 5
@@ -607,6 +609,7 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
   __shared__ __align__(16) HotRefs s_ref[kProducers];
   // ready[t]: chunks staged in tile t so far; used[t]: chunks added from it.
   __shared__ uint32_t s_ready[kHotRing], s_used[kHotRing];
+  __shared__ uint4 s_unit[kUnitCache];  // {start, end, key, col0} of the block's first units
   __shared__ uint32_t s_mode;
   bool write = false;
   if (!VecPrologue<kHotBlock>(a, s_t, s_grad, &s_mode, write)) return;
@@ -638,9 +641,30 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
              << a.slice_bits;
     bucket_end[b] = units;
   }
-  // Hot-row entries are read through the scalar cache (the lists are written
-  // before this kernel and only read here): a scalar load's wait does not
-  // wait for the vector loads in flight.
+  // The block's unit u of round r, and where its hot-row entry lies.
+  auto unit_of = [&](uint32_t r) { return r * xcd_blocks + ((r & 1) ? xcd_blocks - 1 - me : me); };
+  auto entry_of = [&](uint32_t u, uint32_t& col0) {
+    uint32_t b = 0;
+#pragma unroll
+    for (uint32_t k = 0; k + 1 < kHotBuckets; ++k) b += u >= bucket_end[k];
+    const uint32_t local = u - (b ? bucket_end[b - 1] : 0u);
+    col0 = (local & slice_mask) * kSlice;
+    return uint64_t(xcd * kHotBuckets + b) * a.hot_capacity + (local >> a.slice_bits);
+  };
+  // The headers of the block's first kUnitCache units are staged in LDS once,
+  // so walking the stream costs each wave an LDS read per unit.  (A scalar
+  // load per unit would stall every wave's next LDS wait until it returns:
+  // scalar loads and LDS accesses share one wait counter.)  Later units, if
+  // any, are read through the scalar cache.
+  for (uint32_t r = threadIdx.x; r < kUnitCache; r += kHotBlock) {
+    const uint32_t u = unit_of(r);
+    if (u < units) {
+      uint32_t col0;
+      const HotEntry e = a.hot[entry_of(u, col0)];
+      s_unit[r] = make_uint4(e.start, e.end, e.key, col0);
+    }
+  }
+  __syncthreads();
   const auto* hot = reinterpret_cast<const __attribute__((address_space(4))) HotEntry*>(
       reinterpret_cast<uintptr_t>(a.hot));
   // The block's stream of chunks; every wave walks it the same way.
@@ -649,17 +673,18 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
   uint32_t next_col0 = 0;
   bool next_ok = false;
   auto fetch = [&]() {  // header of the block's next unit
-    const uint32_t u = round * xcd_blocks + ((round & 1) ? xcd_blocks - 1 - me : me);
-    ++round;
+    const uint32_t r = round++;
+    const uint32_t u = unit_of(r);
     next_ok = u < units;  // unit indices grow with the round: past the end stays past
     if (!next_ok) return;
-    uint32_t b = 0;
-#pragma unroll
-    for (uint32_t k = 0; k + 1 < kHotBuckets; ++k) b += u >= bucket_end[k];
-    const uint32_t local = u - (b ? bucket_end[b - 1] : 0u);
-    const auto& e = hot[uint64_t(xcd * kHotBuckets + b) * a.hot_capacity + (local >> a.slice_bits)];
+    if (r < kUnitCache) {
+      const uint4 e = s_unit[r];
+      next_entry = HotEntry{e.x, e.y, e.z, 0u};
+      next_col0 = e.w;
+      return;
+    }
+    const auto& e = hot[entry_of(u, next_col0)];
     next_entry = HotEntry{e.start, e.end, e.key, 0u};
-    next_col0 = (local & slice_mask) * kSlice;
   };
   auto take = [&]() {  // the next unit's first chunk; slices past a row's dimension are skipped
     for (;;) {
@@ -768,12 +793,12 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
     }
   } else {
     // Producer p stages chunks p, p + kProducers, ... (its own chunks, counted
-    // by o).  At own chunk o it stages rows(o), decodes the words of o + 2
-    // into its LDS reference slots, loads the words of o + 4 and then the
-    // rows of o + 2.  Loads complete in issue order, so each wait waits only
-    // for what it needs.  Every chunk issues the same loads, also past the
-    // stream's end (then from the start of the reference words, never used),
-    // so the number of loads between any two points is fixed.
+    // by o).  At own chunk o it stages rows(o), decodes the words of o + D
+    // into its LDS reference slots, loads the words of o + 2D and then the
+    // rows of o + D (D = kDepth).  Loads complete in issue order, so each wait
+    // waits only for what it needs.  Every chunk issues the same loads, also
+    // past the stream's end (then from the start of the reference words, never
+    // used), so the number of loads between any two points is fixed.
     const uint32_t p = wave - 1;
     const uint32_t quad = lane % kHotQuads, sub = lane / kHotQuads;
     const float* idle = reinterpret_cast<const float*>(a.rs);
@@ -876,42 +901,45 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
       }
       PostCounter(&s_ready[t], j / kHotRing + 1);
     };
-    HotRows ra, rb;
-    Words wa, wb;
-    // The prologue leaves the loads in the loop's own order (words(2),
-    // rows(0), words(3), rows(1)), so the compiler's load waits inside the
-    // loop can be exact.
-    advance(p);            // own chunk 0
-    load_words(wa);
-    decode(wa);
-    advance(kProducers);   // 1
-    load_words(wb);
-    advance(kProducers);   // 2
-    load_words(wa);
-    load_rows(ra);         // rows(0): the slots hold own chunk 0
-    decode(wb);
-    advance(kProducers);   // 3
-    load_words(wb);
-    load_rows(rb);         // rows(1)
-    // Own chunk o (chunk j = p + kProducers*o): stage rows(o) from row buffer
-    // o % 2, decode words(o + 2) from word buffer o % 2, load words(o + 4)
-    // into it and rows(o + 2) into the row buffer.  Words and rows both get
-    // two own chunks to arrive (the decode needs no wait of its own: its
-    // words were issued before the rows the stage waited for).  Two own
-    // chunks per pass keep the buffers static.
+    // kDepth own chunks of rows and of reference words in flight.  The
+    // prologue leaves the loads in the loop's own order (words(D), rows(0),
+    // words(D+1), rows(1), ...), so the compiler's load waits inside the loop
+    // can be exact.
+    HotRows rows[kDepth];
+    Words words[kDepth];
+    advance(p);  // own chunk 0
+#pragma unroll
+    for (uint32_t k = 0; k < kDepth; ++k) {  // words(0 .. D-1)
+      load_words(words[k]);
+      advance(kProducers);
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < kDepth; ++k) {  // words(D + k), then rows(k) from the slots of own chunk k
+      decode(words[k]);
+      load_words(words[k]);
+      advance(kProducers);
+      load_rows(rows[k]);
+    }
+    // Own chunk o (chunk j = p + kProducers*o), buffers b = o % D: stage
+    // rows(o), decode words(o + D), load words(o + 2D) and rows(o + D).
+    // Words and rows both get D own chunks to arrive (the decode needs no
+    // wait of its own: its words were issued before the rows the stage
+    // waited for).  D own chunks per pass keep the buffers static.
     auto own = [&](HotRows& r, Words& w, uint32_t j) {
       stage(r, j);
       decode(w);
-      advance(kProducers);
       load_words(w);
+      advance(kProducers);
       load_rows(r);
     };
     uint32_t j = p;
-    for (; j + kProducers < total; j += 2 * kProducers) {  // one exit: both halves always run
-      own(ra, wa, j);
-      own(rb, wb, j + kProducers);
+    for (; j + (kDepth - 1) * kProducers < total; j += kDepth * kProducers) {  // one exit: every part runs
+#pragma unroll
+      for (uint32_t k = 0; k < kDepth; ++k) own(rows[k], words[k], j + k * kProducers);
     }
-    if (j < total) stage(ra, j);
+#pragma unroll
+    for (uint32_t k = 0; k + 1 < kDepth; ++k)
+      if (j + k * kProducers < total) stage(rows[k], j + k * kProducers);
   }
   if (stalled) st.err |= EPS_HIP_STATUS_STALLED;
   FinishBlock<kHotBlock / kWave>(st, ctrl, a.bounds, write);
