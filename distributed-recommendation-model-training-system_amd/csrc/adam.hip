@@ -39,63 +39,126 @@ namespace {
 constexpr uint32_t kFallbackGrid = 2048;
 
 // ---------------------------------------------------------------------------
-// Gradient maximum (GradMaxKernel).  A guarded input array: gradient values,
-// reference scales, or 64-bit indices that must all be below `limit` (checked
-// before anything is written).
-enum SpanKind : uint32_t { kGradientSpan = 0, kScaleSpan = 1, kIndexSpan = 2 };
+// Gradient scan (GradMaxKernel), the first kernel of an update.  Its spans are
+// the guarded input arrays: gradient values, reference scales, 64-bit caller
+// indices that must all be below `limit`, and (a push) the sorted keys and
+// reference words of the prepared workspace, whose table indices, slots,
+// features and gradient rows must name the push's tables and gradients.  It
+// records max |gradient| and max |scale| for the guard and any range failure
+// as a prepare-time finding, all before anything is written; block 0 also
+// copies the bounds-domain maxima into the control block, the snapshot the
+// guard decides from.
+enum SpanKind : uint32_t { kGradientSpan = 0, kScaleSpan = 1, kIndexSpan = 2, kSortedSpan = 3 };
 struct Span {
   const float* p;
   uint64_t count;
   uint32_t block_begin, kind;
   uint64_t limit;
 };
+// What the sorted span is checked against (key index order for tables).
+struct SortedCheck {
+  const uint32_t* keys;
+  const uint64_t* rs;
+  uint64_t table_rows[EPS_HIP_MAX_TABLES];
+  uint64_t feature_rows[EPS_HIP_MAX_FEATURES];
+  uint32_t row_bits, tables, features;
+};
 struct GuardArgs {
-  Span span[EPS_HIP_MAX_FEATURES + 1];
+  Span span[EPS_HIP_MAX_FEATURES + 4];
   uint32_t spans;
   Control* ctrl;
+  const Bounds* bounds;  // snapshot source (NULL: no snapshot)
+  SortedCheck sorted;
 };
-constexpr uint32_t kMaxItems = 16;  // float4 per thread per block
+static_assert(sizeof(GuardArgs) <= 4096, "gradient scan arguments fit the kernel-argument segment");
+constexpr uint32_t kMaxItems = 4;      // float4 per thread per block (all issued before any is used)
+constexpr uint32_t kSortedItems = 8;   // sorted positions per thread per block
 
 __global__ void __launch_bounds__(kBlock) GradMaxKernel(GuardArgs a) {
+  __shared__ uint32_t s_max[4];
+  __shared__ uint64_t s_rows[EPS_HIP_MAX_TABLES + EPS_HIP_MAX_FEATURES];
+  if (blockIdx.x == 0 && threadIdx.x < kWave && a.bounds) {
+    const uint32_t lane = threadIdx.x;
+    const uint32_t w = WaveMax(a.bounds->v[lane][0]), m = WaveMax(a.bounds->v[lane][1]),
+                   v = WaveMax(a.bounds->v[lane][2]);
+    if (lane == 0) {
+      a.ctrl->snap[0] = w;
+      a.ctrl->snap[1] = m;
+      a.ctrl->snap[2] = v;
+    }
+  }
+  if (!a.spans) return;
   const Span sp = a.span[PartOf(a.span, a.spans)];
-  const uint64_t per_block = uint64_t(kBlock) * kMaxItems * 4;
-  const uint64_t begin = uint64_t(blockIdx.x - sp.block_begin) * per_block;
-  const uint64_t end = min(begin + per_block, sp.count);
   uint32_t m = 0;
   uint32_t found = 0;  // prepare-status bits this thread found
-  if (sp.kind == kIndexSpan) {
+  if (sp.kind == kSortedSpan) {
+    const SortedCheck& c = a.sorted;
+    for (uint32_t i = threadIdx.x; i < EPS_HIP_MAX_TABLES + EPS_HIP_MAX_FEATURES; i += kBlock)
+      s_rows[i] = i < EPS_HIP_MAX_TABLES ? c.table_rows[i] : c.feature_rows[i - EPS_HIP_MAX_TABLES];
+    __syncthreads();
+    // Positions past the valid count hold keys of rows not on this device,
+    // which no update kernel reads.
+    const uint64_t valid = min<uint64_t>(sp.count, a.ctrl->valid_count);
+    const uint64_t per_block = uint64_t(kBlock) * kSortedItems;
+    const uint64_t begin = uint64_t(blockIdx.x - sp.block_begin) * per_block;
+    uint32_t key[kSortedItems];
+    uint64_t word[kSortedItems];
+#pragma unroll
+    for (uint32_t k = 0; k < kSortedItems; ++k) {
+      const uint64_t i = begin + uint64_t(k) * kBlock + threadIdx.x;
+      key[k] = i < valid ? c.keys[i] : 0u;
+      word[k] = i < valid ? c.rs[i] : 0ull;
+    }
+#pragma unroll
+    for (uint32_t k = 0; k < kSortedItems; ++k) {
+      const uint64_t i = begin + uint64_t(k) * kBlock + threadIdx.x;
+      if (i >= valid) continue;
+      const KeyParts kp = SplitKey(key[k], c.row_bits);
+      const RefParts rp = SplitRef(word[k]);
+      const bool ok = KeyInRange(kp, c.tables, s_rows[min(kp.table, EPS_HIP_MAX_TABLES - 1u)]) &&
+                      RefInRange(rp, c.features, s_rows[EPS_HIP_MAX_TABLES + min(rp.feature,
+                                                                                  EPS_HIP_MAX_FEATURES - 1u)]);
+      if (!ok) found = EPS_HIP_STATUS_BAD_INDEX;
+    }
+  } else if (sp.kind == kIndexSpan) {
+    const uint64_t per_block = uint64_t(kBlock) * kMaxItems * 4;
+    const uint64_t begin = uint64_t(blockIdx.x - sp.block_begin) * per_block;
+    const uint64_t end = min(begin + per_block, sp.count);
     const uint64_t* idx = reinterpret_cast<const uint64_t*>(sp.p);
     for (uint64_t i = begin + threadIdx.x; i < end; i += kBlock)
       if (idx[i] >= sp.limit) found = EPS_HIP_STATUS_BAD_INDEX;
-  } else if (reinterpret_cast<uintptr_t>(sp.p) % 16 == 0) {
-    // All kMaxItems loads of a thread are issued before any is consumed.
-    const uint64_t vend = begin + ((end - begin) & ~uint64_t(3));
-    float4 x[kMaxItems];
-#pragma unroll
-    for (uint32_t k = 0; k < kMaxItems; ++k) {
-      const uint64_t i = begin + (uint64_t(k) * kBlock + threadIdx.x) * 4;
-      x[k] = i < vend ? Load4(sp.p + i) : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    uint32_t neg = 0;  // any value below zero (not -0.0)
-#pragma unroll
-    for (uint32_t k = 0; k < kMaxItems; ++k) {
-      m = max(m, max(max(AbsBits(x[k].x), AbsBits(x[k].y)), max(AbsBits(x[k].z), AbsBits(x[k].w))));
-      neg |= (x[k].x < 0.f) | (x[k].y < 0.f) | (x[k].z < 0.f) | (x[k].w < 0.f);
-    }
-    for (uint64_t i = vend + threadIdx.x; i < end; i += kBlock) {
-      m = max(m, AbsBits(sp.p[i]));
-      neg |= sp.p[i] < 0.f;
-    }
-    if (sp.kind == kScaleSpan && neg) found = EPS_HIP_STATUS_BAD_SCALE;
   } else {
-    for (uint64_t i = begin + threadIdx.x; i < end; i += kBlock) {
-      m = max(m, AbsBits(sp.p[i]));
-      if (sp.kind == kScaleSpan && sp.p[i] < 0.f) found = EPS_HIP_STATUS_BAD_SCALE;
+    const uint64_t per_block = uint64_t(kBlock) * kMaxItems * 4;
+    const uint64_t begin = uint64_t(blockIdx.x - sp.block_begin) * per_block;
+    const uint64_t end = min(begin + per_block, sp.count);
+    if (reinterpret_cast<uintptr_t>(sp.p) % 16 == 0) {
+      const uint64_t vend = begin + ((end - begin) & ~uint64_t(3));
+      float4 x[kMaxItems];
+#pragma unroll
+      for (uint32_t k = 0; k < kMaxItems; ++k) {
+        const uint64_t i = begin + (uint64_t(k) * kBlock + threadIdx.x) * 4;
+        x[k] = i < vend ? Load4(sp.p + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+      uint32_t neg = 0;  // any value below zero (not -0.0)
+#pragma unroll
+      for (uint32_t k = 0; k < kMaxItems; ++k) {
+        m = max(m, max(max(AbsBits(x[k].x), AbsBits(x[k].y)), max(AbsBits(x[k].z), AbsBits(x[k].w))));
+        neg |= (x[k].x < 0.f) | (x[k].y < 0.f) | (x[k].z < 0.f) | (x[k].w < 0.f);
+      }
+      for (uint64_t i = vend + threadIdx.x; i < end; i += kBlock) {
+        m = max(m, AbsBits(sp.p[i]));
+        neg |= sp.p[i] < 0.f;
+      }
+      if (sp.kind == kScaleSpan && neg) found = EPS_HIP_STATUS_BAD_SCALE;
+    } else {
+      for (uint64_t i = begin + threadIdx.x; i < end; i += kBlock) {
+        m = max(m, AbsBits(sp.p[i]));
+        if (sp.kind == kScaleSpan && sp.p[i] < 0.f) found = EPS_HIP_STATUS_BAD_SCALE;
+      }
     }
+    // A compact scale must be finite and >= 0 (compact_gradients.cpp:21).
+    if (sp.kind == kScaleSpan && m >= 0x7f800000u) found = EPS_HIP_STATUS_BAD_SCALE;
   }
-  // A compact scale must be finite and >= 0 (compact_gradients.cpp:21).
-  if (sp.kind == kScaleSpan && m >= 0x7f800000u) found = EPS_HIP_STATUS_BAD_SCALE;
-  __shared__ uint32_t s_max[4];
   if (found) atomicOr(&a.ctrl->prep_status, found);
   m = WaveMax(m);
   if ((threadIdx.x & (kWave - 1)) == 0) s_max[threadIdx.x / kWave] = m;
@@ -112,6 +175,7 @@ __global__ void __launch_bounds__(kBlock) GradMaxKernel(GuardArgs a) {
 // Shared per-row arithmetic.
 struct TableDesc {
   float* state;
+  uint64_t rows;     // slots of the table (sorted keys must name one)
   uint32_t dim;
   float beta1, beta2, omb1, omb2, lr, eps, lo, hi;
   uint32_t bounded;  // lo/hi are the table's weight bounds (else -FLT_MAX/FLT_MAX)
@@ -210,22 +274,22 @@ __device__ __forceinline__ void Accumulate4(float4& acc, float4 x, float s) {
 }
 
 // The guard decision (see the file comment), made by every block of the first
-// kernel of an update from the gradient maxima, the prepare-time findings and
-// the bounds domain -- all written by earlier kernels, so every block reads
-// the same values and decides the same.  Block 0 publishes the mode and the
-// status bits for the kernels after it.  Runs in wavefront 0 (one bounds slot
-// and one gradient slot per lane); returns the mode to every thread.
-static_assert(kBoundSlots == kWave && kSrcSlots == kWave, "one guard slot per lane");
+// kernel of an update from inputs that earlier kernels wrote and nothing
+// changes while the update runs: the gradient maxima, the prepare-time
+// findings and the bounds snapshot the gradient scan took (never the live
+// bounds domain, which the update's own finished blocks raise).  So every
+// block -- of either kernel, when two decide on two streams -- takes the same
+// decision.  Block 0 publishes the mode and the status bits for the kernels
+// after it.  Runs in wavefront 0 (one gradient slot and one table per lane);
+// returns the mode to every thread.
+static_assert(kSrcSlots == kWave, "one guard slot per lane");
 struct GuardScalars {
   uint64_t refs;       // references summed into one reduced gradient, at most; 0: the prepared count
   uint32_t tables;
 };
-__device__ uint32_t DecideBlock(Control* ctrl, const Bounds* bounds, const TableDesc* t,
-                                const GuardScalars& gs, uint32_t* s_mode) {
+__device__ uint32_t DecideBlock(Control* ctrl, const TableDesc* t, const GuardScalars& gs, uint32_t* s_mode) {
   if (threadIdx.x < kWave) {
     const uint32_t lane = threadIdx.x;
-    const uint32_t wb = WaveMax(bounds->v[lane][0]), mb = WaveMax(bounds->v[lane][1]),
-                   vb = WaveMax(bounds->v[lane][2]);
     const uint32_t gb = WaveMax(ctrl->src_slots[lane]);
     const uint32_t scale_bits = WaveMax(ctrl->scale_slots[lane]);
     uint32_t status = ctrl->prep_status;
@@ -239,20 +303,16 @@ __device__ uint32_t DecideBlock(Control* ctrl, const Bounds* bounds, const Table
       status |= EPS_HIP_STATUS_BAD_SCALE;
       mode = kReject;
     } else {
-      const double W = __uint_as_float(wb), M = __uint_as_float(mb), V = __uint_as_float(vb);
+      const double W = __uint_as_float(ctrl->snap[0]), M = __uint_as_float(ctrl->snap[1]),
+                   V = __uint_as_float(ctrl->snap[2]);
       const double refs = double(gs.refs ? gs.refs : uint64_t(ctrl->valid_count));
-      const double scale = fmax(1.0, double(__uint_as_float(scale_bits)));
-      const double G = double(__uint_as_float(gb)) * scale * refs * exp((refs + 2.0) * 0x1.0p-24) * 1.01;
+      const double G = GuardGradBound(__uint_as_float(gb), __uint_as_float(scale_bits), refs);
       bool table_safe = true;  // one table per lane
       if (lane < gs.tables) {
         const TableDesc& T = t[lane];
-        const double b1 = T.beta1, b2 = T.beta2;
-        const double mbound = (b1 * M + (1.0 - b1) * G) * 1.01;
-        const double vbound = (b2 * V + (1.0 - b2) * G * G) * 1.01;
-        const double wbound = (W + double(T.lr) * mbound / double(T.eps)) * 1.01;
-        table_safe = mbound < 1e30 && vbound < 1e30 && wbound < 1e30 && double(T.eps) > 0.0;
+        table_safe = GuardTableSafe(T.beta1, T.beta2, T.lr, T.eps, W, M, V, G);
       }
-      if (!(G < 1e30) || __ballot(!table_safe) != 0) {
+      if (!(G < kGuardLimit) || __ballot(!table_safe) != 0) {
         mode = kChecked;
         status |= EPS_HIP_STATUS_CHECKED_PATH;
       }
@@ -278,11 +338,11 @@ enum Role : uint32_t { kDecide = 0, kFollow = 1, kFallback = 2 };
 
 // Whether this launch has work, and whether it writes (uniform over the
 // block).  s_t must hold the launch's tables; every thread calls it.
-__device__ bool LaunchGate(Control* ctrl, const Bounds* bounds, const TableDesc* s_t,
-                           const GuardScalars& gs, uint32_t role, uint32_t* s_mode, bool& write) {
+__device__ bool LaunchGate(Control* ctrl, const TableDesc* s_t, const GuardScalars& gs, uint32_t role,
+                           uint32_t* s_mode, bool& write) {
   if (role == kDecide) {
     __syncthreads();  // s_t is staged
-    const uint32_t mode = DecideBlock(ctrl, bounds, s_t, gs, s_mode);
+    const uint32_t mode = DecideBlock(ctrl, s_t, gs, s_mode);
     write = mode == kFused;
     return mode != kReject;
   }
@@ -338,6 +398,7 @@ __device__ void FinishBlock(const RowStats& st, Control* ctrl, Bounds* bounds, b
 struct FusedArgs {
   TableDesc t[EPS_HIP_MAX_TABLES];   // by key index
   const float* grad[EPS_HIP_MAX_FEATURES];
+  uint64_t grad_rows[EPS_HIP_MAX_FEATURES];
   const uint32_t* keys;
   const uint64_t* rs;
   const uint32_t* vals;              // reduce mode: sorted occurrence indices
@@ -347,8 +408,10 @@ struct FusedArgs {
   Control* ctrl;
   Bounds* bounds;
   GuardScalars gs;
-  uint32_t row_bits, cls, cls_end, log2g, ppb, vblocks, role, reduce, tables;  // classes [cls, cls_end)
+  uint32_t row_bits, cls, cls_end, log2g, ppb, vblocks, role, reduce, tables, features;  // classes [cls, cls_end)
+  uint32_t n;  // occurrences of the push (sorted positions, occurrence indices)
 };
+static_assert(sizeof(FusedArgs) <= 4096, "update arguments fit the kernel-argument segment");
 
 template <bool kGeneric>
 __global__ void __launch_bounds__(kBlock) SortedUpdateKernel(FusedArgs a) {
@@ -357,17 +420,18 @@ __global__ void __launch_bounds__(kBlock) SortedUpdateKernel(FusedArgs a) {
   __shared__ uint32_t s_heads[kBlock];
   __shared__ uint32_t s_wave_heads[4];
   __shared__ uint32_t s_mode;
+  __shared__ uint64_t s_rows[EPS_HIP_MAX_FEATURES];  // gradient rows per feature
   CopyWords(s_t, a.t, sizeof(a.t));
   CopyWords(s_grad, a.grad, sizeof(a.grad));
+  CopyWords(s_rows, a.grad_rows, sizeof(a.grad_rows));
   Control* ctrl = a.ctrl;
   bool write = true;
-  if (!a.reduce && !LaunchGate(ctrl, a.bounds, s_t, a.gs, a.role, &s_mode, write)) return;
+  if (!a.reduce && !LaunchGate(ctrl, s_t, a.gs, a.role, &s_mode, write)) return;
   const uint32_t start = ctrl->class_start[a.cls];
   const uint32_t end = ctrl->class_start[a.cls_end];
   const uint32_t G = kGeneric ? kWave : (1u << a.log2g);
   const uint32_t lig = threadIdx.x & (G - 1);
   const uint32_t gid = threadIdx.x / G, ngroups = kBlock / G;
-  const uint32_t row_mask = (1u << a.row_bits) - 1;
   const uint32_t lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   RowStats st;
   __syncthreads();
@@ -390,10 +454,19 @@ __global__ void __launch_bounds__(kBlock) SortedUpdateKernel(FusedArgs a) {
       const uint32_t sb = s_heads[h];
       const uint32_t key = a.keys[sb];
       const uint32_t se = h + 1 < nheads ? s_heads[h + 1] : SegmentEndSearch(a.keys, p1, end, key);
-      const TableDesc& T = s_t[key >> a.row_bits];
-      const uint64_t slot = key & row_mask;
+      // A key or reference naming nothing of the push (a damaged workspace)
+      // is not used as an address: its loads read zero and the row is not
+      // written.  The reference checks see the same words in every lane.
+      const KeyParts kp = SplitKey(key, a.row_bits);
+      const TableDesc& T = s_t[min(kp.table, a.tables - 1)];
+      bool ok = KeyInRange(kp, a.tables, T.rows) && (!a.reduce || a.vals[sb] < a.n);
+      const uint64_t slot = ok ? kp.slot : 0;
       const uint32_t dim = T.dim;
-      const uint64_t u = a.reduce ? a.occ2u[a.vals[sb]] : 0;
+      const uint64_t u = a.reduce && ok ? a.occ2u[a.vals[sb]] : 0;
+      auto ref_ok = [&](uint64_t w) {
+        const RefParts rp = SplitRef(w);
+        return RefInRange(rp, a.features, s_rows[min(rp.feature, a.features - 1)]);
+      };
       if (!kGeneric) {
         const uint32_t c = lig * 4;
         const bool active = c < dim;
@@ -409,16 +482,19 @@ __global__ void __launch_bounds__(kBlock) SortedUpdateKernel(FusedArgs a) {
               const uint64_t w = __shfl(my, int(k + q), int(G));
               const uint32_t ref = uint32_t(w);
               s[q] = __uint_as_float(uint32_t(w >> 32));
+              const bool in = k + q < cnt && ref_ok(w);
+              if (k + q < cnt && !in) ok = false;
               const float* src = s_grad[ref >> kRefRowBits] +
                                  uint64_t(ref & ((1u << kRefRowBits) - 1)) * dim + c;
-              x[q] = (k + q < cnt && active) ? Load4(src) : make_float4(0.f, 0.f, 0.f, 0.f);
+              x[q] = (in && active) ? Load4(src) : make_float4(0.f, 0.f, 0.f, 0.f);
             }
 #pragma unroll
             for (uint32_t q = 0; q < 4; ++q)
               if (k + q < cnt) Accumulate4(acc, x[q], s[q]);
           }
         }
-        if (!active) continue;
+        if (!ok) st.err |= EPS_HIP_STATUS_BAD_INDEX;
+        if (!active || !ok) continue;
         if (a.reduce) {
           if (!(Finite(acc.x) && Finite(acc.y) && Finite(acc.z) && Finite(acc.w)))
             st.err |= EPS_HIP_STATUS_REDUCE_OVERFLOW;
@@ -438,13 +514,16 @@ __global__ void __launch_bounds__(kBlock) SortedUpdateKernel(FusedArgs a) {
               const uint64_t w = __shfl(my, int(k), int(kWave));
               const uint32_t ref = uint32_t(w);
               const float s = __uint_as_float(uint32_t(w >> 32));
+              const bool in = ref_ok(w);
+              if (!in) ok = false;
               const float* src = s_grad[ref >> kRefRowBits] +
                                  uint64_t(ref & ((1u << kRefRowBits) - 1)) * dim;
-              const float x = active ? LoadF(src + c) : 0.f;
+              const float x = active && in ? LoadF(src + c) : 0.f;
               acc = acc + x * s;
             }
           }
-          if (!active) continue;
+          if (!ok) st.err |= EPS_HIP_STATUS_BAD_INDEX;
+          if (!active || !ok) continue;
           if (a.reduce) {
             if (!Finite(acc)) st.err |= EPS_HIP_STATUS_REDUCE_OVERFLOW;
             a.reduce_out[u * a.reduce_stride + c] = acc;
@@ -507,15 +586,18 @@ constexpr uint32_t kRefBatch = 4;                       // gradient rows in flig
 struct VecArgs {
   TableDesc t[EPS_HIP_MAX_TABLES];   // by key index
   const float* grad[EPS_HIP_MAX_FEATURES];
+  uint64_t grad_rows[EPS_HIP_MAX_FEATURES];
   const uint32_t* keys;
   const uint64_t* rs;
   const HotEntry* hot;
   Control* ctrl;
   Bounds* bounds;
   GuardScalars gs;
-  uint32_t row_bits, cls, role, slice_bits, hot_capacity;
+  uint32_t row_bits, cls, role, slice_bits, hot_capacity, tables, features;
+  uint32_t n;           // sorted positions of the push (hot-row entries are clamped to them)
   uint32_t spin_limit;  // polls of a hot-row hand-over wait (0: give up at once)
 };
+static_assert(sizeof(VecArgs) <= 4096, "update arguments fit the kernel-argument segment");
 
 // Position of (column c, reference r) in a hot-row tile.  Groups of four
 // references are rotated by the column's 16-column group (XOR; the identity
@@ -537,10 +619,11 @@ __device__ __forceinline__ const float* RefSource(const float* const* grad, uint
 // returns false when it has nothing to do (uniform over the block).
 template <uint32_t kThreads = kBlock>
 __device__ __forceinline__ bool VecPrologue(const VecArgs& a, TableDesc* s_t, const float** s_grad,
-                                            uint32_t* s_mode, bool& write) {
+                                            uint32_t* s_mode, bool& write, uint64_t* s_rows) {
   CopyWords<kThreads>(s_t, a.t, sizeof(a.t));
   CopyWords<kThreads>(s_grad, a.grad, sizeof(a.grad));
-  return LaunchGate(a.ctrl, a.bounds, s_t, a.gs, a.role, s_mode, write);
+  CopyWords<kThreads>(s_rows, a.grad_rows, sizeof(a.grad_rows));
+  return LaunchGate(a.ctrl, s_t, a.gs, a.role, s_mode, write);
 }
 
 // One chunk of a hot work unit: positions [cbase, cbase + kHotChunk) of the
@@ -611,14 +694,18 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
   __shared__ uint32_t s_ready[kHotRing], s_used[kHotRing];
   __shared__ uint4 s_unit[kUnitCache];  // {start, end, key, col0} of the block's first units
   __shared__ uint32_t s_mode;
+  // Set when a hot-row entry, key or reference names nothing of the push (a
+  // damaged workspace): the block writes nothing from then on.
+  __shared__ uint32_t s_bad;
+  __shared__ uint64_t s_rows[EPS_HIP_MAX_FEATURES];  // gradient rows per feature
   bool write = false;
-  if (!VecPrologue<kHotBlock>(a, s_t, s_grad, &s_mode, write)) return;
+  if (!VecPrologue<kHotBlock>(a, s_t, s_grad, &s_mode, write, s_rows)) return;
   if (threadIdx.x < kHotRing) {
     s_ready[threadIdx.x] = 0;
     s_used[threadIdx.x] = 0;
   }
+  if (threadIdx.x == 0) s_bad = 0;
   Control* ctrl = a.ctrl;
-  const uint32_t row_mask = (1u << a.row_bits) - 1;
   const uint32_t lane = threadIdx.x & (kWave - 1);
   const uint32_t wave = uint32_t(__builtin_amdgcn_readfirstlane(int(threadIdx.x / kWave)));
   RowStats st;
@@ -637,12 +724,20 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
   uint32_t units = 0;
 #pragma unroll
   for (uint32_t b = 0; b < kHotBuckets; ++b) {
-    units += uint32_t(__builtin_amdgcn_readfirstlane(int(ctrl->long_count[xcd * kHotBuckets + b])))
-             << a.slice_bits;
+    const uint32_t count = uint32_t(__builtin_amdgcn_readfirstlane(int(ctrl->long_count[xcd * kHotBuckets + b])));
+    units += min(count, a.hot_capacity) << a.slice_bits;
     bucket_end[b] = units;
   }
   // The block's unit u of round r, and where its hot-row entry lies.
   auto unit_of = [&](uint32_t r) { return r * xcd_blocks + ((r & 1) ? xcd_blocks - 1 - me : me); };
+  // An entry's positions, kept inside the push's sorted positions (start < end
+  // <= n), so a damaged list can neither read past them nor run unbounded.
+  auto sane = [&](uint32_t& start, uint32_t& end) {
+    if (start < end && end <= a.n) return true;
+    start = min(start, a.n - 1);
+    end = min(max(end, start + 1), a.n);
+    return false;
+  };
   auto entry_of = [&](uint32_t u, uint32_t& col0) {
     uint32_t b = 0;
 #pragma unroll
@@ -660,7 +755,8 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
     const uint32_t u = unit_of(r);
     if (u < units) {
       uint32_t col0;
-      const HotEntry e = a.hot[entry_of(u, col0)];
+      HotEntry e = a.hot[entry_of(u, col0)];
+      if (!sane(e.start, e.end)) s_bad = 1;
       s_unit[r] = make_uint4(e.start, e.end, e.key, col0);
     }
   }
@@ -685,11 +781,13 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
     }
     const auto& e = hot[entry_of(u, next_col0)];
     next_entry = HotEntry{e.start, e.end, e.key, 0u};
+    if (!sane(next_entry.start, next_entry.end)) s_bad = 1;
   };
   auto take = [&]() {  // the next unit's first chunk; slices past a row's dimension are skipped
     for (;;) {
       HotSlot t{next_entry.start, next_entry.end, next_entry.key, next_col0, next_entry.start, next_ok};
-      const uint32_t dim = uint32_t(__builtin_amdgcn_readfirstlane(int(s_t[next_entry.key >> a.row_bits].dim)));
+      const uint32_t dim = uint32_t(__builtin_amdgcn_readfirstlane(
+          int(s_t[min(next_entry.key >> a.row_bits, a.tables - 1)].dim)));
       const bool usable = !next_ok || next_col0 < dim;
       fetch();
       if (usable) return t;
@@ -761,11 +859,13 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
         __hip_atomic_store(&s_used[t], j / kHotRing + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       __builtin_amdgcn_sched_barrier(0);
       if (c.cbase + kHotChunk >= c.end) {  // the unit's last chunk
-        const TableDesc& T = s_t[c.key >> a.row_bits];
+        const KeyParts kp = SplitKey(c.key, a.row_bits);
+        const TableDesc& T = s_t[min(kp.table, a.tables - 1)];
+        if (!KeyInRange(kp, a.tables, T.rows)) s_bad = 1;
         if (lane < kSlice && c.col0 + lane < T.dim && !stalled) {
           AdamElement(T, acc, w, m, v, st);
-          if (write) {
-            float* row = T.state + uint64_t(c.key & row_mask) * T.dim * 3 + c.col0 + lane;
+          if (write && !s_bad) {
+            float* row = T.state + uint64_t(kp.slot) * T.dim * 3 + c.col0 + lane;
             StoreF(row, w); StoreF(row + T.dim, m); StoreF(row + 2 * T.dim, v);
           }
         }
@@ -821,7 +921,7 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
     HotSlot dc{};  // chunk whose references are in the LDS slots
     auto load_words = [&](Words& w) {
       w.c = cur;
-      const uint32_t pos = cur.ok ? min(cur.cbase + lane, cur.end - 1) : 0u;
+      const uint32_t pos = cur.ok ? min(cur.cbase + lane, cur.end - 1) : 0u;  // end <= n (sane)
       w.word = a.rs[pos];
     };
     // Lane l decodes the word of reference l: its gradient row (from the
@@ -829,10 +929,13 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
     auto decode = [&](const Words& w) {
       const HotSlot& wc = w.c;
       dc = wc;
-      const TableDesc& T = s_t[wc.key >> a.row_bits];
+      const TableDesc& T = s_t[min(wc.key >> a.row_bits, a.tables - 1)];
+      const RefParts rp = SplitRef(w.word);
+      const bool ref_ok = RefInRange(rp, a.features, s_rows[min(rp.feature, a.features - 1)]);
+      if (wc.ok && !ref_ok) s_bad = 1;
       float scale;
       const float* src = RefSource(s_grad, w.word, T.dim, wc.col0, scale);
-      slots.src[lane % kHotRefsPerLoad][lane / kHotRefsPerLoad] = wc.ok ? src : idle;
+      slots.src[lane % kHotRefsPerLoad][lane / kHotRefsPerLoad] = wc.ok && ref_ok ? src : idle;
       slots.scale[lane % kHotRefsPerLoad][lane / kHotRefsPerLoad] = scale;
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
       __builtin_amdgcn_wave_barrier();
@@ -842,7 +945,9 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
     // columns; their products are never stored by the adding wave.
     auto load_rows = [&](HotRows& r) {
       r.c = dc;
-      const TableDesc& T = s_t[dc.key >> a.row_bits];
+      const KeyParts kp = SplitKey(dc.key, a.row_bits);
+      const TableDesc& T = s_t[min(kp.table, a.tables - 1)];
+      const bool key_ok = KeyInRange(kp, a.tables, T.rows);
       const uint32_t dim = T.dim;
       const uint32_t off = dc.col0 + 4 * quad < dim ? 4 * quad : 0u;
       const uint32_t step = dc.ok ? off : 0u;
@@ -861,8 +966,8 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
 #pragma unroll
       for (uint32_t k = 0; k < kHotLoads; ++k) r.x[k] = Load4(src[k] + step);
       const uint32_t wcol = dc.col0 + (lane < kSlice && dc.col0 + lane < dim ? lane : 0u);
-      const float* row = dc.ok ? T.state + uint64_t(dc.key & row_mask) * dim * 3 + wcol : idle;
-      const uint32_t ms = dc.ok ? dim : 0u;
+      const float* row = dc.ok && key_ok ? T.state + uint64_t(kp.slot) * dim * 3 + wcol : idle;
+      const uint32_t ms = dc.ok && key_ok ? dim : 0u;
       r.wmv[0] = LoadF(row); r.wmv[1] = LoadF(row + ms); r.wmv[2] = LoadF(row + 2 * ms);
     };
     auto stage = [&](const HotRows& r, uint32_t j) {
@@ -942,6 +1047,8 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
       if (j + k * kProducers < total) stage(rows[k], j + k * kProducers);
   }
   if (stalled) st.err |= EPS_HIP_STATUS_STALLED;
+  __syncthreads();
+  if (s_bad) st.err |= EPS_HIP_STATUS_BAD_INDEX;
   FinishBlock<kHotBlock / kWave>(st, ctrl, a.bounds, write);
 }
 
@@ -962,10 +1069,14 @@ RowRunKernel(VecArgs a) {
   __shared__ uint32_t s_heads[kWindow];
   __shared__ uint32_t s_wave_heads[kBlock / kWave];
   __shared__ uint32_t s_next;               // next unclaimed row (head index) of the window
-  __shared__ uint32_t s_mode;
+  __shared__ uint32_t s_mode, s_bad;
+  __shared__ uint64_t s_rows[EPS_HIP_MAX_FEATURES];  // gradient rows per feature
   bool write = false;
-  if (!VecPrologue(a, s_t, s_grad, &s_mode, write)) return;
+  if (!VecPrologue(a, s_t, s_grad, &s_mode, write, s_rows)) return;
   Control* ctrl = a.ctrl;
+  // Safe address for reads a damaged workspace would point elsewhere: the
+  // control block and what follows it (far more than a row of 3 x 256 floats).
+  const float* safe = reinterpret_cast<const float*>(a.ctrl);
   const uint32_t begin = ctrl->class_start[a.cls], end = ctrl->class_start[a.cls + 1];
   const uint32_t row_mask = (1u << a.row_bits) - 1;
   const uint32_t lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
@@ -980,6 +1091,7 @@ RowRunKernel(VecArgs a) {
   const uint32_t xcd = blockIdx.x % kXcds, per_xcd = gridDim.x / kXcds;
   const uint32_t span = ((end - begin + kXcds - 1) / kXcds + kWindow - 1) / kWindow * kWindow;
   const uint32_t xbegin = min(begin + xcd * span, end), xend = min(xbegin + span, end);
+  if (threadIdx.x == 0) s_bad = 0;
   __syncthreads();
   for (uint32_t p0 = xbegin + (blockIdx.x / kXcds) * kWindow; p0 < xend; p0 += per_xcd * kWindow) {
     const uint32_t p1 = min(p0 + kWindow, xend);
@@ -995,12 +1107,24 @@ RowRunKernel(VecArgs a) {
     }
     for (uint32_t i = threadIdx.x; i < staged; i += kBlock) {
       const uint32_t key = a.keys[p0 + i];
+      const uint64_t word = a.rs[p0 + i];
       s_key[i + 1] = key;
+      // A key or reference that names no table, slot, feature or gradient row
+      // of the push (a damaged workspace) is read from a safe address instead,
+      // and the block writes nothing from then on.
+      const KeyParts kp = SplitKey(key, a.row_bits);
+      const RefParts rp = SplitRef(word);
+      const uint32_t ti = min(kp.table, a.tables - 1);
+      const uint32_t fi = min(rp.feature, a.features - 1);
+      const bool ok = KeyInRange(kp, a.tables, s_t[ti].rows) && RefInRange(rp, a.features, s_rows[fi]);
       float scale;
-      s_src[i] = RefSource(s_grad, a.rs[p0 + i], s_t[key >> a.row_bits].dim, 0, scale);
+      const float* src = RefSource(s_grad, word, s_t[ti].dim, 0, scale);
+      s_src[i] = ok ? src : safe;
       s_scale[i] = scale;
+      if (!ok) s_bad = 1;
     }
     __syncthreads();
+    const bool window_ok = s_bad == 0;
     const bool head = threadIdx.x < p1 - p0 && s_key[threadIdx.x + 1] != s_key[threadIdx.x];
     const uint64_t ballot = __ballot(head);
     if (lane == 0) s_wave_heads[wave] = uint32_t(__popcll(ballot));
@@ -1026,11 +1150,11 @@ RowRunKernel(VecArgs a) {
       }
       uint32_t se = h + 1 < nheads ? s_heads[h + 1] : p1 - p0;
       while (se < staged && s_key[se + 1] == key) ++se;
-      const TableDesc& T = s_t[key >> a.row_bits];
+      const TableDesc& T = s_t[min(key >> a.row_bits, a.tables - 1)];
       const uint32_t dim = T.dim;
       const bool active = c < dim;
       const uint32_t cl = active ? c : 0;  // inactive lanes read column 0 and drop it
-      float* row = T.state + uint64_t(key & row_mask) * dim * 3;
+      float* row = window_ok ? T.state + uint64_t(key & row_mask) * dim * 3 : const_cast<float*>(safe);
       const float4 w0 = Load4Stream(row + cl), m0 = Load4Stream(row + dim + cl),
                    v0 = Load4Stream(row + 2 * dim + cl);
       float4 g = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -1069,7 +1193,7 @@ RowRunKernel(VecArgs a) {
           AdamElement<false>(T, g.z, w.z, m.z, v.z, st);
           AdamElement<false>(T, g.w, w.w, m.w, v.w, st);
         }
-        if (write) {
+        if (write && window_ok) {
           Store4Stream(row + c, w);
           Store4Stream(row + dim + c, m);
           Store4Stream(row + 2 * dim + c, v);
@@ -1078,6 +1202,7 @@ RowRunKernel(VecArgs a) {
       h = uint32_t(__shfl(int(claim), 0, int(G)));
     }
   }
+  if (s_bad) st.err |= EPS_HIP_STATUS_BAD_INDEX;
   FinishBlock(st, ctrl, a.bounds, write);
 }
 
@@ -1104,7 +1229,7 @@ __global__ void __launch_bounds__(kBlock) RowUpdateKernel(RowArgs a) {
   Control* ctrl = a.ctrl;
   if (threadIdx.x == 0) s_t[0] = a.t;
   bool write = false;
-  if (!LaunchGate(ctrl, a.bounds, s_t, a.gs, a.role, &s_mode, write)) return;
+  if (!LaunchGate(ctrl, s_t, a.gs, a.role, &s_mode, write)) return;
   const TableDesc T = a.t;
   const uint32_t dim = T.dim;
   const uint32_t G = kGeneric ? kWave : (1u << a.log2g);
@@ -1152,6 +1277,7 @@ __global__ void __launch_bounds__(kBlock) RowUpdateKernel(RowArgs a) {
 TableDesc MakeTable(const eps_hip_table& t, const eps_hip_optimizer& o) {
   TableDesc d;
   d.state = t.state;
+  d.rows = t.rows;
   d.dim = t.dim;
   d.beta1 = o.beta1;
   d.beta2 = o.beta2;
@@ -1185,17 +1311,17 @@ uint32_t Log2G(uint32_t dim) {
   return log2g;
 }
 
-// The gradient scan; the decision itself is made by the first kernel of the
-// update (DecideBlock), so nothing is launched when there is nothing to scan.
+// The gradient scan.  It always runs (one block at least), since its block 0
+// takes the bounds snapshot the guard decides from; the decision itself is
+// made by the first kernel of the update (DecideBlock).
 int LaunchGuard(const GuardArgs& g, uint64_t blocks, hipStream_t s) {
-  if (!blocks) return EPS_HIP_OK;
-  hipLaunchKernelGGL(GradMaxKernel, dim3(unsigned(blocks)), dim3(kBlock), 0, s, g);
+  hipLaunchKernelGGL(GradMaxKernel, dim3(unsigned(std::max<uint64_t>(blocks, 1))), dim3(kBlock), 0, s, g);
   EPS_HIP_LAUNCHED("gradient guard");
   return EPS_HIP_OK;
 }
 
-uint64_t SpanBlocks(uint64_t count) {
-  const uint64_t per = uint64_t(kBlock) * kMaxItems * 4;
+uint64_t SpanBlocks(uint64_t count, SpanKind kind = kGradientSpan) {
+  const uint64_t per = kind == kSortedSpan ? uint64_t(kBlock) * kSortedItems : uint64_t(kBlock) * kMaxItems * 4;
   return (count + per - 1) / per;
 }
 
@@ -1281,6 +1407,8 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
   a.row_bits = plan.row_bits;
   a.reduce = reduce ? 1 : 0;
   a.tables = table_count;
+  a.features = feature_count;
+  a.n = uint32_t(plan.occurrences);
   a.gs = GuardScalars{0, table_count};  // refs: the prepared valid count
   // The first kernel of the primary phase makes the guard decision.
   uint32_t role = kDecide;
@@ -1293,12 +1421,21 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
     else { o.learning_rate = 1; o.beta1 = 0; o.beta2 = 0; o.epsilon = 1; }
     a.t[k] = MakeTable(tables[t], o);
   }
-  for (uint32_t f = 0; f < feature_count; ++f) a.grad[f] = features[f].gradients;
+  for (uint32_t f = 0; f < feature_count; ++f) {
+    a.grad[f] = features[f].gradients;
+    a.grad_rows[f] = features[f].pooling == EPS_HIP_POOL_SEQUENCE ? features[f].occurrences : features[f].bags;
+  }
   if (!reduce) {
     // Vector classes: hot rows (sliced) first, then the other rows per class.
     VecArgs va{};
     for (uint32_t k = 0; k < table_count; ++k) va.t[k] = a.t[k];
-    for (uint32_t f = 0; f < feature_count; ++f) va.grad[f] = features[f].gradients;
+    for (uint32_t f = 0; f < feature_count; ++f) {
+      va.grad[f] = a.grad[f];
+      va.grad_rows[f] = a.grad_rows[f];
+    }
+    va.tables = table_count;
+    va.features = feature_count;
+    va.n = a.n;
     va.keys = a.keys;
     va.rs = a.rs;
     va.hot = reinterpret_cast<const HotEntry*>(ws + L.long_list);
@@ -1430,15 +1567,30 @@ int eps_hip_push_begin(const eps_hip_table* tables, const eps_hip_optimizer* opt
                         workspace_bytes, bounds, plan));
   GuardArgs g{};
   uint64_t blocks = 0;
+  auto add = [&](const void* p, uint64_t count, SpanKind kind) {
+    if (!count) return;
+    g.span[g.spans++] = Span{static_cast<const float*>(p), count, uint32_t(blocks), kind, 0};
+    blocks += SpanBlocks(count, kind);
+  };
   for (uint32_t f = 0; f < feature_count; ++f) {
     const auto& in = features[f];
     const uint64_t rows = in.pooling == EPS_HIP_POOL_SEQUENCE ? in.occurrences : in.bags;
-    const uint64_t count = rows * tables[in.table].dim;
-    if (!count) continue;
-    g.span[g.spans++] = Span{in.gradients, count, uint32_t(blocks), kGradientSpan, 0};
-    blocks += SpanBlocks(count);
+    add(in.gradients, rows * tables[in.table].dim, kGradientSpan);
+    g.sorted.feature_rows[f] = rows;
   }
+  // The prepared keys and reference words, checked before the update uses
+  // them as addresses.
+  const PushLayout L(plan.occurrences);
+  auto* ws = static_cast<uint8_t*>(workspace);
+  g.sorted.keys = reinterpret_cast<const uint32_t*>(ws + (plan.passes % 2 == 1 ? L.keys_b : L.keys_a));
+  g.sorted.rs = reinterpret_cast<const uint64_t*>(ws + L.sorted_rs);
+  for (uint32_t k = 0; k < table_count; ++k) g.sorted.table_rows[k] = tables[plan.table_of_key[k]].rows;
+  g.sorted.row_bits = plan.row_bits;
+  g.sorted.tables = table_count;
+  g.sorted.features = feature_count;
+  add(nullptr, plan.occurrences, kSortedSpan);
   g.ctrl = static_cast<Control*>(workspace);
+  g.bounds = static_cast<const Bounds*>(bounds);
   return LaunchGuard(g, blocks, AsStream(stream));
 }
 
@@ -1540,6 +1692,7 @@ static int RunRows(const eps_hip_table* table, const eps_hip_optimizer* optimize
   }
   const TableDesc d = MakeTable(*table, *optimizer);
   g.ctrl = ctrl;  // the index checks report to its prepare status
+  g.bounds = static_cast<const Bounds*>(bounds);
   EPS_HIP_TRY(LaunchGuard(g, blocks, s));
   RowArgs a{};
   a.t = d;

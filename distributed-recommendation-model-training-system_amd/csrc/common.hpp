@@ -8,6 +8,7 @@
 #include <string>
 
 #include "eps_hip.h"
+#include "guard.hpp"
 
 namespace eps_hip {
 
@@ -26,6 +27,7 @@ static_assert(kDigitsPerThread == 2, "radix digits per thread");
 constexpr uint32_t kKeygenItems = 4;      // occurrences per keygen thread
 constexpr uint32_t kClasses = 6;          // 5 vector widths + generic
 constexpr uint32_t kRefRowBits = 27;      // gradient row bits in a reference word
+static_assert(kRefRowBits == kGuardRefRowBits, "one reference word layout");
 constexpr uint32_t kLongRefs = 128;       // rows with more references take the sliced path
 constexpr uint32_t kSlice = 16;           // columns per hot-row work unit
 
@@ -51,7 +53,12 @@ struct Control {
   uint32_t tile_counter[kMaxPasses];
   uint32_t class_start[8];  // first sorted position of each dimension class (+ end)
   uint32_t long_count[kXcds * kHotBuckets];  // entries of each hot-row list
-  uint32_t pad[77];
+  // Bounds-domain maxima W, M, V as float bits, copied by the gradient scan
+  // before the update: the guard decides from this copy only, so every block
+  // of every update kernel decides the same, whatever the update's own
+  // blocks have since raised the live domain to.
+  uint32_t snap[4];
+  uint32_t pad[73];
   // Error bits of every push or update run in this workspace, OR-ed in as they
   // are found; the per-call clears of the block skip this word (it starts at
   // zero with the workspace and only eps_hip_status_history_word's user

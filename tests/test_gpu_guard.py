@@ -140,3 +140,114 @@ def test_history_survives_later_pushes(torch_gpu, pkg):
     assert np.array_equal(shard.powers, powers * np.array([[spec.beta1, spec.beta2]], F32))
     shard.clear_history()
     assert shard.history() == 0
+
+
+def _near_limit_shard(torch, W, H, rows, dim, x=0.7e30):
+    """A table whose every row has w = v = 0 and m = m0, loaded through the
+    bounds domain, with m0 chosen so that a zero-gradient first step writes
+    |w'| = lr_t * m' / eps = x: the guard's w bound before the step is
+    x * 1.0201 (below 1e30, so the fused pass runs), but a decision taken from
+    the bounds as raised by rows already written would be 2.04 * x (checked)."""
+    spec = W.TableSpec(0, dim, rows, seed=4)
+    shard = H.DeviceShard(torch, [spec])
+    lr = float(H.lr_t(spec.lr, spec.b1p, spec.b2p))
+    m0 = F32(x * spec.eps / (spec.beta1 * lr))
+    packed = torch.zeros((rows, 3 * dim), dtype=torch.float32, device="cuda")
+    packed[:, dim:2 * dim] = float(m0)
+    shard.load_rows(0, torch.arange(rows, device="cuda"), packed)
+    del packed
+    return spec, shard, m0
+
+
+@pytest.mark.parametrize("hot", [False, True], ids=["rows", "rows+hot-rows-beside"])
+def test_guard_decides_from_snapshot(torch_gpu, pkg, hot):
+    """1.2 M distinct rows (several times the update blocks the GPU holds at
+    once) whose zero-gradient step takes |w| to 0.7e30.  Every block must take
+    the decision the bounds before the push allow (fused) and every row must
+    be updated exactly as the CPU shard updates it (lazy_adam.cpp:7-42 applies
+    the whole push: every value stays finite).  `hot` adds rows with 300
+    references each on a table of more than 65,536 references, so the hot-row
+    kernel runs beside the row kernel and both decide."""
+    torch, W, H = torch_gpu, pkg.workloads, pkg.eps_hip
+    rows, dim = 1_200_000, 16
+    spec, shard, m0 = _near_limit_shard(torch, W, H, rows, dim)
+    ids = np.arange(rows, dtype=np.uint64)
+    if hot:
+        ids = np.concatenate([ids, np.repeat(np.arange(0, 40, dtype=np.uint64) * 7919, 300)])
+    lengths = np.ones(len(ids), np.uint64)
+    offsets = np.arange(len(ids) + 1, dtype=np.uint64)
+    grad = np.zeros((len(ids), dim), F32)
+    f = W.Feature(0, 0, W.SUM, ids, offsets, lengths, None, grad)
+    dev = [H.DeviceFeature(torch, f)]
+    print(f"case: snapshot guard hot={hot} rows={rows} refs={len(ids)}", flush=True)
+    shard.prepare(dev)
+    status = shard.push(dev)
+    assert status & H.STATUS_ERRORS == 0, f"{status:#x}"
+    assert not status & H.STATUS_CHECKED_PATH, f"decision should be fused: {status:#x}"
+    rc, w1, m1, v1 = oracle.adam_rows_ctx(np.zeros((1, dim), F32), np.full((1, dim), m0, F32),
+                                          np.zeros((1, dim), F32), np.zeros((1, dim), F32),
+                                          spec.beta1, spec.beta2, spec.eps, spec.lr, spec.b1p, spec.b2p)
+    assert rc == 0
+    assert 0.5e30 < abs(float(w1[0, 0])) < 0.98e30
+    want = np.concatenate([w1, m1, v1], axis=1)
+    got = shard.read_rows(0, torch.arange(rows, device="cuda")).cpu().numpy()
+    bad = np.flatnonzero(~(got == want).all(axis=1))
+    assert bad.size == 0, f"{bad.size} rows differ from the CPU shard (first {bad[:5]})"
+    # The bounds now hold |w| = 0.7e30: the next push must take the checked path.
+    shard.prepare(dev)
+    status = shard.push(dev)
+    assert status & H.STATUS_CHECKED_PATH and status & H.STATUS_ERRORS == 0, f"{status:#x}"
+
+
+def _find(haystack, needle):
+    """Offset (in elements) of the first occurrence of array `needle` in `haystack`."""
+    hb, nb = haystack.tobytes(), needle.tobytes()
+    at = hb.find(nb)
+    while at >= 0 and at % needle.itemsize:
+        at = hb.find(nb, at + 1)
+    assert at >= 0, "array not found in the workspace"
+    return at // needle.itemsize
+
+
+@pytest.mark.parametrize("what", ["key-table", "key-slot", "ref-feature", "ref-row"])
+def test_damaged_workspace_rejects(torch_gpu, pkg, what):
+    """A prepared workspace with one sorted key or reference word changed
+    after preparation (naming a table, slot, feature or gradient row the push
+    does not have) is rejected before anything is written: BAD_INDEX and
+    REJECTED, every row unchanged, no fault."""
+    torch, W, H = torch_gpu, pkg.workloads, pkg.eps_hip
+    rng = np.random.default_rng(21)
+    spec = W.TableSpec(0, 64, 3000, seed=8)
+    shard = H.DeviceShard(torch, [spec])
+    shard.init_rows()
+    everything = torch.arange(spec.rows, device="cuda")
+    before = shard.read_rows(0, everything).clone()
+    f = hot_feature(W, rng, spec, W.MEAN)
+    dev = [H.DeviceFeature(torch, f)]
+    shard.prepare(dev)
+    torch.cuda.synchronize()
+    ws = shard.wss[0]
+    host = ws.cpu().numpy().view(np.uint32)
+    host = host[: len(host) // 2 * 2]
+    order = np.argsort(f.keys, kind="stable")
+    keys = f.keys[order].astype(np.uint32)  # one table: key == slot
+    at = _find(host, keys)
+    bag = np.searchsorted(f.offsets, np.arange(len(f.keys)), side="right") - 1
+    scale = (F32(1) / f.valid_lengths[bag].astype(F32)).view(np.uint32).astype(np.uint64)
+    words = (scale << np.uint64(32)) | bag.astype(np.uint64)
+    wat = _find(host.view(np.uint64), words[order])
+    k = len(keys) // 2
+    print(f"case: damaged workspace {what} at sorted position {k}", flush=True)
+    flat = ws.view(torch.int32)
+    if what == "key-table":   # row_bits of 3000 rows is 12: table index 1 of a one-table push
+        flat[at + k] = int((1 << 12) | int(keys[k]))
+    elif what == "key-slot":  # slot 3000 is inside the 12 row bits, past the table
+        flat[at + k] = spec.rows
+    else:
+        w64 = ws[: ws.numel() // 2 * 2].view(torch.int64)
+        word = int(words[order][k])
+        word = (word | (5 << 27)) if what == "ref-feature" else ((word & ~((1 << 27) - 1)) | len(f.valid_lengths))
+        w64[wat + k] = word - (1 << 64) if word >= 1 << 63 else word
+    status = shard.push(dev)
+    assert status & H.STATUS_BAD_INDEX and status & H.STATUS_REJECTED, f"{status:#x}"
+    assert torch.equal(shard.read_rows(0, everything), before), "a rejected push wrote rows"
