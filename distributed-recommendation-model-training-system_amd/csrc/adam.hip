@@ -41,13 +41,15 @@ constexpr uint32_t kFallbackGrid = 2048;
 // ---------------------------------------------------------------------------
 // Gradient scan (GradMaxKernel), the first kernel of an update.  Its spans are
 // the guarded input arrays: gradient values, reference scales, 64-bit caller
-// indices that must all be below `limit`, and (a push) the sorted keys and
-// reference words of the prepared workspace, whose table indices, slots,
-// features and gradient rows must name the push's tables and gradients.  It
-// records max |gradient| and max |scale| for the guard and any range failure
-// as a prepare-time finding, all before anything is written; block 0 also
-// copies the bounds-domain maxima into the control block, the snapshot the
-// guard decides from.
+// indices that must all be below `limit`, and (a push) the sorted keys of the
+// prepared workspace, whose table indices and slots must name the push's
+// tables and rows.  It records max |gradient| and max |scale| for the guard
+// and any range failure as a prepare-time finding, all before anything is
+// written; block 0 also copies the bounds-domain maxima into the control
+// block, the snapshot the guard decides from.  (The reference words are
+// checked where the update kernels decode them: a word naming no gradient row
+// of the push is never used as an address, and the rows it feeds are not
+// written.)
 enum SpanKind : uint32_t { kGradientSpan = 0, kScaleSpan = 1, kIndexSpan = 2, kSortedSpan = 3 };
 struct Span {
   const float* p;
@@ -55,13 +57,11 @@ struct Span {
   uint32_t block_begin, kind;
   uint64_t limit;
 };
-// What the sorted span is checked against (key index order for tables).
+// What the sorted keys are checked against (key index order for tables).
 struct SortedCheck {
   const uint32_t* keys;
-  const uint64_t* rs;
   uint64_t table_rows[EPS_HIP_MAX_TABLES];
-  uint64_t feature_rows[EPS_HIP_MAX_FEATURES];
-  uint32_t row_bits, tables, features;
+  uint32_t row_bits, tables;
 };
 struct GuardArgs {
   Span span[EPS_HIP_MAX_FEATURES + 4];
@@ -71,12 +71,12 @@ struct GuardArgs {
   SortedCheck sorted;
 };
 static_assert(sizeof(GuardArgs) <= 4096, "gradient scan arguments fit the kernel-argument segment");
-constexpr uint32_t kMaxItems = 4;      // float4 per thread per block (all issued before any is used)
-constexpr uint32_t kSortedItems = 8;   // sorted positions per thread per block
+constexpr uint32_t kMaxItems = 16;     // float4 per thread per block (all issued before any is used)
+constexpr uint32_t kSortedItems = 16;  // sorted keys per thread per block
 
 __global__ void __launch_bounds__(kBlock) GradMaxKernel(GuardArgs a) {
   __shared__ uint32_t s_max[4];
-  __shared__ uint64_t s_rows[EPS_HIP_MAX_TABLES + EPS_HIP_MAX_FEATURES];
+  __shared__ uint64_t s_rows[EPS_HIP_MAX_TABLES];
   if (blockIdx.x == 0 && threadIdx.x < kWave && a.bounds) {
     const uint32_t lane = threadIdx.x;
     const uint32_t w = WaveMax(a.bounds->v[lane][0]), m = WaveMax(a.bounds->v[lane][1]),
@@ -93,32 +93,31 @@ __global__ void __launch_bounds__(kBlock) GradMaxKernel(GuardArgs a) {
   uint32_t found = 0;  // prepare-status bits this thread found
   if (sp.kind == kSortedSpan) {
     const SortedCheck& c = a.sorted;
-    for (uint32_t i = threadIdx.x; i < EPS_HIP_MAX_TABLES + EPS_HIP_MAX_FEATURES; i += kBlock)
-      s_rows[i] = i < EPS_HIP_MAX_TABLES ? c.table_rows[i] : c.feature_rows[i - EPS_HIP_MAX_TABLES];
+    if (threadIdx.x < EPS_HIP_MAX_TABLES) s_rows[threadIdx.x] = c.table_rows[threadIdx.x];
     __syncthreads();
     // Positions past the valid count hold keys of rows not on this device,
     // which no update kernel reads.
-    const uint64_t valid = min<uint64_t>(sp.count, a.ctrl->valid_count);
     const uint64_t per_block = uint64_t(kBlock) * kSortedItems;
     const uint64_t begin = uint64_t(blockIdx.x - sp.block_begin) * per_block;
-    uint32_t key[kSortedItems];
-    uint64_t word[kSortedItems];
+    {
+      // Every load is issued before any is used (and before the valid count
+      // is known): positions past the span read the block's first position,
+      // and positions past the valid count are not judged.
+      uint32_t key[kSortedItems];
 #pragma unroll
-    for (uint32_t k = 0; k < kSortedItems; ++k) {
-      const uint64_t i = begin + uint64_t(k) * kBlock + threadIdx.x;
-      key[k] = i < valid ? c.keys[i] : 0u;
-      word[k] = i < valid ? c.rs[i] : 0ull;
-    }
+      for (uint32_t k = 0; k < kSortedItems; ++k) {
+        const uint64_t i = begin + uint64_t(k) * kBlock + threadIdx.x;
+        key[k] = c.keys[i < sp.count ? i : begin];
+      }
+      const uint64_t valid = min<uint64_t>(sp.count, a.ctrl->valid_count);
+      bool bad = false;
 #pragma unroll
-    for (uint32_t k = 0; k < kSortedItems; ++k) {
-      const uint64_t i = begin + uint64_t(k) * kBlock + threadIdx.x;
-      if (i >= valid) continue;
-      const KeyParts kp = SplitKey(key[k], c.row_bits);
-      const RefParts rp = SplitRef(word[k]);
-      const bool ok = KeyInRange(kp, c.tables, s_rows[min(kp.table, EPS_HIP_MAX_TABLES - 1u)]) &&
-                      RefInRange(rp, c.features, s_rows[EPS_HIP_MAX_TABLES + min(rp.feature,
-                                                                                  EPS_HIP_MAX_FEATURES - 1u)]);
-      if (!ok) found = EPS_HIP_STATUS_BAD_INDEX;
+      for (uint32_t k = 0; k < kSortedItems; ++k) {
+        const uint64_t i = begin + uint64_t(k) * kBlock + threadIdx.x;
+        const KeyParts kp = SplitKey(key[k], c.row_bits);
+        bad |= i < valid && !KeyInRange(kp, c.tables, s_rows[min(kp.table, EPS_HIP_MAX_TABLES - 1u)]);
+      }
+      if (bad) found = EPS_HIP_STATUS_BAD_INDEX;
     }
   } else if (sp.kind == kIndexSpan) {
     const uint64_t per_block = uint64_t(kBlock) * kMaxItems * 4;
@@ -133,11 +132,24 @@ __global__ void __launch_bounds__(kBlock) GradMaxKernel(GuardArgs a) {
     const uint64_t end = min(begin + per_block, sp.count);
     if (reinterpret_cast<uintptr_t>(sp.p) % 16 == 0) {
       const uint64_t vend = begin + ((end - begin) & ~uint64_t(3));
+      // Every load is issued before any is used (a branch around each would
+      // make the compiler wait for each pair): quads past the vector part
+      // read the block's first quad and count as zeros.
       float4 x[kMaxItems];
+      if (vend > begin) {  // uniform over the block
 #pragma unroll
-      for (uint32_t k = 0; k < kMaxItems; ++k) {
-        const uint64_t i = begin + (uint64_t(k) * kBlock + threadIdx.x) * 4;
-        x[k] = i < vend ? Load4(sp.p + i) : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (uint32_t k = 0; k < kMaxItems; ++k) {
+          const uint64_t i = begin + (uint64_t(k) * kBlock + threadIdx.x) * 4;
+          x[k] = Load4(sp.p + (i < vend ? i : begin));
+        }
+#pragma unroll
+        for (uint32_t k = 0; k < kMaxItems; ++k) {
+          const uint64_t i = begin + (uint64_t(k) * kBlock + threadIdx.x) * 4;
+          if (i >= vend) x[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+      } else {
+#pragma unroll
+        for (uint32_t k = 0; k < kMaxItems; ++k) x[k] = make_float4(0.f, 0.f, 0.f, 0.f);
       }
       uint32_t neg = 0;  // any value below zero (not -0.0)
 #pragma unroll
@@ -568,13 +580,19 @@ constexpr uint32_t kHotBlock = 256;                       // threads of a hot-ro
 constexpr uint32_t kHotRing = 4;                          // chunks staged in LDS per block
 constexpr uint32_t kUnitCache = 512;                      // unit headers a block stages in LDS
 constexpr uint32_t kHotPitch = kHotChunk + 4;             // floats per tile row (one column)
-constexpr uint32_t kHotQuads = kSlice / 4;                // lanes per reference in a row load
-constexpr uint32_t kHotRefsPerLoad = kWave / kHotQuads;   // references per row load
-constexpr uint32_t kHotLoads = kHotChunk / kHotRefsPerLoad;  // row loads per producer lane per chunk
+// Shape of a hot-row unit of kS columns (16 or 64): lanes per reference in a
+// producer's row load, references per row load, row loads per producer lane
+// per chunk.
+template <uint32_t kS>
+struct HotShape {
+  static constexpr uint32_t kQuads = kS / 4;
+  static constexpr uint32_t kRefsPerLoad = kWave / kQuads;
+  static constexpr uint32_t kLoads = kHotChunk / kRefsPerLoad;
+  static_assert(kHotChunk == kWave && kS <= kWave && kWave % kQuads == 0 && kLoads % 4 == 0,
+                "hot-row tile shape");
+};
 constexpr uint32_t kProducers = kHotBlock / kWave - 1;
 constexpr uint32_t kDepth = 2;  // own chunks each producer keeps in flight (4 measured no faster)
-static_assert(kHotChunk == kWave && kSlice <= kWave && kWave % kHotQuads == 0 && kHotLoads % 4 == 0,
-              "hot-row tile shape");
 // Sorted positions per row-run window for groups of 2^log2g lanes: about 5
 // rows per group at the usual ~3 references per row.  Wider groups take
 // narrower windows, so a class of wide rows still spreads over many blocks.
@@ -639,10 +657,11 @@ struct HotSlot {
 // 4*quad .. 4*quad+3 of reference kHotRefsPerLoad*k + sub, with its scale;
 // wmv is lane l's column of the unit's w, m, v (used when the chunk ends its
 // unit).
+template <uint32_t kS>
 struct HotRows {
   HotSlot c;
-  float4 x[kHotLoads];
-  float s[kHotLoads];
+  float4 x[HotShape<kS>::kLoads];
+  float s[HotShape<kS>::kLoads];
   float wmv[3];
 };
 
@@ -650,9 +669,10 @@ struct HotRows {
 // order the row loads use them: entry [sub][k] is reference
 // kHotRefsPerLoad*k + sub, so a lane reads its kHotLoads pointers and scales
 // with a few 16-byte reads.
+template <uint32_t kS>
 struct HotRefs {
-  const float* src[kHotRefsPerLoad][kHotLoads];
-  float scale[kHotRefsPerLoad][kHotLoads];
+  const float* src[HotShape<kS>::kRefsPerLoad][HotShape<kS>::kLoads];
+  float scale[HotShape<kS>::kRefsPerLoad][HotShape<kS>::kLoads];
 };
 
 // s_waitcnt operand that waits for LDS (and scalar memory) accesses only:
@@ -684,12 +704,16 @@ __device__ __forceinline__ void PostCounter(uint32_t* counter, uint32_t value) {
     __hip_atomic_store(counter, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
+template <uint32_t kSlice>
 __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
+  constexpr uint32_t kHotQuads = HotShape<kSlice>::kQuads;
+  constexpr uint32_t kHotRefsPerLoad = HotShape<kSlice>::kRefsPerLoad;
+  constexpr uint32_t kHotLoads = HotShape<kSlice>::kLoads;
   __shared__ TableDesc s_t[EPS_HIP_MAX_TABLES];
   __shared__ const float* s_grad[EPS_HIP_MAX_FEATURES];
   __shared__ __align__(16) float s_tile[kHotRing][kSlice * kHotPitch];
   __shared__ float s_wmv[kHotRing][3][kSlice];
-  __shared__ __align__(16) HotRefs s_ref[kProducers];
+  __shared__ __align__(16) HotRefs<kSlice> s_ref[kProducers];
   // ready[t]: chunks staged in tile t so far; used[t]: chunks added from it.
   __shared__ uint32_t s_ready[kHotRing], s_used[kHotRing];
   __shared__ uint4 s_unit[kUnitCache];  // {start, end, key, col0} of the block's first units
@@ -902,7 +926,7 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
     const uint32_t p = wave - 1;
     const uint32_t quad = lane % kHotQuads, sub = lane / kHotQuads;
     const float* idle = reinterpret_cast<const float*>(a.rs);
-    HotRefs& slots = s_ref[p];
+    HotRefs<kSlice>& slots = s_ref[p];
     fetch();
     HotSlot cur = take();  // cursor over the stream, at chunk jc
     uint32_t jc = 0, total = cur.ok ? ~0u : 0u;
@@ -943,7 +967,7 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
     };
     // Lanes whose columns lie past the row's dimension read the slice's first
     // columns; their products are never stored by the adding wave.
-    auto load_rows = [&](HotRows& r) {
+    auto load_rows = [&](HotRows<kSlice>& r) {
       r.c = dc;
       const KeyParts kp = SplitKey(dc.key, a.row_bits);
       const TableDesc& T = s_t[min(kp.table, a.tables - 1)];
@@ -970,7 +994,7 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
       const uint32_t ms = dc.ok && key_ok ? dim : 0u;
       r.wmv[0] = LoadF(row); r.wmv[1] = LoadF(row + ms); r.wmv[2] = LoadF(row + 2 * ms);
     };
-    auto stage = [&](const HotRows& r, uint32_t j) {
+    auto stage = [&](const HotRows<kSlice>& r, uint32_t j) {
       const uint32_t t = j % kHotRing;
       if (!stalled && !WaitCounter(&s_used[t], j / kHotRing, 1, a.spin_limit)) stalled = true;
       if (stalled) return;  // nothing more is staged
@@ -1010,7 +1034,7 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
     // prologue leaves the loads in the loop's own order (words(D), rows(0),
     // words(D+1), rows(1), ...), so the compiler's load waits inside the loop
     // can be exact.
-    HotRows rows[kDepth];
+    HotRows<kSlice> rows[kDepth];
     Words words[kDepth];
     advance(p);  // own chunk 0
 #pragma unroll
@@ -1030,7 +1054,7 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
     // Words and rows both get D own chunks to arrive (the decode needs no
     // wait of its own: its words were issued before the rows the stage
     // waited for).  D own chunks per pass keep the buffers static.
-    auto own = [&](HotRows& r, Words& w, uint32_t j) {
+    auto own = [&](HotRows<kSlice>& r, Words& w, uint32_t j) {
       stage(r, j);
       decode(w);
       load_words(w);
@@ -1356,6 +1380,7 @@ int ThreadOverlap(Overlap** out) {
 // each, the row kernels lose more occupancy beside it than they gain (26
 // tables of ~43,000: 283 -> 321 us), so they run after it.
 constexpr uint64_t kOverlapTableRefs = 1ull << 16;
+constexpr uint32_t kNarrowSlice = 16, kWideSlice = 64;  // columns per hot-row unit
 
 std::atomic<uint32_t> g_spin_limit{1u << 22};
 uint32_t SpinLimit() { return g_spin_limit.load(std::memory_order_relaxed); }
@@ -1374,9 +1399,12 @@ int LaunchRowRun(unsigned grid, const VecArgs& a, hipStream_t s) {
 }
 
 // Hot rows (any vector class) when `hot`, else the other rows of class `cls`.
-int LaunchVectorUpdate(uint32_t cls, bool hot, unsigned grid, const VecArgs& a, hipStream_t s) {
-  if (hot) {
-    hipLaunchKernelGGL(HotSliceKernel, dim3(grid), dim3(kHotBlock), 0, s, a);
+int LaunchVectorUpdate(uint32_t cls, uint32_t hot_slice, unsigned grid, const VecArgs& a, hipStream_t s) {
+  if (hot_slice) {
+    if (hot_slice == kWideSlice)
+      hipLaunchKernelGGL(HotSliceKernel<kWideSlice>, dim3(grid), dim3(kHotBlock), 0, s, a);
+    else
+      hipLaunchKernelGGL(HotSliceKernel<kNarrowSlice>, dim3(grid), dim3(kHotBlock), 0, s, a);
     EPS_HIP_LAUNCHED("hot row update");
     return EPS_HIP_OK;
   }
@@ -1445,20 +1473,27 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
     va.gs = a.gs;
     va.spin_limit = SpinLimit();
     va.row_bits = plan.row_bits;
+    uint64_t table_refs[EPS_HIP_MAX_TABLES] = {};
+    for (uint32_t f = 0; f < feature_count; ++f) table_refs[features[f].table] += features[f].occurrences;
+    const bool long_rows = *std::max_element(table_refs, table_refs + table_count) >= kOverlapTableRefs;
+    // Slice width: pushes with very long hot rows (some table with 65,536 or
+    // more references) cut each row into 16-column units, so one row's chain
+    // data spreads over several CUs; otherwise 64-column units, whose fewer
+    // and fuller units a block's producers stage with less bookkeeping per
+    // column (26 tables of ~43,000 references: 47 -> 41 us a push).
+    const uint32_t slice = long_rows ? kNarrowSlice : kWideSlice;
     // Units per hot row: the widest vector table's slices, rounded up to a
     // power of two (units past a row's dimension are skipped in the kernel).
     uint32_t slices = 1;
     for (uint32_t t = 0; t < table_count; ++t)
       if (DimClass(tables[t].dim) < kClasses - 1)
-        slices = std::max(slices, (tables[t].dim + kSlice - 1) / kSlice);
+        slices = std::max(slices, (tables[t].dim + slice - 1) / slice);
     va.slice_bits = 0;
     while ((1u << va.slice_bits) < slices) ++va.slice_bits;
     uint64_t vector_occurrences = 0;
     for (uint32_t cls = 0; cls + 1 < kClasses; ++cls) vector_occurrences += plan.class_occurrences[cls];
     const uint64_t hot_units = (vector_occurrences / (kLongRefs + 1)) << va.slice_bits;
-    uint64_t table_refs[EPS_HIP_MAX_TABLES] = {};
-    for (uint32_t f = 0; f < feature_count; ++f) table_refs[features[f].table] += features[f].occurrences;
-    overlap = hot_units && *std::max_element(table_refs, table_refs + table_count) >= kOverlapTableRefs;
+    overlap = hot_units && long_rows;
     if (phases & kPrimary) {
       // Grids are multiples of kXcds (the kernels split their work by XCD).
       auto xcd_grid = [](uint64_t b) { return (b + kXcds - 1) / kXcds * kXcds; };
@@ -1476,10 +1511,10 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
           EPS_HIP_TRY(ThreadOverlap(&ov));
           EPS_HIP_TRY(Check(hipEventRecord(ov->fork, s), "hot-row fork"));
           EPS_HIP_TRY(Check(hipStreamWaitEvent(ov->side, ov->fork, 0), "hot-row fork wait"));
-          EPS_HIP_TRY(LaunchVectorUpdate(0, true, unsigned(blocks), va, ov->side));
+          EPS_HIP_TRY(LaunchVectorUpdate(0, slice, unsigned(blocks), va, ov->side));
           EPS_HIP_TRY(Check(hipEventRecord(ov->join, ov->side), "hot-row join"));
         } else {
-          EPS_HIP_TRY(LaunchVectorUpdate(0, true, unsigned(blocks), va, s));
+          EPS_HIP_TRY(LaunchVectorUpdate(0, slice, unsigned(blocks), va, s));
           role = kFollow;
         }
       }
@@ -1492,7 +1527,7 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
             std::max<uint64_t>(1, (plan.class_occurrences[cls] + RunPositions(cls + 2) - 1) /
                                       RunPositions(cls + 2)),
             kVectorGrid));
-        EPS_HIP_TRY(LaunchVectorUpdate(cls, false, unsigned(blocks), va, s));
+        EPS_HIP_TRY(LaunchVectorUpdate(cls, 0, unsigned(blocks), va, s));
       }
     }
   }
@@ -1576,18 +1611,14 @@ int eps_hip_push_begin(const eps_hip_table* tables, const eps_hip_optimizer* opt
     const auto& in = features[f];
     const uint64_t rows = in.pooling == EPS_HIP_POOL_SEQUENCE ? in.occurrences : in.bags;
     add(in.gradients, rows * tables[in.table].dim, kGradientSpan);
-    g.sorted.feature_rows[f] = rows;
   }
-  // The prepared keys and reference words, checked before the update uses
-  // them as addresses.
+  // The prepared keys, checked before the update uses them as addresses.
   const PushLayout L(plan.occurrences);
   auto* ws = static_cast<uint8_t*>(workspace);
   g.sorted.keys = reinterpret_cast<const uint32_t*>(ws + (plan.passes % 2 == 1 ? L.keys_b : L.keys_a));
-  g.sorted.rs = reinterpret_cast<const uint64_t*>(ws + L.sorted_rs);
   for (uint32_t k = 0; k < table_count; ++k) g.sorted.table_rows[k] = tables[plan.table_of_key[k]].rows;
   g.sorted.row_bits = plan.row_bits;
   g.sorted.tables = table_count;
-  g.sorted.features = feature_count;
   add(nullptr, plan.occurrences, kSortedSpan);
   g.ctrl = static_cast<Control*>(workspace);
   g.bounds = static_cast<const Bounds*>(bounds);

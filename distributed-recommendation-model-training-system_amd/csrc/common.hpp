@@ -29,7 +29,6 @@ constexpr uint32_t kClasses = 6;          // 5 vector widths + generic
 constexpr uint32_t kRefRowBits = 27;      // gradient row bits in a reference word
 static_assert(kRefRowBits == kGuardRefRowBits, "one reference word layout");
 constexpr uint32_t kLongRefs = 128;       // rows with more references take the sliced path
-constexpr uint32_t kSlice = 16;           // columns per hot-row work unit
 
 constexpr uint32_t kSrcSlots = 64;        // spread of the gradient/scale maximum atomics
 constexpr uint32_t kHistCopies = 16;      // spread of the keygen histogram atomics

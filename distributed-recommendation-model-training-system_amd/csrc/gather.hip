@@ -1,6 +1,6 @@
 // gather.hip -- pooled gather (pull), row-state movement and initialisation.
 //
-// Pull = one launch for up to 16 features.  A block owns a tile of output rows
+// Pull = one launch for up to 32 features.  A block owns a tile of output rows
 // (bags, or positions for sequence pooling) of one feature.  It stages the
 // tile's bag offsets and row slots in LDS (one coalesced pass, unique->slot
 // remap and range checks done once per occurrence), then sub-wavefront groups
@@ -33,6 +33,9 @@ namespace {
 constexpr uint32_t kIdCap = 1024;     // occurrences staged in LDS per tile (LDS sets the occupancy)
 constexpr uint32_t kGatherBatch = 8;  // source rows in flight per lane group
 constexpr uint32_t kGenericLog2 = 0xff;
+constexpr int kBufferWord3 = 0x00020000;         // raw buffer resource, dword data (gfx9 family)
+constexpr uint32_t kBufferOutside = 0xFFFFFFF0u;  // an offset past every buffer range
+typedef int EpsI4 __attribute__((ext_vector_type(4)));
 
 struct GatherDesc {
   const float* source;
@@ -43,7 +46,12 @@ struct GatherDesc {
   const float* weights;
   float* output;
   uint64_t stride, rows, source_rows, remap_count;
-  uint32_t dim, pooling, block_begin, log2g, rows_per_block, pad;
+  uint32_t dim, pooling, block_begin, log2g, rows_per_block;
+  // Bytes of the source when they fit a 32-bit buffer range (0: they do not):
+  // the row loads then go through a buffer resource, and the slots of a batch
+  // past the bag's end (or holes) take an offset outside the range, which
+  // returns zeros without a memory request.
+  uint32_t buffer_bytes;
 };
 struct GatherArgs {
   GatherDesc part[EPS_HIP_MAX_GATHER_PARTS];
@@ -113,6 +121,8 @@ __global__ void __launch_bounds__(kBlock) GatherKernel(GatherArgs args) {
         // with no branch around a load (a hole or a position past the bag
         // reads row 0, column 0 and is dropped; row 0 exists).
         const uint32_t cl = active ? c : 0;
+        const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+            const_cast<float*>(d.source), (short)0, int(d.buffer_bytes), kBufferWord3);
         for (uint64_t pos = beg; pos < end; pos += kGatherBatch) {
           float4 v[kGatherBatch];
           float a[kGatherBatch];
@@ -124,7 +134,14 @@ __global__ void __launch_bounds__(kBlock) GatherKernel(GatherArgs args) {
             const uint64_t slot = s_slot[at];
             ok[u] = i < end && slot != kHole;
             a[u] = weighted ? s_weight[at] : 1.f;
-            v[u] = Load4(d.source + (ok[u] ? slot : 0) * d.stride + cl);
+            if (d.buffer_bytes) {
+              const uint32_t boff = ok[u] && active ? uint32_t((slot * d.stride + c) * 4) : kBufferOutside;
+              const EpsI4 q = __builtin_amdgcn_raw_buffer_load_b128(rsrc, boff, 0, 0);
+              v[u] = make_float4(__int_as_float(q[0]), __int_as_float(q[1]), __int_as_float(q[2]),
+                                 __int_as_float(q[3]));
+            } else {
+              v[u] = Load4(d.source + (ok[u] ? slot : 0) * d.stride + cl);
+            }
           }
 #pragma unroll
           for (uint32_t u = 0; u < kGatherBatch; ++u) {
@@ -594,6 +611,9 @@ int eps_hip_gather(const eps_hip_gather_part* parts, uint32_t count, uint32_t* s
     d.lengths = in.valid_lengths; d.weights = in.weights; d.output = in.output;
     d.stride = in.stride; d.rows = in.rows; d.source_rows = in.source_rows;
     d.remap_count = in.remap_count; d.dim = in.dim; d.pooling = in.pooling;
+    const uint64_t source_bytes = in.source_rows * in.stride * 4;
+    d.buffer_bytes = source_bytes && source_bytes < kBufferOutside && in.source_rows < (1ull << 32)
+                         ? uint32_t(source_bytes) : 0u;
     const bool vec = in.dim % 4 == 0 && in.dim <= 256 && in.stride % 4 == 0 &&
                      reinterpret_cast<uintptr_t>(in.source) % 16 == 0 &&
                      reinterpret_cast<uintptr_t>(in.output) % 16 == 0;

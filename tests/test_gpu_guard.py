@@ -212,9 +212,12 @@ def _find(haystack, needle):
 @pytest.mark.parametrize("what", ["key-table", "key-slot", "ref-feature", "ref-row"])
 def test_damaged_workspace_rejects(torch_gpu, pkg, what):
     """A prepared workspace with one sorted key or reference word changed
-    after preparation (naming a table, slot, feature or gradient row the push
-    does not have) is rejected before anything is written: BAD_INDEX and
-    REJECTED, every row unchanged, no fault."""
+    after preparation, naming a table, slot, feature or gradient row the push
+    does not have.  A damaged key is found by the gradient scan before
+    anything is written: BAD_INDEX and REJECTED, every row unchanged.  A
+    damaged reference word is found where the update kernels decode it: it is
+    never used as an address, BAD_INDEX is reported and the row it feeds is
+    not written.  No case faults."""
     torch, W, H = torch_gpu, pkg.workloads, pkg.eps_hip
     rng = np.random.default_rng(21)
     spec = W.TableSpec(0, 64, 3000, seed=8)
@@ -237,7 +240,7 @@ def test_damaged_workspace_rejects(torch_gpu, pkg, what):
     words = (scale << np.uint64(32)) | bag.astype(np.uint64)
     wat = _find(host.view(np.uint64), words[order])
     k = len(keys) // 2
-    print(f"case: damaged workspace {what} at sorted position {k}", flush=True)
+    print(f"case: damaged workspace {what} at sorted position {k} (row {keys[k]})", flush=True)
     flat = ws.view(torch.int32)
     if what == "key-table":   # row_bits of 3000 rows is 12: table index 1 of a one-table push
         flat[at + k] = int((1 << 12) | int(keys[k]))
@@ -249,5 +252,12 @@ def test_damaged_workspace_rejects(torch_gpu, pkg, what):
         word = (word | (5 << 27)) if what == "ref-feature" else ((word & ~((1 << 27) - 1)) | len(f.valid_lengths))
         w64[wat + k] = word - (1 << 64) if word >= 1 << 63 else word
     status = shard.push(dev)
-    assert status & H.STATUS_BAD_INDEX and status & H.STATUS_REJECTED, f"{status:#x}"
-    assert torch.equal(shard.read_rows(0, everything), before), "a rejected push wrote rows"
+    assert status & H.STATUS_BAD_INDEX, f"{status:#x}"
+    assert shard.history() & H.STATUS_BAD_INDEX
+    after = shard.read_rows(0, everything)
+    if what.startswith("key"):
+        assert status & H.STATUS_REJECTED, f"{status:#x}"
+        assert torch.equal(after, before), "a rejected push wrote rows"
+    else:
+        row = int(keys[k])
+        assert torch.equal(after[row], before[row]), "the row of a damaged reference was written"
