@@ -1372,24 +1372,33 @@ int ThreadOverlap(Overlap** out) {
   return EPS_HIP_OK;
 }
 
-// The hot-row kernel runs beside the row kernels (on the side stream) when
-// some table takes at least this many references in the push: its hottest
-// rows then hold serial chains long enough to keep the whole push waiting
+// The hot-row kernel runs beside the row kernels (on a side stream): its
+// serial chains then overlap the row traffic instead of preceding it
 // (measured on MI355X: 65,536 pairs on one table, 167 -> 133 us a push; 4 x
-// 8.4 M references, 13.4 -> 11.6 ms).  With many tables of fewer references
-// each, the row kernels lose more occupancy beside it than they gain (26
-// tables of ~43,000: 283 -> 321 us), so they run after it.
+// 8.4 M references, 13.4 -> 11.6 ms; 26 tables of ~43,000 references with
+// 64-column units on 256 blocks, 245 -> 236 us a step).  Pushes with a table
+// of at least this many references take 16-column units on 512 blocks, so a
+// very long row's chain data spreads over several CUs.
 constexpr uint64_t kOverlapTableRefs = 1ull << 16;
 constexpr uint32_t kNarrowSlice = 16, kWideSlice = 64;  // columns per hot-row unit
 
 std::atomic<uint32_t> g_spin_limit{1u << 22};
 uint32_t SpinLimit() { return g_spin_limit.load(std::memory_order_relaxed); }
 
-constexpr int kPrimary = 1, kSecond = 2;
+// Phases of a push (kPrimary: the fused update; kSecond: the checked apply)
+// and kOneStream: every kernel on the caller's stream, the hot-row kernel
+// before the row kernels (no side stream or event is created or used, so the
+// push can be captured in a graph).
+constexpr int kPrimary = 1, kSecond = 2, kOneStream = 4;
 constexpr uint64_t kVectorGrid = 4096;  // persistent grid cap of the vector kernels
 constexpr uint64_t kSecondGrid = 32;      // grid cap of the checked apply: it usually exits at
                                           // once, and a small grid launches faster
 constexpr uint64_t kHotGrid = 512;      // two blocks per CU (LDS: four 17 KiB tiles per block)
+// Blocks of the 64-column hot-row kernel beside the row kernels: enough to
+// finish the hot rows well before the row kernels do, few enough to leave
+// them most of the GPU (26 tables of ~43,000 references: 64 blocks 259 us a
+// step of pull + push, 256 blocks 236, 512 blocks 240).
+constexpr uint64_t kWideHotGrid = 256;
 
 template <uint32_t kLog2G>
 int LaunchRowRun(unsigned grid, const VecArgs& a, hipStream_t s) {
@@ -1440,7 +1449,7 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
   a.gs = GuardScalars{0, table_count};  // refs: the prepared valid count
   // The first kernel of the primary phase makes the guard decision.
   uint32_t role = kDecide;
-  bool overlap = false;  // hot rows on the side stream, joined before the checked apply
+  bool overlap = false;  // hot rows (on the side stream, joined before the checked apply)
   Overlap* ov = nullptr;
   for (uint32_t k = 0; k < table_count; ++k) {
     const uint32_t t = plan.table_of_key[k];
@@ -1493,19 +1502,16 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
     uint64_t vector_occurrences = 0;
     for (uint32_t cls = 0; cls + 1 < kClasses; ++cls) vector_occurrences += plan.class_occurrences[cls];
     const uint64_t hot_units = (vector_occurrences / (kLongRefs + 1)) << va.slice_bits;
-    overlap = hot_units && long_rows;
+    overlap = hot_units != 0 && !(phases & kOneStream);
     if (phases & kPrimary) {
       // Grids are multiples of kXcds (the kernels split their work by XCD).
       auto xcd_grid = [](uint64_t b) { return (b + kXcds - 1) / kXcds * kXcds; };
-      // Hot rows first, then the row runs of each class, in stream order: the
-      // two run at full occupancy one after the other (side by side they
-      // compete for the same registers and bandwidth and finish later).
-      // Pushes with very long hot rows run the hot-row kernel beside the row
-      // kernels instead: a few serial chains of up to a million references
-      // then no longer keep the rest of the push waiting.  Both sides make the
-      // guard decision themselves (they read the same inputs and decide the same).
+      // The hot-row kernel on the side stream, beside the row runs of each
+      // class on this one, joined before the checked apply.  Both sides make
+      // the guard decision themselves, from the same snapshot, so they decide
+      // the same.
       if (hot_units) {
-        const uint64_t blocks = xcd_grid(std::min<uint64_t>(hot_units, kHotGrid));
+        const uint64_t blocks = xcd_grid(std::min<uint64_t>(hot_units, long_rows ? kHotGrid : kWideHotGrid));
         va.role = role;
         if (overlap) {
           EPS_HIP_TRY(ThreadOverlap(&ov));
@@ -1513,7 +1519,7 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
           EPS_HIP_TRY(Check(hipStreamWaitEvent(ov->side, ov->fork, 0), "hot-row fork wait"));
           EPS_HIP_TRY(LaunchVectorUpdate(0, slice, unsigned(blocks), va, ov->side));
           EPS_HIP_TRY(Check(hipEventRecord(ov->join, ov->side), "hot-row join"));
-        } else {
+        } else {  // one stream: the hot rows first, deciding; the row kernels follow
           EPS_HIP_TRY(LaunchVectorUpdate(0, slice, unsigned(blocks), va, s));
           role = kFollow;
         }
@@ -1654,6 +1660,23 @@ int eps_hip_push_end(const eps_hip_table* tables, const eps_hip_optimizer* optim
   return PushPhase(tables, optimizers, table_count, features, feature_count, workspace,
                    workspace_bytes, bounds, stream, kSecond);
 }
+
+}  // extern "C"
+
+namespace eps_hip {
+int PushOneStream(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, uint32_t table_count,
+                  const eps_hip_push_feature* features, uint32_t feature_count, void* workspace,
+                  uint64_t workspace_bytes, void* bounds, void* stream) {
+  EPS_HIP_TRY(eps_hip_push_begin(tables, optimizers, table_count, features, feature_count,
+                                 workspace, workspace_bytes, bounds, stream));
+  EPS_HIP_TRY(PushPhase(tables, optimizers, table_count, features, feature_count, workspace,
+                        workspace_bytes, bounds, stream, kPrimary | kOneStream));
+  return PushPhase(tables, optimizers, table_count, features, feature_count, workspace, workspace_bytes,
+                   bounds, stream, kSecond | kOneStream);
+}
+}  // namespace eps_hip
+
+extern "C" {
 
 int eps_hip_push(const eps_hip_table* tables, const eps_hip_optimizer* optimizers,
                  uint32_t table_count, const eps_hip_push_feature* features,

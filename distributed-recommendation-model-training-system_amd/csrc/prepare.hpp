@@ -32,6 +32,12 @@ struct PushPlan {
   std::array<uint64_t, kClasses> class_occurrences{};  // upper bound of sorted positions
 };
 
+// eps_hip_push with every kernel on `stream` (the hot-row kernel before the
+// row kernels): no side stream or event is created or waited on.
+int PushOneStream(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, uint32_t table_count,
+                  const eps_hip_push_feature* features, uint32_t feature_count, void* workspace,
+                  uint64_t workspace_bytes, void* bounds, void* stream);
+
 int PlanPush(const eps_hip_table* tables, uint32_t table_count,
              const eps_hip_push_feature* features, uint32_t feature_count, PushPlan& plan);
 

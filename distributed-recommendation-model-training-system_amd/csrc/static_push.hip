@@ -7,10 +7,13 @@
 // until the process ends) at its own address, found once per device with
 // hipGetSymbolAddress; kernels get that address, never the symbol.  Calls on
 // one GPU share the array, so calls that overlap on one GPU race; each call's
-// preparation clears what must start at zero (with a fill kernel).
+// preparation clears what must start at zero (with a fill kernel).  Every
+// kernel of a call runs on the caller's stream (no side stream or event), and
+// the only runtime calls besides launches are the first call's symbol lookup
+// per device, so a call can be captured in a graph once that lookup is done.
 #include <mutex>
 
-#include "common.hpp"
+#include "prepare.hpp"
 
 namespace {
 constexpr uint64_t kStaticBytes = eps_hip::PushLayout(EPS_HIP_STATIC_MAX_OCCURRENCES).total;
@@ -49,10 +52,13 @@ using namespace eps_hip;
 
 namespace eps_hip {
 namespace {
-// Copies a finished push's status and the workspace history to the caller.
-__global__ void ReportKernel(const Control* ctrl, uint32_t* out) {
+// Copies a finished push's status and the static workspace's history (the
+// failure bits of every static push since the last report) to the caller,
+// then clears the history.
+__global__ void ReportKernel(Control* ctrl, uint32_t* out) {
   out[0] = ctrl->status;
   out[1] = ctrl->history;
+  ctrl->history = 0;
 }
 }  // namespace
 }  // namespace eps_hip
@@ -72,9 +78,10 @@ int eps_hip_push_static(const eps_hip_table* tables, const eps_hip_optimizer* op
   void* ws = nullptr;
   EPS_HIP_TRY(ScratchAddress(&ws));
   EPS_HIP_TRY(eps_hip_prepare(tables, table_count, features, feature_count, ws, kStaticBytes, stream));
-  EPS_HIP_TRY(eps_hip_push(tables, optimizers, table_count, features, feature_count, ws, kStaticBytes, bounds, stream));
+  EPS_HIP_TRY(PushOneStream(tables, optimizers, table_count, features, feature_count, ws, kStaticBytes, bounds,
+                            stream));
   if (status) {
-    hipLaunchKernelGGL(ReportKernel, dim3(1), dim3(1), 0, AsStream(stream), static_cast<const Control*>(ws), status);
+    hipLaunchKernelGGL(ReportKernel, dim3(1), dim3(1), 0, AsStream(stream), static_cast<Control*>(ws), status);
     EPS_HIP_LAUNCHED("static push status");
   }
   return EPS_HIP_OK;

@@ -303,7 +303,15 @@ struct HipCacheBackend::Impl {
     }
   }
 
-  void Activate() { HipOk(hipSetDevice(options.device), "select device"); }
+  // Set when a device push may have been applied in part (a stalled hot-row
+  // hand-over, or a prepared workspace naming rows or gradients the push does
+  // not have): the tables can no longer be trusted, so every later operation
+  // fails with run_failed.  Recovery is a fresh backend and RestoreSnapshot.
+  bool stopped = false;
+  void Activate() {
+    HipOk(hipSetDevice(options.device), "select device");
+    if (stopped) Raise(Code::run_failed, "HIP agent stopped after a device push that may be partial; restore a snapshot");
+  }
   void Await() { HipOk(hipStreamSynchronize(stream), "device work"); }
 
   SlotTable& Table(TableId id) {
@@ -1082,7 +1090,9 @@ std::future<Result<Ack>> HipCacheBackend::PushDevice(std::vector<UpdateContext> 
                           ws, bytes, I.stream));
     AbiOk(eps_hip_push(tables.data(), optimizers.data(), std::uint32_t(tables.size()), features.data(),
                        std::uint32_t(features.size()), ws, bytes, I.bounds.Get(), I.stream));
-    Impl::UpdateVerdict(I.ReadFlag(eps_hip_status_word(ws)));
+    const std::uint32_t status = I.ReadFlag(eps_hip_status_word(ws));
+    if (status & (EPS_HIP_STATUS_STALLED | EPS_HIP_STATUS_BAD_INDEX)) I.stopped = true;
+    Impl::UpdateVerdict(status);
     for (Resident* r : updated) ++r->updates;
     return Ack{};
   });

@@ -268,8 +268,12 @@ int eps_hip_reduce(const eps_hip_table* tables, uint32_t table_count,
  * EPS_HIP_STATIC_MAX_OCCURRENCES occurrences are refused with
  * EPS_HIP_CAPACITY_EXCEEDED before anything is enqueued.  `status` (device
  * memory, 2 u32, may be NULL) receives the push's status word and the array's
- * status history once the push has run.  Every call on one GPU shares that
- * GPU's array: calls that overlap on one GPU race. */
+ * status history (the failure bits of every static push since the last call
+ * that passed `status`, which then clears it) once the push has run.  Every
+ * kernel runs on `stream`, the hot-row kernel before the row kernels (no side
+ * stream or event), so once a device's first call has looked up the array's
+ * address a call can be captured in a graph.  Every call on one GPU shares
+ * that GPU's array: calls that overlap on one GPU race. */
 #define EPS_HIP_STATIC_MAX_OCCURRENCES 262144u
 int eps_hip_push_static(const eps_hip_table* tables, const eps_hip_optimizer* optimizers,
                         uint32_t table_count, const eps_hip_push_feature* features,
@@ -298,9 +302,12 @@ int eps_hip_adam_compact(const eps_hip_table* table, const eps_hip_optimizer* op
  * failure bit but EPS_HIP_STATUS_STALLED, nothing was written.  A stall (a
  * hot-row hand-over that exceeded its spin limit, which no correct run
  * reaches) writes none of the stalled work units' rows; rows of other work
- * units of the same push may have been written (always so when the hot-row
- * kernel ran beside the row kernels, as it does once a table takes 65,536 or
- * more references), so the tables are to be restored, e.g. from a snapshot. */
+ * units of the same push may have been written (the hot-row kernel runs beside
+ * the row kernels, except in eps_hip_push_static), so the tables are to be
+ * restored, e.g. from a snapshot; eps::HipCacheBackend stops after one.  A
+ * bad-index bit from a push whose prepared keys were in range (a damaged
+ * reference word) likewise leaves the rows that reference fed unwritten and
+ * others written. */
 uint32_t* eps_hip_status_word(void* workspace);
 /* Device address of the workspace's status history: the OR of the failure
  * bits of every push or update run in it since it was zeroed (a workspace

@@ -31,6 +31,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include "eps/hip_cache_backend.hpp"
+#include "eps_hip.h"
 #include "eps_oracle.h"
 
 using namespace eps;
@@ -1097,12 +1098,58 @@ void LargeOccurrences() {
   }
 }
 
+// A device push whose hot-row hand-over times out (forced from the host with a
+// spin limit of 0: the hot-row kernel runs for a push with a table of 65,536
+// or more references) may have been applied in part -- the row kernels beside
+// it keep writing -- so the agent stops: that push fails with run_failed, and
+// so does every later operation on the agent.
+void StalledPushStops() {
+  HipCacheOptions o = SmallOptions(4096);
+  o.state_bytes = 64ull << 20;
+  o.transfer_bytes = 16ull << 20;
+  HipCacheBackend gpu(o);
+  constexpr TableId kTable = 21;
+  Take(gpu.Define(Table(kTable, 64)));
+  std::vector<RowState> part;
+  for (Key k = 0; k < 3000; ++k) part.push_back(MakeRow(kTable, k, 64));
+  std::map<Key, LocatedRow> where;
+  for (const auto& loc : Take(gpu.Load(Plan(part), part))) where[loc.row.key] = loc;
+  // 70,000 single-id bags: key 0 in every tenth bag (a hot row), the rest spread.
+  FeatureInput f{kTable, 0, Pooling::sum, {}, {0}, {}};
+  AgentWork w{0, AccessRoute::resident_gpu, 0, {}, {}, {}};
+  std::map<Key, std::uint64_t> unique;
+  for (std::uint64_t b = 0; b < 70000; ++b) {
+    const Key key = b % 10 == 0 ? 0 : 1 + b % 2999;
+    f.keys.push_back(key);
+    f.offsets.push_back(b + 1);
+    f.valid_lengths.push_back(1);
+    auto [it, fresh] = unique.emplace(key, w.rows.size());
+    if (fresh) w.rows.push_back(where.at(key));
+    w.occurrence_to_unique.push_back(it->second);
+  }
+  std::vector<float> g(70000 * 64);
+  for (std::size_t i = 0; i < g.size(); ++i) g[i] = 1e-3f * float(int(i % 17) - 8);
+  const std::vector<UpdateContext> contexts = {{{"stall", 0, 1, Phase::push}, 0, kTable, 1, kLr, 0.81f, 0.998f}};
+  const std::vector<FeatureInput> layouts = {f};
+  const std::vector<AgentWork> work = {w};
+  std::vector<DeviceTensorBlock> blocks = {{0, {70000, 64}, std::make_shared<DeviceBuffer>(g)}};
+  Check(eps_hip_debug_set_spin_limit(0) == 0, "spin limit");
+  const auto code = Fails(gpu.PushDevice(contexts, work, layouts, blocks), "stalled device push");
+  Check(eps_hip_debug_set_spin_limit(1u << 22) == 0, "spin limit");
+  Check(code == Error::Code::run_failed, "a stalled push is the agent's own failure");
+  Check(Fails(gpu.PushDevice(contexts, work, layouts, blocks), "push after a stall") == Error::Code::run_failed,
+        "the agent stopped after a stalled push");
+  Check(Fails(gpu.GatherHost(work, layouts), "gather after a stall") == Error::Code::run_failed,
+        "a stopped agent serves no gathers");
+}
+
 void Main() {
   AtomicReserve();
   SnapshotWriteback();
   DevicePushAtScale();
   MixedPush();
   LargeOccurrences();
+  StalledPushStops();
   auto gpu = std::make_shared<HipCacheBackend>(SmallOptions(8));
   for (const auto& t : {Table(1, 128), Table(2, 64)}) Take(gpu->Define(t));
   Take(gpu->Define(Table(1, 128)));  // identical redefinition is accepted

@@ -7,9 +7,17 @@ workspace's status history.
     (ValidateCompactGradients requires finite scales >= 0,
     src/access/compact_gradients.cpp:21);
   * a hot-row hand-over that times out (driven from the host with a spin limit
-    of 0, so every wait gives up at once) writes nothing and reports STALLED;
+    of 0, so every wait gives up at once) writes none of its hot rows and
+    reports STALLED;
   * a rejected push does not advance the beta powers (ApplyLazyAdam advances
-    them only after the update, src/update/lazy_adam.cpp:39-41).
+    them only after the update, src/update/lazy_adam.cpp:39-41);
+  * the guard decides from a snapshot of the bounds taken before the update,
+    so every block decides the same even when the update's own rows raise the
+    bounds past the limit on the way (1.2 M rows, with and without the
+    hot-row kernel beside the row kernel);
+  * a prepared workspace damaged after preparation is never used as an
+    address: a bad key rejects the push before any write, a bad reference
+    word keeps its row unwritten.
 """
 import numpy as np
 import pytest
@@ -78,11 +86,14 @@ def test_bad_compact_scales_reject(torch_gpu, pkg):
     assert shard.adam_compact(0, slots, offsets, sources, scales, values) & H.STATUS_ERRORS == 0
 
 
-def test_forced_stall_writes_nothing(torch_gpu, pkg):
-    """Spin limit 0: every hot-row hand-over wait times out.  The push must
-    report STALLED and leave every row unchanged (the hot-row kernel skips its
-    staging, adds and stores; the row kernels after it see the stall and write
-    nothing).  With the default limit the same push applies, bit-exact."""
+def test_forced_stall_reports_and_writes_no_hot_row(torch_gpu, pkg):
+    """Spin limit 0: every hand-over wait of the hot-row kernel times out (it
+    runs for pushes with a table of 65,536 or more references, beside the row
+    kernels).  The push must report STALLED, in its status and in the
+    workspace history, and write none of the hot rows it stalled on; the row
+    kernels beside it do write theirs, so such a push is partial -- the C++
+    backend stops after one (tests/cpp/hip_backend_test.cpp).  From fresh
+    state, the same push with the default limit applies bit-exact."""
     torch, W, H = torch_gpu, pkg.workloads, pkg.eps_hip
     rng = np.random.default_rng(12)
     spec = W.TableSpec(0, 64, 3000, seed=6)
@@ -90,8 +101,11 @@ def test_forced_stall_writes_nothing(torch_gpu, pkg):
     shard.init_rows()
     everything = torch.arange(spec.rows, device="cuda")
     before = shard.read_rows(0, everything).clone()
-    f = hot_feature(W, rng, spec, W.MEAN)
-    assert np.max(np.unique(f.keys, return_counts=True)[1]) > 128, "no hot row"
+    f = hot_feature(W, rng, spec, W.MEAN, bags=24000, hot_refs=3000)
+    assert len(f.keys) >= 65536
+    ids, counts = np.unique(f.keys, return_counts=True)
+    hot = torch.from_numpy(ids[counts > 128].astype(np.int64)).cuda()
+    assert hot.numel() > 0, "no hot row"
     dev = [H.DeviceFeature(torch, f)]
     L = H.lib()
     try:
@@ -102,9 +116,10 @@ def test_forced_stall_writes_nothing(torch_gpu, pkg):
         H.check(L.eps_hip_debug_set_spin_limit(1 << 22))
     print(f"forced stall: status {status:#x}", flush=True)
     assert status & H.STATUS_STALLED, f"{status:#x}"
-    assert torch.equal(shard.read_rows(0, everything), before), "a stalled push wrote rows"
     assert shard.history() & H.STATUS_STALLED
+    assert torch.equal(shard.read_rows(0, hot), before[hot]), "a stalled hot row was written"
     shard.clear_history()
+    shard.init_rows()  # fresh state: the stalled push was partial
     shard.prepare(dev)
     status = shard.push(dev)
     assert status & H.STATUS_ERRORS == 0, f"{status:#x}"

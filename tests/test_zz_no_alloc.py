@@ -77,3 +77,47 @@ def test_static_push_matches_workspace_push(torch_gpu, pkg):
     assert b"262144" in L.eps_hip_last_error()
     torch.cuda.synchronize()
     assert torch.equal(static.state[0], before)
+
+
+def test_static_push_replays_in_a_graph(torch_gpu, pkg):
+    """A static push captured in a HIP graph: every kernel runs on the
+    capturing stream (no side stream or event), so the capture holds the
+    whole push.  Each of three replays, with eager work and synchronisations
+    between them, must leave the tables bit-identical to the same push run
+    eagerly with a caller workspace (the optimizer powers are the captured
+    ones, so the eager pushes keep them too), and report a clean status."""
+    torch, W, H = torch_gpu, pkg.workloads, pkg.eps_hip
+    L = H.lib()
+    specs = [W.TableSpec(0, 64, 20000, seed=71)]
+    captured, eager, warm = (H.DeviceShard(torch, specs) for _ in range(3))
+    for shard in (captured, eager, warm):
+        shard.init_rows()
+    rng = np.random.default_rng(72)
+    feats = features(W, rng, specs, 3000)
+    dev = [H.DeviceFeature(torch, f) for f in feats]
+    arr = captured._push_args(dev)
+    out = torch.full((2,), -1, dtype=torch.int32, device="cuda")
+    # One eager call first: it looks the static array's address up on this device.
+    warm_stream = C.c_void_p(torch.cuda.current_stream().cuda_stream)
+    H.check(L.eps_hip_push_static(warm.tables, warm._opts, len(specs), warm._push_args(dev), len(dev),
+                                  warm.bounds.data_ptr(), out.data_ptr(), warm_stream))
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        H.check(L.eps_hip_push_static(captured.tables, captured._opts, len(specs), arr, len(dev),
+                                      captured.bounds.data_ptr(), out.data_ptr(), C.c_void_p(side.cuda_stream)))
+    scratch = torch.ones(1 << 20, device="cuda")
+    for replay in range(3):
+        print(f"case: graph replay {replay}", flush=True)
+        out.fill_(-1)
+        graph.replay()
+        scratch.mul_(1.5).add_(1.0)  # eager work between replays
+        torch.cuda.synchronize()
+        eager.prepare(dev)
+        eager.push(dev, advance=False)
+        want = eager.status()
+        assert want & H.STATUS_ERRORS == 0, f"{want:#x}"
+        got, history = (int(x) & 0xFFFFFFFF for x in out.cpu().tolist())
+        assert got == want and history & H.STATUS_ERRORS == 0, f"replay {replay}: {got:#x} / {history:#x}"
+        assert torch.equal(captured.state[0], eager.state[0]), f"replay {replay}: states differ"
