@@ -1704,6 +1704,8 @@ int eps_hip_reduce(const eps_hip_table* tables, uint32_t table_count,
   for (uint32_t t = 0; t < table_count; ++t) max_dim = std::max(max_dim, tables[t].dim);
   if (row_stride < max_dim || (row_stride % 4 && max_dim % 4 == 0 && max_dim <= 256))
     return Fail(EPS_HIP_INVALID_ARGUMENT, "row stride must cover every dimension (multiple of 4)");
+  EPS_HIP_TRY(PrepareWithOccurrences(tables, table_count, features, feature_count, workspace, workspace_bytes,
+                                     stream));
   if (!plan.occurrences) return EPS_HIP_OK;
   auto* ws = static_cast<uint8_t*>(workspace);
   return RunSorted(tables, nullptr, table_count, features, feature_count, plan, L, ws, true,

@@ -24,7 +24,7 @@ constexpr uint32_t kRadixBits = 9;        // largest radix digit
 constexpr uint32_t kDigits = 1u << kRadixBits;
 constexpr uint32_t kDigitsPerThread = kDigits / kBlock;  // the sort kernels assume two
 static_assert(kDigitsPerThread == 2, "radix digits per thread");
-constexpr uint32_t kKeygenItems = 4;      // occurrences per keygen thread
+constexpr uint32_t kKeygenItems = 8;      // occurrences per keygen thread
 constexpr uint32_t kClasses = 6;          // 5 vector widths + generic
 constexpr uint32_t kRefRowBits = 27;      // gradient row bits in a reference word
 static_assert(kRefRowBits == kGuardRefRowBits, "one reference word layout");

@@ -163,7 +163,7 @@ __global__ void __launch_bounds__(kBlock) KeygenKernel(PrepArgs args) {
     const uint64_t row = f.pooling == EPS_HIP_POOL_SEQUENCE ? li[k] : lo[k];
     if (s != kHole) scale_max = max(scale_max, AbsBits(scale[k]));
     args.keys[gi] = key;
-    args.vals[gi] = uint32_t(gi);
+    if (args.vals) args.vals[gi] = uint32_t(gi);
     args.refscale[gi] = (uint64_t(__float_as_uint(scale[k])) << 32) |
                         (uint64_t(f.feature) << kRefRowBits) | row;
     for (uint32_t p = 0; p < args.passes; ++p)
@@ -205,6 +205,10 @@ __device__ __forceinline__ uint32_t BlockExclusiveScan(uint32_t x, uint32_t* s_w
   return before + inc - x;
 }
 
+// kVals: the occurrence indices travel with the keys (for eps_hip_unique and
+// eps_hip_reduce, which map sorted positions back to occurrences); a push
+// needs only the keys and reference words.
+template <bool kVals>
 __global__ void __launch_bounds__(kBlock) RadixPassKernel(
     const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
     uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out,
@@ -217,7 +221,7 @@ __global__ void __launch_bounds__(kBlock) RadixPassKernel(
   __shared__ uint32_t s_global[kDigits];
   __shared__ uint32_t s_scan[4];
   __shared__ uint32_t s_keys[kSortTile];
-  __shared__ uint32_t s_vals[kSortTile];
+  __shared__ uint32_t s_vals[kVals ? kSortTile : 1];
   __shared__ uint64_t s_rs[kSortTile];
 
   const uint32_t t = threadIdx.x, lane = t & (kWave - 1), wave = t / kWave;
@@ -241,7 +245,7 @@ __global__ void __launch_bounds__(kBlock) RadixPassKernel(
   for (uint32_t i = 0; i < kSortItems; ++i) {
     const uint32_t p = base + i * kWave + lane;
     key[i] = p < n ? keys_in[p] : 0u;
-    val[i] = p < n ? vals_in[p] : 0u;
+    val[i] = kVals && p < n ? vals_in[p] : 0u;
     rs[i] = p < n ? rs_in[p] : 0ull;
   }
   const uint64_t lt_mask = (1ull << lane) - 1;
@@ -388,7 +392,7 @@ __global__ void __launch_bounds__(kBlock) RadixPassKernel(
       const uint32_t digit = (key[i] >> shift) & mask;
       const uint32_t at = s_tile_start[digit] + s_wcount[wave][digit] + rank[i];
       s_keys[at] = key[i];
-      s_vals[at] = val[i];
+      if (kVals) s_vals[at] = val[i];
       s_rs[at] = rs[i];
     }
   }
@@ -403,7 +407,7 @@ __global__ void __launch_bounds__(kBlock) RadixPassKernel(
   for (uint32_t i = 0; i < kSortItems; ++i) {
     const uint32_t q = i * kBlock + t;
     key[i] = s_keys[q];
-    val[i] = s_vals[q];
+    if (kVals) val[i] = s_vals[q];
     rs[i] = s_rs[q];
     const uint32_t digit = (key[i] >> shift) & mask;
     dest[i] = s_global[digit] + (q - s_tile_start[digit]);
@@ -412,7 +416,7 @@ __global__ void __launch_bounds__(kBlock) RadixPassKernel(
   for (uint32_t i = 0; i < kSortItems; ++i) {
     if (i * kBlock + t < tile_n) {
       keys_out[dest[i]] = key[i];
-      vals_out[dest[i]] = val[i];
+      if (kVals) vals_out[dest[i]] = val[i];
       rs_out[dest[i]] = rs[i];
     }
   }
@@ -658,9 +662,12 @@ uint64_t eps_hip_push_workspace_bytes(uint64_t occurrences) {
   return PushLayout(occurrences).total;
 }
 
-int eps_hip_prepare(const eps_hip_table* tables, uint32_t table_count,
-                    const eps_hip_push_feature* features, uint32_t feature_count,
-                    void* workspace, uint64_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace eps_hip {
+namespace {
+int Prepare(const eps_hip_table* tables, uint32_t table_count, const eps_hip_push_feature* features,
+            uint32_t feature_count, void* workspace, uint64_t workspace_bytes, void* stream, bool with_vals) {
   PushPlan plan;
   EPS_HIP_TRY(PlanPush(tables, table_count, features, feature_count, plan));
   const PushLayout L(plan.occurrences);
@@ -669,10 +676,13 @@ int eps_hip_prepare(const eps_hip_table* tables, uint32_t table_count,
   auto* ws = static_cast<uint8_t*>(workspace);
   auto* ctrl = reinterpret_cast<Control*>(ws);
   const hipStream_t s = AsStream(stream);
-  // Control block (but its status history), histograms and look-back flags
-  // start at zero.
-  EPS_HIP_TRY(LaunchFill(reinterpret_cast<uint32_t*>(ws), 0, L.keys_a / 4, s, kHistoryWord));
-  if (!plan.occurrences) return EPS_HIP_OK;
+  // Control block (but its status history), histograms and the look-back
+  // flags of the passes this push sorts with start at zero.
+  if (!plan.occurrences)
+    return LaunchFill(reinterpret_cast<uint32_t*>(ws), 0, sizeof(Control) / 4, s, kHistoryWord);
+  EPS_HIP_TRY(LaunchFill(reinterpret_cast<uint32_t*>(ws), 0, (L.look + plan.passes * L.tiles * kDigits * 4) / 4, s,
+                         kHistoryWord));
+  EPS_HIP_TRY(LaunchFill(reinterpret_cast<uint32_t*>(ws + L.group_look), 0, plan.passes * L.groups * kDigits, s));
 
   PrepArgs args{};
   args.count = feature_count;
@@ -683,7 +693,7 @@ int eps_hip_prepare(const eps_hip_table* tables, uint32_t table_count,
   args.ctrl = ctrl;
   args.hist = reinterpret_cast<uint32_t*>(ws + L.hist);
   args.keys = reinterpret_cast<uint32_t*>(ws + L.keys_a);
-  args.vals = reinterpret_cast<uint32_t*>(ws + L.vals_a);
+  args.vals = with_vals ? reinterpret_cast<uint32_t*>(ws + L.vals_a) : nullptr;
   // Reference words ping-pong between two buffers through the passes and
   // end in sorted_rs: keygen writes them where an even number of swaps
   // before the end starts.
@@ -711,7 +721,8 @@ int eps_hip_prepare(const eps_hip_table* tables, uint32_t table_count,
   auto* group_look = reinterpret_cast<uint32_t*>(ws + L.group_look);
   const uint32_t n = uint32_t(plan.occurrences);
   for (uint32_t p = 0; p < plan.passes; ++p) {
-    hipLaunchKernelGGL(RadixPassKernel, dim3(unsigned(L.tiles)), dim3(kBlock), 0, s, keys[p % 2], vals[p % 2],
+    hipLaunchKernelGGL(with_vals ? RadixPassKernel<true> : RadixPassKernel<false>, dim3(unsigned(L.tiles)),
+                       dim3(kBlock), 0, s, keys[p % 2], vals[p % 2],
                        keys[(p + 1) % 2], vals[(p + 1) % 2], rs[p % 2], rs[(p + 1) % 2], n,
                        plan.shift[p], plan.bits[p],
                        args.hist + p * kDigits, look + uint64_t(p) * L.tiles * kDigits,
@@ -734,6 +745,22 @@ int eps_hip_prepare(const eps_hip_table* tables, uint32_t table_count,
   EPS_HIP_LAUNCHED("hot rows");
   return EPS_HIP_OK;
 }
+}  // namespace
+
+int PrepareWithOccurrences(const eps_hip_table* tables, uint32_t table_count,
+                           const eps_hip_push_feature* features, uint32_t feature_count, void* workspace,
+                           uint64_t workspace_bytes, void* stream) {
+  return Prepare(tables, table_count, features, feature_count, workspace, workspace_bytes, stream, true);
+}
+}  // namespace eps_hip
+
+extern "C" {
+
+int eps_hip_prepare(const eps_hip_table* tables, uint32_t table_count,
+                    const eps_hip_push_feature* features, uint32_t feature_count,
+                    void* workspace, uint64_t workspace_bytes, void* stream) {
+  return Prepare(tables, table_count, features, feature_count, workspace, workspace_bytes, stream, false);
+}
 
 int eps_hip_unique(const eps_hip_table* tables, uint32_t table_count,
                    const eps_hip_push_feature* features, uint32_t feature_count,
@@ -747,6 +774,8 @@ int eps_hip_unique(const eps_hip_table* tables, uint32_t table_count,
     return Fail(EPS_HIP_CAPACITY_EXCEEDED, "push workspace too small");
   if (!unique_slots || !unique_tables || !occurrence_to_unique)
     return Fail(EPS_HIP_INVALID_ARGUMENT, "null unique outputs");
+  EPS_HIP_TRY(PrepareWithOccurrences(tables, table_count, features, feature_count, workspace, workspace_bytes,
+                                     stream));
   auto* ws = static_cast<uint8_t*>(workspace);
   auto* ctrl = reinterpret_cast<Control*>(ws);
   const hipStream_t s = AsStream(stream);

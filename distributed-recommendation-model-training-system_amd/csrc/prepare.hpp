@@ -38,6 +38,12 @@ int PushOneStream(const eps_hip_table* tables, const eps_hip_optimizer* optimize
                   const eps_hip_push_feature* features, uint32_t feature_count, void* workspace,
                   uint64_t workspace_bytes, void* bounds, void* stream);
 
+// eps_hip_prepare with the occurrence indices carried through the sort (the
+// sorted position -> occurrence map eps_hip_unique and eps_hip_reduce use).
+int PrepareWithOccurrences(const eps_hip_table* tables, uint32_t table_count,
+                           const eps_hip_push_feature* features, uint32_t feature_count, void* workspace,
+                           uint64_t workspace_bytes, void* stream);
+
 int PlanPush(const eps_hip_table* tables, uint32_t table_count,
              const eps_hip_push_feature* features, uint32_t feature_count, PushPlan& plan);
 

@@ -243,16 +243,20 @@ int eps_hip_push_end(const eps_hip_table* tables, const eps_hip_optimizer* optim
                      uint32_t table_count, const eps_hip_push_feature* features,
                      uint32_t feature_count, void* workspace, uint64_t workspace_bytes,
                      void* bounds, void* stream);
-/* Unique rows of a prepared workspace in first-occurrence order (PrepareFeature /
+/* Unique rows of the features in first-occurrence order (PrepareFeature /
  * ReduceGradients row order): unique_slots[u], unique_tables[u],
- * occurrence_to_unique[i] (UINT64_MAX for holes), and the count (device u64). */
+ * occurrence_to_unique[i] (UINT64_MAX for holes), and the count (device u64).
+ * Prepares the workspace itself, keeping each sorted position's occurrence
+ * index (which eps_hip_prepare leaves out); the workspace then also serves
+ * eps_hip_push. */
 int eps_hip_unique(const eps_hip_table* tables, uint32_t table_count,
                    const eps_hip_push_feature* features, uint32_t feature_count,
                    void* workspace, uint64_t workspace_bytes, uint64_t* unique_slots,
                    uint32_t* unique_tables, uint64_t* occurrence_to_unique,
                    uint64_t* unique_count, void* stream);
-/* ReduceGradients values of a prepared workspace after eps_hip_unique: row u
- * written at values + u * row_stride (first-occurrence order). */
+/* ReduceGradients values with eps_hip_unique's occurrence map: row u written
+ * at values + u * row_stride (first-occurrence order).  Prepares the workspace
+ * itself, as eps_hip_unique does. */
 int eps_hip_reduce(const eps_hip_table* tables, uint32_t table_count,
                    const eps_hip_push_feature* features, uint32_t feature_count,
                    void* workspace, uint64_t workspace_bytes,
