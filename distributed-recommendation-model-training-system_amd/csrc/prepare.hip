@@ -541,7 +541,11 @@ __global__ void __launch_bounds__(kBlock) HotListKernel(HotArgs a) {
   const uint32_t end = SegmentEndSearch(a.keys, p + kLongRefs, a.n, key), refs = end - p;
   const uint32_t bucket = refs >= 2048 ? 0u : refs >= 1024 ? 1u : refs >= 512 ? 2u : 3u;
   const uint32_t list = uint32_t(uint64_t(p) * kXcds / a.n) * kHotBuckets + bucket;
-  a.hot[uint64_t(list) * a.capacity + atomicAdd(&a.ctrl->long_count[list], 1u)] = HotEntry{p, end, key, 0u};
+  // Sorted keys give each hot row one first position, so a list never holds
+  // more than n / 129 entries; the bound keeps the write inside the list
+  // whatever the keys (the readers clamp the counts to the capacity too).
+  const uint32_t at = atomicAdd(&a.ctrl->long_count[list], 1u);
+  if (at < a.capacity) a.hot[uint64_t(list) * a.capacity + at] = HotEntry{p, end, key, 0u};
 }
 
 struct UniqueArgs {
@@ -620,6 +624,7 @@ int PlanPush(const eps_hip_table* tables, uint32_t table_count,
   plan.key_bits = BitLength(max_valid + 1);
   if (plan.key_bits > 32) return Fail(EPS_HIP_CAPACITY_EXCEEDED, "table rows exceed 32-bit sort keys");
   plan.passes = (plan.key_bits + kRadixBits - 1) / kRadixBits;
+  if (plan.passes > kMaxPasses) return Fail(EPS_HIP_CAPACITY_EXCEEDED, "sort keys need too many passes");
   uint32_t at = 0;
   for (uint32_t p = 0; p < plan.passes; ++p) {
     const uint32_t remaining = plan.key_bits - at, left = plan.passes - p;
