@@ -29,7 +29,8 @@ reference CPU shard (or the oracle's C restatement of it) on the host over a
 bounded sample, on one core and on the GPU's share of host cores.
 
 `--ceiling` instead measures what the memory system gives the fused update's
-access pattern (eps_hip_probe_row_rmw): the config's first batch's unique rows
+access pattern (eps_measure_row_rmw of libeps_hip_measure.so, a measurement
+library beside the kernel library): the config's first batch's unique rows
 (sorted, one scratch table holding every table's rows) read and written back
 with one gradient row each, for several loads-in-flight and grid shapes, and
 the same count of consecutive rows; one JSON line per variant.
@@ -282,7 +283,12 @@ def ceiling(config):
     grads = torch.randn(grad_rows * dim, dtype=torch.float32, device="cuda") * 1e-2
     lists = {"sorted unique rows of the batch": torch.from_numpy(slots.view(np.int64)).cuda(),
              "consecutive rows": torch.arange(n, dtype=torch.int64, device="cuda")}
-    fn = H.lib().eps_hip_probe_row_rmw
+    measure = C.CDLL(str(H.HERE / "libeps_hip_measure.so"))
+    fn = measure.eps_measure_row_rmw
+    fn.restype = C.c_int
+    fn.argtypes = [C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint64, C.c_uint32,
+                   C.c_uint32, C.c_void_p]
+    measure.eps_measure_last_error.restype = C.c_char_p
     stream = torch.cuda.current_stream()
     row_bytes = 2 * 3 * dim * 4 + dim * 4
     full = (n * dim // 4 + 255) // 256
@@ -294,7 +300,7 @@ def ceiling(config):
                             C.c_void_p(grads.data_ptr()), grad_rows, rows_per_group, grid,
                             C.c_void_p(stream.cuda_stream))
                     if rc:
-                        raise RuntimeError(H.lib().eps_hip_last_error().decode())
+                        raise RuntimeError(measure.eps_measure_last_error().decode())
                 for _ in range(3):
                     launch()
                 start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)

@@ -119,8 +119,6 @@ SYMBOLS = {
     "eps_hip_status_word": (C.c_void_p, [C.c_void_p]),
     "eps_hip_status_history_word": (C.c_void_p, [C.c_void_p]),
     "eps_hip_debug_set_spin_limit": (C.c_int, [C.c_uint32]),
-    "eps_hip_probe_row_rmw": (C.c_int, [C.c_void_p, C.c_uint32, C.c_void_p, C.c_uint64, C.c_void_p, C.c_uint64,
-                                        C.c_uint32, C.c_uint32, C.c_void_p]),
     "eps_hip_read_status": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p]),
     "eps_hip_fill_u32": (C.c_int, [C.c_void_p, C.c_uint32, C.c_uint64, C.c_void_p]),
 }

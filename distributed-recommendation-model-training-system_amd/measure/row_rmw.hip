@@ -1,4 +1,6 @@
-// probe.hip -- the bandwidth ceiling of the row update's access pattern.
+// row_rmw.hip -- the bandwidth ceiling of the row update's access pattern.
+// Measurement code only: built into libeps_hip_measure.so, which bench.py's
+// ceiling run loads; the kernel library and its C ABI do not contain it.
 //
 // The fused update reads each touched row's [w | m | v] (3 x dim floats, at a
 // random slot), reads the gradient rows that reference it, and writes the row
@@ -7,7 +9,12 @@
 // pattern: the row update's roofline measured instead of assumed.  It changes
 // the rows it is given (w -= 1e-3 * m and the moments move), so it runs on a
 // scratch table only.
-#include "common.hpp"
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <string>
+
+#include "../csrc/common.hpp"
 
 namespace eps_hip {
 namespace {
@@ -62,18 +69,33 @@ __global__ void __launch_bounds__(kBlock) RowRmwProbeKernel(float* state, uint32
 
 using namespace eps_hip;
 
-extern "C" int eps_hip_probe_row_rmw(float* state, uint32_t dim, const uint64_t* slots, uint64_t n,
-                                     const float* gradients, uint64_t gradient_rows, uint32_t rows_per_group,
-                                     uint32_t grid, void* stream) {
+namespace {
+thread_local std::string measure_error;
+int Reject(const char* message) {
+  measure_error = message;
+  return EPS_HIP_INVALID_ARGUMENT;
+}
+}  // namespace
+
+// For list entries i < n: read row slots[i]'s [w | m | v] (3 x dim floats of
+// `state`) and one gradient row (gradients + ((i * 0x9E3779B1) %
+// gradient_rows) * dim), apply a fixed moment update, write the row back.
+// Every slot must be < the rows `state` holds and distinct; the rows are
+// changed, so `state` is a scratch table.  dim: a power of two in [4, 256];
+// rows_per_group: 1, 2 or 4 entries with their loads in flight per group of
+// dim/4 lanes; grid: workgroups of 256.  Returns 0 or EPS_HIP_INVALID_ARGUMENT
+// / EPS_HIP_RUN_FAILED with eps_measure_last_error() saying why.
+extern "C" int eps_measure_row_rmw(float* state, uint32_t dim, const uint64_t* slots, uint64_t n,
+                                   const float* gradients, uint64_t gradient_rows, uint32_t rows_per_group,
+                                   uint32_t grid, void* stream) {
   if (!n) return EPS_HIP_OK;
-  if (!state || !slots || !gradients || !gradient_rows)
-    return Fail(EPS_HIP_INVALID_ARGUMENT, "null row probe buffers");
+  if (!state || !slots || !gradients || !gradient_rows) return Reject("null row probe buffers");
   if (dim < 4 || dim > 256 || (dim & (dim - 1)))
-    return Fail(EPS_HIP_INVALID_ARGUMENT, "row probe dimension must be a power of two in [4, 256]");
-  if (grid == 0 || grid > 65536) return Fail(EPS_HIP_INVALID_ARGUMENT, "row probe grid must be in [1, 65536]");
+    return Reject("row probe dimension must be a power of two in [4, 256]");
+  if (grid == 0 || grid > 65536) return Reject("row probe grid must be in [1, 65536]");
   uint32_t log2g = 0;
   while ((4u << log2g) < dim) ++log2g;
-  const hipStream_t s = AsStream(stream);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
   switch (rows_per_group) {
     case 1: hipLaunchKernelGGL(RowRmwProbeKernel<1>, dim3(grid), dim3(kBlock), 0, s, state, dim, log2g, slots, n,
                                gradients, gradient_rows); break;
@@ -81,8 +103,14 @@ extern "C" int eps_hip_probe_row_rmw(float* state, uint32_t dim, const uint64_t*
                                gradients, gradient_rows); break;
     case 4: hipLaunchKernelGGL(RowRmwProbeKernel<4>, dim3(grid), dim3(kBlock), 0, s, state, dim, log2g, slots, n,
                                gradients, gradient_rows); break;
-    default: return Fail(EPS_HIP_INVALID_ARGUMENT, "row probe rows per group must be 1, 2 or 4");
+    default: return Reject("row probe rows per group must be 1, 2 or 4");
   }
-  EPS_HIP_LAUNCHED("row probe");
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    measure_error = std::string("row probe launch: ") + hipGetErrorString(e);
+    return EPS_HIP_RUN_FAILED;
+  }
   return EPS_HIP_OK;
 }
+
+extern "C" const char* eps_measure_last_error() { return measure_error.c_str(); }

@@ -329,18 +329,6 @@ int eps_hip_fill_u32(uint32_t* target, uint32_t value, uint64_t count, void* str
  * at once, so tests can drive the stall path from the host. */
 int eps_hip_debug_set_spin_limit(uint32_t polls);
 
-/* Measurement hook, no counterpart in the reference: the fused update's memory
- * traffic without its bookkeeping.  For list entries i < n: read row
- * slots[i]'s [w | m | v] (3 x dim floats of `state`) and one gradient row
- * (gradients + ((i * 0x9E3779B1) % gradient_rows) * dim), apply a fixed
- * moment update, write the row back.  Every slot must be < the rows `state`
- * holds and distinct; the rows are changed, so `state` is a scratch table.
- * dim: a power of two in [4, 256]; rows_per_group: 1, 2 or 4 entries with
- * their loads in flight per group of dim/4 lanes; grid: workgroups of 256. */
-int eps_hip_probe_row_rmw(float* state, uint32_t dim, const uint64_t* slots, uint64_t n,
-                          const float* gradients, uint64_t gradient_rows, uint32_t rows_per_group,
-                          uint32_t grid, void* stream);
-
 #ifdef __cplusplus
 }
 #endif

@@ -58,3 +58,21 @@ def test_host_only_queries(pkg):
     rc = L.eps_hip_prepare(None, 0, None, 0, None, 0, None)
     assert rc == pkg.eps_hip.INVALID_ARGUMENT
     assert b"tables" in L.eps_hip_last_error()
+
+
+def test_measurement_library_is_separate(pkg):
+    """The row read-modify-write ceiling kernel lives in libeps_hip_measure.so,
+    which only bench.py's ceiling run loads; the kernel library exports
+    nothing that is not in include/eps_hip.h."""
+    kernels = subprocess.run(["nm", "-D", "--defined-only", str(pkg.eps_hip.LIB_PATH)], capture_output=True,
+                             text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (eps_\w+)", kernels))
+    assert exported == set(declared("eps_hip.h")), sorted(exported ^ set(declared("eps_hip.h")))
+    measure = ctypes.CDLL(str(pkg.eps_hip.HERE / "libeps_hip_measure.so"))
+    measure.eps_measure_last_error.restype = ctypes.c_char_p
+    fn = measure.eps_measure_row_rmw
+    fn.argtypes = [ctypes.c_void_p, ctypes.c_uint32, ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p,
+                   ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint32, ctypes.c_void_p]
+    assert fn(None, 64, None, 0, None, 0, 1, 1, None) == 0  # nothing to do
+    assert fn(None, 64, None, 8, None, 8, 1, 1, None) == pkg.eps_hip.INVALID_ARGUMENT
+    assert b"null" in measure.eps_measure_last_error()
