@@ -565,10 +565,12 @@ __global__ void __launch_bounds__(kBlock) SortedUpdateKernel(FusedArgs a) {
 //    the unit's w, m, v when the chunk is its last.  Tiles change hands
 //    through two LDS counters per tile (staged / added), so the waves never
 //    meet at a block barrier, and each producer keeps two chunks of rows in
-//    flight.  The slices are narrow (16 columns) so that a hot row's chain
-//    data spreads over several CUs: a block's producers then move a quarter
-//    of a 64-column chunk's bytes through their CU per chunk, and the adding
-//    wave's serial chain, not the CU's memory pipeline, sets the rate.
+//    flight.  For very long rows the slices are narrow (32 columns) so that a
+//    hot row's chain data spreads over several CUs: a block's producers then
+//    move half of a 64-column chunk's bytes through their CU per chunk, and
+//    the adding wave's serial chain, not the CU's memory pipeline, sets the
+//    rate; a 32-column slice of a reference is one whole 128-byte line, so
+//    no line is fetched for part of its bytes.
 //  * RowRunKernel: every other row.  A block owns a window of sorted
 //    positions (RunPositions: 256, or 128 / 64 for 32- / 64-lane groups, so
 //    every group has a few rows per window whatever the width); it stages
@@ -580,7 +582,7 @@ constexpr uint32_t kHotBlock = 256;                       // threads of a hot-ro
 constexpr uint32_t kHotRing = 4;                          // chunks staged in LDS per block
 constexpr uint32_t kUnitCache = 512;                      // unit headers a block stages in LDS
 constexpr uint32_t kHotPitch = kHotChunk + 4;             // floats per tile row (one column)
-// Shape of a hot-row unit of kS columns (16 or 64): lanes per reference in a
+// Shape of a hot-row unit of kS columns (32 or 64): lanes per reference in a
 // producer's row load, references per row load, row loads per producer lane
 // per chunk.
 template <uint32_t kS>
@@ -614,6 +616,7 @@ struct VecArgs {
   uint32_t row_bits, cls, role, slice_bits, hot_capacity, tables, features;
   uint32_t n;           // sorted positions of the push (hot-row entries are clamped to them)
   uint32_t spin_limit;  // polls of a hot-row hand-over wait (0: give up at once)
+  uint32_t class_block[kClasses], class_grid[kClasses];  // RowRunClassesKernel's blocks per class
 };
 static_assert(sizeof(VecArgs) <= 4096, "update arguments fit the kernel-argument segment");
 
@@ -1076,48 +1079,47 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
   FinishBlock<kHotBlock / kWave>(st, ctrl, a.bounds, write);
 }
 
-// Seven waves per SIMD (72 registers) where that needs no spill: more rows'
-// loads in flight per CU.
+// LDS of a row-run block, sized for the widest window.
+struct RunShared {
+  uint32_t key[kRunPositions + kLongRefs + 1];  // key[i + 1] = key at position p0 + i
+  const float* src[kRunPositions + kLongRefs];  // gradient row of position p0 + i
+  float scale[kRunPositions + kLongRefs];
+  uint32_t heads[kRunPositions];
+  uint32_t wave_heads[kBlock / kWave];
+  uint32_t next;  // next unclaimed row (head index) of the window
+  uint32_t bad;
+};
+
+// The rows of dimension class `cls` (groups of 2^kLog2G lanes), for block
+// `block` of the `grid` blocks the class has.
 template <uint32_t kLog2G>
-__global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kLog2G == 2 || kLog2G == 6 ? 6 : 7)))
-RowRunKernel(VecArgs a) {
+__device__ __forceinline__ void RowRuns(const VecArgs& a, RunShared& sh, const TableDesc* s_t,
+                                        const float* const* s_grad, const uint64_t* s_rows, uint32_t cls,
+                                        uint32_t block, uint32_t grid, bool write, RowStats& st) {
   constexpr uint32_t G = 1u << kLog2G;
   constexpr uint32_t ngroups = kBlock / G;
   constexpr uint32_t kWindow = RunPositions(kLog2G);
   constexpr uint32_t kStaged = kWindow + kLongRefs;
-  __shared__ TableDesc s_t[EPS_HIP_MAX_TABLES];
-  __shared__ const float* s_grad[EPS_HIP_MAX_FEATURES];
-  __shared__ uint32_t s_key[kStaged + 1];   // s_key[i + 1] = key at position p0 + i
-  __shared__ const float* s_src[kStaged];   // gradient row of position p0 + i
-  __shared__ float s_scale[kStaged];
-  __shared__ uint32_t s_heads[kWindow];
-  __shared__ uint32_t s_wave_heads[kBlock / kWave];
-  __shared__ uint32_t s_next;               // next unclaimed row (head index) of the window
-  __shared__ uint32_t s_mode, s_bad;
-  __shared__ uint64_t s_rows[EPS_HIP_MAX_FEATURES];  // gradient rows per feature
-  bool write = false;
-  if (!VecPrologue(a, s_t, s_grad, &s_mode, write, s_rows)) return;
+  static_assert(kStaged <= kRunPositions + kLongRefs, "row-run window fits its LDS");
   Control* ctrl = a.ctrl;
   // Safe address for reads a damaged workspace would point elsewhere: the
   // control block and what follows it (far more than a row of 3 x 256 floats).
   const float* safe = reinterpret_cast<const float*>(a.ctrl);
-  const uint32_t begin = ctrl->class_start[a.cls], end = ctrl->class_start[a.cls + 1];
+  const uint32_t begin = ctrl->class_start[cls], end = ctrl->class_start[cls + 1];
   const uint32_t row_mask = (1u << a.row_bits) - 1;
   const uint32_t lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   const uint32_t lig = threadIdx.x & (G - 1), gid = threadIdx.x >> kLog2G;
   const uint32_t c = lig * 4;
-  RowStats st;
   // The class's positions are cut into kXcds contiguous ranges, one per XCD
-  // (the grid is a multiple of kXcds and blocks reach the XCDs round robin):
-  // the gradient rows a range references then come from a few features and
-  // stay in that XCD's L2 for all their references.  Rows that straddle a cut
-  // belong to the range holding their first position.
-  const uint32_t xcd = blockIdx.x % kXcds, per_xcd = gridDim.x / kXcds;
+  // (the class's blocks start at a multiple of kXcds and number a multiple of
+  // it, and blocks reach the XCDs round robin): the gradient rows a range
+  // references then come from a few features and stay in that XCD's L2 for
+  // all their references.  Rows that straddle a cut belong to the range
+  // holding their first position.
+  const uint32_t xcd = block % kXcds, per_xcd = grid / kXcds;
   const uint32_t span = ((end - begin + kXcds - 1) / kXcds + kWindow - 1) / kWindow * kWindow;
   const uint32_t xbegin = min(begin + xcd * span, end), xend = min(xbegin + span, end);
-  if (threadIdx.x == 0) s_bad = 0;
-  __syncthreads();
-  for (uint32_t p0 = xbegin + (blockIdx.x / kXcds) * kWindow; p0 < xend; p0 += per_xcd * kWindow) {
+  for (uint32_t p0 = xbegin + (block / kXcds) * kWindow; p0 < xend; p0 += per_xcd * kWindow) {
     const uint32_t p1 = min(p0 + kWindow, xend);
     const uint32_t lim = min(p1 + kLongRefs, end);
     const uint32_t staged = lim - p0;
@@ -1126,13 +1128,13 @@ RowRunKernel(VecArgs a) {
     // scale (one coalesced pass; the table and feature lookups happen here
     // once per position instead of once per lane).
     if (threadIdx.x == 0) {
-      s_key[0] = p0 > begin ? a.keys[p0 - 1] : ~a.keys[p0];
-      s_next = ngroups;
+      sh.key[0] = p0 > begin ? a.keys[p0 - 1] : ~a.keys[p0];
+      sh.next = ngroups;
     }
     for (uint32_t i = threadIdx.x; i < staged; i += kBlock) {
       const uint32_t key = a.keys[p0 + i];
       const uint64_t word = a.rs[p0 + i];
-      s_key[i + 1] = key;
+      sh.key[i + 1] = key;
       // A key or reference that names no table, slot, feature or gradient row
       // of the push (a damaged workspace) is read from a safe address instead,
       // and the block writes nothing from then on.
@@ -1143,37 +1145,37 @@ RowRunKernel(VecArgs a) {
       const bool ok = KeyInRange(kp, a.tables, s_t[ti].rows) && RefInRange(rp, a.features, s_rows[fi]);
       float scale;
       const float* src = RefSource(s_grad, word, s_t[ti].dim, 0, scale);
-      s_src[i] = ok ? src : safe;
-      s_scale[i] = scale;
-      if (!ok) s_bad = 1;
+      sh.src[i] = ok ? src : safe;
+      sh.scale[i] = scale;
+      if (!ok) sh.bad = 1;
     }
     __syncthreads();
-    const bool window_ok = s_bad == 0;
-    const bool head = threadIdx.x < p1 - p0 && s_key[threadIdx.x + 1] != s_key[threadIdx.x];
+    const bool window_ok = sh.bad == 0;
+    const bool head = threadIdx.x < p1 - p0 && sh.key[threadIdx.x + 1] != sh.key[threadIdx.x];
     const uint64_t ballot = __ballot(head);
-    if (lane == 0) s_wave_heads[wave] = uint32_t(__popcll(ballot));
+    if (lane == 0) sh.wave_heads[wave] = uint32_t(__popcll(ballot));
     __syncthreads();
     uint32_t before = 0;
-    for (uint32_t w = 0; w < wave; ++w) before += s_wave_heads[w];
+    for (uint32_t w = 0; w < wave; ++w) before += sh.wave_heads[w];
     uint32_t nheads = 0;
-    for (uint32_t w = 0; w < kBlock / kWave; ++w) nheads += s_wave_heads[w];
-    if (head) s_heads[before + uint32_t(__popcll(ballot & ((1ull << lane) - 1)))] = threadIdx.x;
+    for (uint32_t w = 0; w < kBlock / kWave; ++w) nheads += sh.wave_heads[w];
+    if (head) sh.heads[before + uint32_t(__popcll(ballot & ((1ull << lane) - 1)))] = threadIdx.x;
     __syncthreads();
     // Groups take rows in order from a shared counter (claimed at the top of
     // a row, used at its end), so a group held up by a row with many
     // references does not hold up the rows behind it.
     for (uint32_t h = gid; h < nheads;) {
       uint32_t claim = 0;
-      if (lig == 0) claim = atomicAdd(&s_next, 1u);
-      const uint32_t sb = s_heads[h];
-      const uint32_t key = s_key[sb + 1];
+      if (lig == 0) claim = atomicAdd(&sh.next, 1u);
+      const uint32_t sb = sh.heads[h];
+      const uint32_t key = sh.key[sb + 1];
       // Hot rows (more than kLongRefs references) belong to HotSliceKernel.
-      if (sb + kLongRefs < staged && s_key[sb + kLongRefs + 1] == key) {
+      if (sb + kLongRefs < staged && sh.key[sb + kLongRefs + 1] == key) {
         h = uint32_t(__shfl(int(claim), 0, int(G)));
         continue;
       }
-      uint32_t se = h + 1 < nheads ? s_heads[h + 1] : p1 - p0;
-      while (se < staged && s_key[se + 1] == key) ++se;
+      uint32_t se = h + 1 < nheads ? sh.heads[h + 1] : p1 - p0;
+      while (se < staged && sh.key[se + 1] == key) ++se;
       const TableDesc& T = s_t[min(key >> a.row_bits, a.tables - 1)];
       const uint32_t dim = T.dim;
       const bool active = c < dim;
@@ -1192,8 +1194,8 @@ RowRunKernel(VecArgs a) {
 #pragma unroll
         for (uint32_t k = 0; k < kRefBatch; ++k) {
           const uint32_t j = min(j0 + k, se - 1);
-          s[k] = s_scale[j];
-          x[k] = Load4(s_src[j] + cl);
+          s[k] = sh.scale[j];
+          x[k] = Load4(sh.src[j] + cl);
         }
 #pragma unroll
         for (uint32_t k = 0; k < kRefBatch; ++k) {
@@ -1226,8 +1228,58 @@ RowRunKernel(VecArgs a) {
       h = uint32_t(__shfl(int(claim), 0, int(G)));
     }
   }
-  if (s_bad) st.err |= EPS_HIP_STATUS_BAD_INDEX;
-  FinishBlock(st, ctrl, a.bounds, write);
+}
+
+// Seven waves per SIMD (72 registers) where that needs no spill: more rows'
+// loads in flight per CU.
+template <uint32_t kLog2G>
+__global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(kLog2G == 2 || kLog2G == 6 ? 6 : 7)))
+RowRunKernel(VecArgs a) {
+  __shared__ TableDesc s_t[EPS_HIP_MAX_TABLES];
+  __shared__ const float* s_grad[EPS_HIP_MAX_FEATURES];
+  __shared__ RunShared sh;
+  __shared__ uint32_t s_mode;
+  __shared__ uint64_t s_rows[EPS_HIP_MAX_FEATURES];  // gradient rows per feature
+  bool write = false;
+  if (!VecPrologue(a, s_t, s_grad, &s_mode, write, s_rows)) return;
+  RowStats st;
+  if (threadIdx.x == 0) sh.bad = 0;
+  __syncthreads();
+  RowRuns<kLog2G>(a, sh, s_t, s_grad, s_rows, a.cls, blockIdx.x, gridDim.x, write, st);
+  if (sh.bad) st.err |= EPS_HIP_STATUS_BAD_INDEX;
+  FinishBlock(st, a.ctrl, a.bounds, write);
+}
+
+// Every vector class of a push in one launch: class c has the blocks
+// [class_block[c], class_block[c] + class_grid[c]) (starts and counts are
+// multiples of kXcds; absent classes have none), so the classes' rows run
+// side by side instead of one launch (and its tail) after another.
+__global__ void __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(6)))
+RowRunClassesKernel(VecArgs a) {
+  __shared__ TableDesc s_t[EPS_HIP_MAX_TABLES];
+  __shared__ const float* s_grad[EPS_HIP_MAX_FEATURES];
+  __shared__ RunShared sh;
+  __shared__ uint32_t s_mode;
+  __shared__ uint64_t s_rows[EPS_HIP_MAX_FEATURES];
+  bool write = false;
+  if (!VecPrologue(a, s_t, s_grad, &s_mode, write, s_rows)) return;
+  RowStats st;
+  if (threadIdx.x == 0) sh.bad = 0;
+  __syncthreads();
+  uint32_t cls = 0;
+#pragma unroll
+  for (uint32_t c = 1; c + 1 < kClasses; ++c)
+    if (a.class_grid[c] && blockIdx.x >= a.class_block[c]) cls = c;
+  const uint32_t block = blockIdx.x - a.class_block[cls], grid = a.class_grid[cls];
+  switch (cls) {
+    case 0: RowRuns<2>(a, sh, s_t, s_grad, s_rows, 0, block, grid, write, st); break;
+    case 1: RowRuns<3>(a, sh, s_t, s_grad, s_rows, 1, block, grid, write, st); break;
+    case 2: RowRuns<4>(a, sh, s_t, s_grad, s_rows, 2, block, grid, write, st); break;
+    case 3: RowRuns<5>(a, sh, s_t, s_grad, s_rows, 3, block, grid, write, st); break;
+    default: RowRuns<6>(a, sh, s_t, s_grad, s_rows, 4, block, grid, write, st); break;
+  }
+  if (sh.bad) st.err |= EPS_HIP_STATUS_BAD_INDEX;
+  FinishBlock(st, a.ctrl, a.bounds, write);
 }
 
 // ---------------------------------------------------------------------------
@@ -1377,10 +1429,10 @@ int ThreadOverlap(Overlap** out) {
 // (measured on MI355X: 65,536 pairs on one table, 167 -> 133 us a push; 4 x
 // 8.4 M references, 13.4 -> 11.6 ms; 26 tables of ~43,000 references with
 // 64-column units on 256 blocks, 245 -> 236 us a step).  Pushes with a table
-// of at least this many references take 16-column units on 512 blocks, so a
+// of at least this many references take 32-column units on 512 blocks, so a
 // very long row's chain data spreads over several CUs.
 constexpr uint64_t kOverlapTableRefs = 1ull << 16;
-constexpr uint32_t kNarrowSlice = 16, kWideSlice = 64;  // columns per hot-row unit
+constexpr uint32_t kNarrowSlice = 32, kWideSlice = 64;  // columns per hot-row unit
 
 std::atomic<uint32_t> g_spin_limit{1u << 22};
 uint32_t SpinLimit() { return g_spin_limit.load(std::memory_order_relaxed); }
@@ -1486,10 +1538,12 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
     for (uint32_t f = 0; f < feature_count; ++f) table_refs[features[f].table] += features[f].occurrences;
     const bool long_rows = *std::max_element(table_refs, table_refs + table_count) >= kOverlapTableRefs;
     // Slice width: pushes with very long hot rows (some table with 65,536 or
-    // more references) cut each row into 16-column units, so one row's chain
-    // data spreads over several CUs; otherwise 64-column units, whose fewer
-    // and fuller units a block's producers stage with less bookkeeping per
-    // column (26 tables of ~43,000 references: 47 -> 41 us a push).
+    // more references) cut each row into 32-column units, so one row's chain
+    // data spreads over several CUs (4 x 8.4 M references: 16-column units
+    // 13.8 ms a step, 32-column units, each a whole line per reference, 12.8);
+    // otherwise 64-column units, whose fewer and fuller units a block's
+    // producers stage with less bookkeeping per column (26 tables of ~43,000
+    // references: 47 -> 41 us a push).
     const uint32_t slice = long_rows ? kNarrowSlice : kWideSlice;
     // Units per hot row: the widest vector table's slices, rounded up to a
     // power of two (units past a row's dimension are skipped in the kernel).
@@ -1524,16 +1578,37 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
           role = kFollow;
         }
       }
+      // The row runs: one launch per present vector class, or one launch
+      // for all of them when there are several.
+      uint32_t present = 0;
+      uint64_t total_blocks = 0;
       for (uint32_t cls = 0; cls + 1 < kClasses; ++cls) {
+        va.class_block[cls] = uint32_t(total_blocks);
+        va.class_grid[cls] = 0;
         if (!plan.class_occurrences[cls]) continue;
-        va.cls = cls;
-        va.role = role;
-        role = kFollow;
         const uint64_t blocks = xcd_grid(std::min<uint64_t>(
             std::max<uint64_t>(1, (plan.class_occurrences[cls] + RunPositions(cls + 2) - 1) /
                                       RunPositions(cls + 2)),
             kVectorGrid));
-        EPS_HIP_TRY(LaunchVectorUpdate(cls, 0, unsigned(blocks), va, s));
+        va.class_grid[cls] = uint32_t(blocks);
+        total_blocks += blocks;
+        ++present;
+      }
+      va.class_block[kClasses - 1] = uint32_t(total_blocks);
+      va.class_grid[kClasses - 1] = 0;
+      if (present > 1) {
+        va.role = role;
+        role = kFollow;
+        hipLaunchKernelGGL(RowRunClassesKernel, dim3(unsigned(total_blocks)), dim3(kBlock), 0, s, va);
+        EPS_HIP_LAUNCHED("row update (all classes)");
+      } else {
+        for (uint32_t cls = 0; cls + 1 < kClasses; ++cls) {
+          if (!va.class_grid[cls]) continue;
+          va.cls = cls;
+          va.role = role;
+          role = kFollow;
+          EPS_HIP_TRY(LaunchVectorUpdate(cls, 0, va.class_grid[cls], va, s));
+        }
       }
     }
   }

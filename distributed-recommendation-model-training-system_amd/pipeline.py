@@ -3,16 +3,17 @@
 One step over a batch of features = the pooled pull of every feature on the
 main stream, then the push (gradient scan, fused aggregation + sparse Adam,
 checked apply) on the main stream.  The push's preparation (device dedup sort
-and hot-row lists) reads only the batch's ids, so it runs on a side stream
-ahead of the pull, rotating over the shard's W push workspaces (W >= 2):
+and hot-row lists) reads only the batch's ids, so it runs on a side stream,
+one batch ahead: step k issues batch k+1's preparation before its own pull
+and push, rotating over the shard's W push workspaces (W >= 3):
 
-  * batch k's preparation waits for the push of batch k-W, the last reader of
-    its workspace;
-  * batch k's push waits for its preparation.
+  * batch j's preparation waits for the push of batch j-W, the last reader of
+    its workspace (issued two or more steps earlier);
+  * batch k's push waits for its preparation (issued a step earlier).
 
-With W = 3 a preparation has two steps' time to finish before its push needs
-it, so a preparation slowed by the steps it overlaps does not hold the main
-stream up.
+Issued a step ahead, a preparation is on the side stream as soon as the one
+before it ends, so it has a whole step's time to finish before its push
+needs it, however late the host issues the step.
 
 Pushes are issued without reading their status (that would stall the
 pipeline): optimizer powers are advanced when a push is issued and every
@@ -28,6 +29,7 @@ import numpy as np
 from . import eps_hip as H
 
 WORKSPACES = 3  # push workspaces the timed pipeline rotates over
+AHEAD = 1       # batches prepared ahead of the batch being pushed
 
 
 class StepPipeline:
@@ -37,8 +39,8 @@ class StepPipeline:
         tensor per feature position.  `pull` False: the step is the push alone
         (duplicate-heavy gradient pairs).  `moves`: a TierMoves whose
         admissions run before the pull and whose write-backs run after the push."""
-        if len(shard.wss) < 2:
-            raise ValueError("the pipeline rotates over two or more push workspaces")
+        if len(shard.wss) < AHEAD + 2:
+            raise ValueError(f"the pipeline rotates over {AHEAD + 2} or more push workspaces")
         self.slots = len(shard.wss)
         self.torch, self.shard, self.batches, self.outputs = torch, shard, batches, outputs
         self.pull, self.moves = pull, moves
@@ -48,22 +50,37 @@ class StepPipeline:
         self.pushed = [torch.cuda.Event() for _ in range(self.slots)]
         for slot in range(self.slots):
             shard.clear_history(slot)
+        self.next_step = 0
+        self.next_prep = 0  # batches [0, next_prep) have their preparation issued
+
+    def _prepare(self, j, phases=None):
+        """Issues batch j's preparation on the side stream, in workspace j mod W."""
+        slot = j % self.slots
+        self.side.wait_event(self.pushed[slot])
+        if phases:
+            phases[5].record(self.side)
+        self.shard.prepare(self.batches[j % len(self.batches)], stream=self.side, slot=slot)
+        self.prepared[slot].record(self.side)
+        if phases:
+            phases[6].record(self.side)
 
     def step(self, k, fused=None, phases=None):
-        """Issues step k (batch k mod len(batches)).  `fused` = two timing
-        events around the fused update; `phases` = seven events for a
-        per-phase breakdown (see bench.py)."""
+        """Issues step k (batch k mod len(batches)); steps are issued in order
+        from 0.  `fused` = two timing events around the fused update;
+        `phases` = seven events for a per-phase breakdown (see bench.py; the
+        preparation timed is batch k+1's, the one this step issues)."""
+        if k != self.next_step:
+            raise ValueError(f"steps are issued in order: expected step {self.next_step}, got {k}")
+        self.next_step += 1
         feats = self.batches[k % len(self.batches)]
         slot = k % self.slots
-        stream, side, shard = self.stream, self.side, self.shard
-        side.wait_event(self.pushed[slot])
+        stream = self.stream
+        shard = self.shard
         if phases:
             phases[0].record(stream)
-            phases[5].record(side)
-        shard.prepare(feats, stream=side, slot=slot)
-        self.prepared[slot].record(side)
-        if phases:
-            phases[6].record(side)
+        while self.next_prep <= k + AHEAD:
+            self._prepare(self.next_prep, phases if self.next_prep == k + AHEAD else None)
+            self.next_prep += 1
         if self.moves:
             self.moves.admit(k)
         if self.pull:
