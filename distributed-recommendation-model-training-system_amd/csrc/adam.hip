@@ -1436,6 +1436,8 @@ constexpr uint32_t kNarrowSlice = 32, kWideSlice = 64;  // columns per hot-row u
 
 std::atomic<uint32_t> g_spin_limit{1u << 22};
 uint32_t SpinLimit() { return g_spin_limit.load(std::memory_order_relaxed); }
+// Whether this thread's pushes run the hot-row kernel on the side stream.
+thread_local bool t_hot_row_overlap = true;
 
 // Phases of a push (kPrimary: the fused update; kSecond: the checked apply)
 // and kOneStream: every kernel on the caller's stream, the hot-row kernel
@@ -1556,7 +1558,7 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
     uint64_t vector_occurrences = 0;
     for (uint32_t cls = 0; cls + 1 < kClasses; ++cls) vector_occurrences += plan.class_occurrences[cls];
     const uint64_t hot_units = (vector_occurrences / (kLongRefs + 1)) << va.slice_bits;
-    overlap = hot_units != 0 && !(phases & kOneStream);
+    overlap = hot_units != 0 && !(phases & kOneStream) && t_hot_row_overlap;
     if (phases & kPrimary) {
       // Grids are multiples of kXcds (the kernels split their work by XCD).
       auto xcd_grid = [](uint64_t b) { return (b + kXcds - 1) / kXcds * kXcds; };
@@ -1879,6 +1881,11 @@ uint32_t* eps_hip_status_word(void* workspace) {
 
 uint32_t* eps_hip_status_history_word(void* workspace) {
   return workspace ? &static_cast<Control*>(workspace)->history : nullptr;
+}
+
+int eps_hip_set_hot_row_overlap(int enabled) {
+  t_hot_row_overlap = enabled != 0;
+  return EPS_HIP_OK;
 }
 
 int eps_hip_debug_set_spin_limit(uint32_t polls) {

@@ -119,6 +119,7 @@ SYMBOLS = {
     "eps_hip_status_word": (C.c_void_p, [C.c_void_p]),
     "eps_hip_status_history_word": (C.c_void_p, [C.c_void_p]),
     "eps_hip_debug_set_spin_limit": (C.c_int, [C.c_uint32]),
+    "eps_hip_set_hot_row_overlap": (C.c_int, [C.c_int]),
     "eps_hip_read_status": (C.c_int, [C.c_void_p, C.c_void_p, C.c_void_p]),
     "eps_hip_fill_u32": (C.c_int, [C.c_void_p, C.c_uint32, C.c_uint64, C.c_void_p]),
 }
@@ -349,7 +350,7 @@ class DeviceShard:
         check(lib().eps_hip_prepare(self.tables, len(self.specs), arr, len(feats),
                                     _ptr(self.wss[slot]), self.ws_bytes, _stream(self.torch, stream)))
 
-    def push(self, feats, stream=None, advance=True, events=None, slot=0):
+    def push(self, feats, stream=None, advance=True, events=None, slot=0, hot_overlap=True):
         """Fused aggregation + Adam of a prepared push.  With `advance` the call
         waits for the push, and advances the optimizer powers of the pushed
         tables only if it applied (a rejected update leaves them unchanged, as
@@ -357,7 +358,8 @@ class DeviceShard:
         status.  Callers that overlap pushes pass advance=False (asynchronous),
         advance the powers themselves and check history() afterwards.
         `events` = (start, end) torch events recorded around the fused pass;
-        `slot` = the workspace the batch was prepared in."""
+        `slot` = the workspace the batch was prepared in; `hot_overlap` False
+        runs the hot-row kernel on `stream` (eps_hip_set_hot_row_overlap)."""
         arr = self._push_args(feats)
         self._opts_view["beta1_power"] = self.powers[:, 0]
         self._opts_view["beta2_power"] = self.powers[:, 1]
@@ -367,7 +369,13 @@ class DeviceShard:
         check(L.eps_hip_push_begin(*args))
         if events:
             events[0].record(stream)
-        check(L.eps_hip_push_apply(*args))
+        if not hot_overlap:
+            check(L.eps_hip_set_hot_row_overlap(0))
+        try:
+            check(L.eps_hip_push_apply(*args))
+        finally:
+            if not hot_overlap:
+                check(L.eps_hip_set_hot_row_overlap(1))
         if events:
             events[1].record(stream)
         check(L.eps_hip_push_end(*args))

@@ -24,6 +24,8 @@ Lookup followed by one Push per step (src/server/service.cpp:137-331).
 """
 from __future__ import annotations
 
+import os
+
 import numpy as np
 
 from . import eps_hip as H
@@ -52,6 +54,15 @@ class StepPipeline:
             shard.clear_history(slot)
         self.next_step = 0
         self.next_prep = 0  # batches [0, next_prep) have their preparation issued
+        # The pushes' hot-row kernel runs on the library's side stream only
+        # while every busy stream (this one, the preparation stream, that side
+        # stream and a tier-move pair's two) can have a hardware queue of its
+        # own: HIP maps streams onto GPU_MAX_HW_QUEUES queues round robin, and
+        # a hot-row kernel queued behind a host-link copy waits for it
+        # (ragged mixed-dim step with tier moves on 4 queues: side stream
+        # 0.47 ms, in-stream 0.44 ms).
+        queues = int(os.environ.get("GPU_MAX_HW_QUEUES", "4"))
+        self.hot_overlap = 3 + (2 if moves else 0) <= queues
 
     def _prepare(self, j, phases=None):
         """Issues batch j's preparation on the side stream, in workspace j mod W."""
@@ -91,7 +102,7 @@ class StepPipeline:
         if phases:
             phases[2].record(stream)
         shard.push(feats, stream=stream, slot=slot, advance=False,
-                   events=fused or (tuple(phases[3:5]) if phases else None))
+                   events=fused or (tuple(phases[3:5]) if phases else None), hot_overlap=self.hot_overlap)
         shard.advance_powers([f.table for f in feats])
         self.pushed[slot].record(stream)
         if self.moves:

@@ -324,6 +324,18 @@ int eps_hip_read_status(void* workspace, uint32_t* status, void* stream);
 /* Fills count u32 words with value (a kernel, safe under graph capture). */
 int eps_hip_fill_u32(uint32_t* target, uint32_t value, uint64_t count, void* stream);
 
+/* Where this thread's pushes run the hot-row kernel (rows with more than 128
+ * references).  Enabled (the default): beside the row kernels, on a side
+ * stream the library creates per thread and device, forked from and joined
+ * back into the push's stream.  Disabled: on the push's stream, before the
+ * row kernels (as eps_hip_push_static does).  No counterpart in the
+ * reference.  The side stream pays off when it has a hardware queue of its
+ * own: HIP maps a process's streams onto GPU_MAX_HW_QUEUES queues (4 by
+ * default) round robin, so a caller that keeps more streams busy than there
+ * are queues (e.g. a pipeline with cache-tier copy streams) should disable
+ * it.  Per calling thread; returns EPS_HIP_OK. */
+int eps_hip_set_hot_row_overlap(int enabled);
+
 /* Test hook: polls of an LDS hand-over wait of the hot-row kernel before it
  * gives up (default 4194304; process-wide).  0 makes every such wait give up
  * at once, so tests can drive the stall path from the host. */

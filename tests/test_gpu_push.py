@@ -87,8 +87,12 @@ def test_unique_and_reduce_match_oracle(torch_gpu, pkg, dims):
         assert_close(values[rows, : s.dim], vals, f"reduce table {t}", strict_ulp=0)
 
 
-@pytest.mark.parametrize("dims", [(64,), (4, 32, 192), (96, 6, 256, 300)])
-def test_push_steps_match_oracle(torch_gpu, pkg, dims):
+@pytest.mark.parametrize("dims,hot_overlap", [((64,), True), ((4, 32, 192), True), ((96, 6, 256, 300), True),
+                                               ((4, 32, 192), False)])
+def test_push_steps_match_oracle(torch_gpu, pkg, dims, hot_overlap):
+    """Zipf(1.15) keys over 4,000 rows: some rows have more than 128
+    references (the hot-row kernel), on its side stream or, with hot_overlap
+    False, on the push's stream."""
     torch, W, H = torch_gpu, pkg.workloads, pkg.eps_hip
     rng = np.random.default_rng(100 + sum(dims))
     specs = [W.TableSpec(i, d, 4000, seed=30 + i,
@@ -98,10 +102,10 @@ def test_push_steps_match_oracle(torch_gpu, pkg, dims):
     stores = [oracle_store(s) for s in specs]
     for step in range(4):
         feats = random_features(W, rng, specs, 6, holes=0.03, grad_scale=1e-1 if step % 2 else 1.0)
-        print(f"case: dims={dims} step={step}", flush=True)
+        print(f"case: dims={dims} hot_overlap={hot_overlap} step={step}", flush=True)
         dev = [H.DeviceFeature(torch, f) for f in feats]
         shard.prepare(dev)
-        shard.push(dev)
+        shard.push(dev, hot_overlap=hot_overlap)
         status = shard.status()
         assert status & H.STATUS_ERRORS == 0, f"status {status:#x}"
         cpu = [live(f) for f in feats]
