@@ -739,10 +739,14 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
   __syncthreads();
   // XCD x takes its hot-row lists: the hot rows of the x-th eighth of the
   // sorted positions, whose gradient rows the row runs of that XCD also read.
-  // Work units are (row, slice) in list order, longest rows first, dealt to
-  // the XCD's blocks in snake order (round r goes left to right when r is
-  // even, right to left when odd), so each block gets at most one of the
-  // longest units and the per-block totals stay close.
+  // Work units are (row, slice) in list order, longest rows first.  Units of
+  // the first list (rows of 65,536 or more references) each get a block of
+  // their own, when there are fewer of them than the XCD has blocks: one such
+  // unit can take longer than all the shorter units spread over the other
+  // blocks (4 x 8.4 M references: 15,200 chunks vs ~1,800 a block), so its
+  // block takes nothing else.  The other units are dealt to the remaining
+  // blocks in snake order (round r goes left to right when r is even, right
+  // to left when odd), so the per-block totals stay close.
   const uint32_t xcd = blockIdx.x % kXcds;
   const uint32_t xcd_blocks = gridDim.x / kXcds;
   const uint32_t me = blockIdx.x / kXcds;
@@ -755,8 +759,14 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
     units += min(count, a.hot_capacity) << a.slice_bits;
     bucket_end[b] = units;
   }
-  // The block's unit u of round r, and where its hot-row entry lies.
-  auto unit_of = [&](uint32_t r) { return r * xcd_blocks + ((r & 1) ? xcd_blocks - 1 - me : me); };
+  // The block's unit u of round r (units or more: none), and where its
+  // hot-row entry lies.
+  const uint32_t own = bucket_end[0] < xcd_blocks ? bucket_end[0] : 0u;  // blocks with a unit of their own
+  const uint32_t shared = xcd_blocks - own, mine = me - own;
+  auto unit_of = [&](uint32_t r) {
+    if (me < own) return r == 0 ? me : units;
+    return own + r * shared + ((r & 1) ? shared - 1 - mine : mine);
+  };
   // An entry's positions, kept inside the push's sorted positions (start < end
   // <= n), so a damaged list can neither read past them nor run unbounded.
   auto sane = [&](uint32_t& start, uint32_t& end) {

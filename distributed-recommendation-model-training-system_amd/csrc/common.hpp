@@ -33,7 +33,7 @@ constexpr uint32_t kLongRefs = 128;       // rows with more references take the 
 constexpr uint32_t kSrcSlots = 64;        // spread of the gradient/scale maximum atomics
 constexpr uint32_t kHistCopies = 16;      // spread of the keygen histogram atomics
 constexpr uint32_t kXcds = 8;             // XCDs of an MI355X
-constexpr uint32_t kHotBuckets = 4;       // hot-row lists per XCD, by length (longest first)
+constexpr uint32_t kHotBuckets = 8;       // hot-row lists per XCD, by length (longest first)
 constexpr uint32_t kHotChunk = 64;        // references per chunk of the hot-row kernel
 
 // Control block at offset 0 of a push or update workspace (1 KiB).  Values
@@ -57,7 +57,7 @@ struct Control {
   // of every update kernel decides the same, whatever the update's own
   // blocks have since raised the live domain to.
   uint32_t snap[4];
-  uint32_t pad[73];
+  uint32_t pad[41];
   // Error bits of every push or update run in this workspace, OR-ed in as they
   // are found; the per-call clears of the block skip this word (it starts at
   // zero with the workspace and only eps_hip_status_history_word's user

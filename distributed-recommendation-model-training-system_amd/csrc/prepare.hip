@@ -521,7 +521,7 @@ __device__ __forceinline__ uint32_t ClassOfKey(const HotArgs& a, uint32_t key) {
 //    positions and key) is appended, by the thread at its first position, to
 //    one of the lists of the XCD that owns that eighth of the positions (the
 //    update kernels split their work the same way); the row's length picks
-//    the list (>= 2048 references, 1024-2047, 512-1023, fewer), so the
+//    the list (eight ranges, from 65,536 or more references down), so the
 //    hot-row kernel can deal the longest rows out first.
 __global__ void __launch_bounds__(kBlock) HotListKernel(HotArgs a) {
   const uint32_t p = blockIdx.x * kBlock + threadIdx.x;
@@ -539,7 +539,9 @@ __global__ void __launch_bounds__(kBlock) HotListKernel(HotArgs a) {
   if (p >= a.n || cls + 1 >= kClasses || !first) return;
   if (p + kLongRefs >= a.n || a.keys[p + kLongRefs] != key) return;
   const uint32_t end = SegmentEndSearch(a.keys, p + kLongRefs, a.n, key), refs = end - p;
-  const uint32_t bucket = refs >= 2048 ? 0u : refs >= 1024 ? 1u : refs >= 512 ? 2u : 3u;
+  // Lists by length, longest first: >= 65536, 16384, 4096, 2048, 1024, 512, 256, fewer.
+  const uint32_t bucket = refs >= 65536 ? 0u : refs >= 16384 ? 1u : refs >= 4096 ? 2u : refs >= 2048 ? 3u :
+                          refs >= 1024 ? 4u : refs >= 512 ? 5u : refs >= 256 ? 6u : 7u;
   const uint32_t list = uint32_t(uint64_t(p) * kXcds / a.n) * kHotBuckets + bucket;
   // Sorted keys give each hot row one first position, so a list never holds
   // more than n / 129 entries; the bound keeps the write inside the list
