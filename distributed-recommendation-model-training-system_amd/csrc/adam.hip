@@ -1572,24 +1572,29 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
     if (phases & kPrimary) {
       // Grids are multiples of kXcds (the kernels split their work by XCD).
       auto xcd_grid = [](uint64_t b) { return (b + kXcds - 1) / kXcds * kXcds; };
-      // The hot-row kernel on the side stream, beside the row runs of each
-      // class on this one, joined before the checked apply.  Both sides make
-      // the guard decision themselves, from the same snapshot, so they decide
-      // the same.
-      if (hot_units) {
-        const uint64_t blocks = xcd_grid(std::min<uint64_t>(hot_units, long_rows ? kHotGrid : kWideHotGrid));
-        va.role = role;
-        if (overlap) {
-          EPS_HIP_TRY(ThreadOverlap(&ov));
-          EPS_HIP_TRY(Check(hipEventRecord(ov->fork, s), "hot-row fork"));
-          EPS_HIP_TRY(Check(hipStreamWaitEvent(ov->side, ov->fork, 0), "hot-row fork wait"));
-          EPS_HIP_TRY(LaunchVectorUpdate(0, slice, unsigned(blocks), va, ov->side));
-          EPS_HIP_TRY(Check(hipEventRecord(ov->join, ov->side), "hot-row join"));
-        } else {  // one stream: the hot rows first, deciding; the row kernels follow
-          EPS_HIP_TRY(LaunchVectorUpdate(0, slice, unsigned(blocks), va, s));
-          role = kFollow;
-        }
+      // The hot-row kernel and the row runs side by side on two streams,
+      // joined before the checked apply: the longer of the two stays on this
+      // stream and the other goes to the side stream, so this stream waits
+      // for no event while the longer part runs.  The hot rows are the longer
+      // part when some table takes 65,536 or more references (its hottest
+      // rows' chains outlast the row runs: 65,536 pairs on one table, hot rows
+      // 80 us against row runs 49 us); otherwise the row runs are.  Both
+      // sides make the guard decision themselves, from the same snapshot, so
+      // they decide the same.
+      const bool rows_beside = overlap && long_rows;
+      const uint64_t hot_blocks =
+          hot_units ? xcd_grid(std::min<uint64_t>(hot_units, long_rows ? kHotGrid : kWideHotGrid)) : 0;
+      if (overlap) {
+        EPS_HIP_TRY(ThreadOverlap(&ov));
+        EPS_HIP_TRY(Check(hipEventRecord(ov->fork, s), "update fork"));
+        EPS_HIP_TRY(Check(hipStreamWaitEvent(ov->side, ov->fork, 0), "update fork wait"));
       }
+      if (hot_units && !rows_beside) {
+        va.role = role;
+        EPS_HIP_TRY(LaunchVectorUpdate(0, slice, unsigned(hot_blocks), va, overlap ? ov->side : s));
+        if (!overlap) role = kFollow;  // one stream: the hot rows first, deciding; the row kernels follow
+      }
+      const hipStream_t rs = rows_beside ? ov->side : s;
       // The row runs: one launch per present vector class, or one launch
       // for all of them when there are several.
       uint32_t present = 0;
@@ -1608,10 +1613,11 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
       }
       va.class_block[kClasses - 1] = uint32_t(total_blocks);
       va.class_grid[kClasses - 1] = 0;
+      const uint32_t hot_role = role;  // the hot rows beside the row runs decide too
       if (present > 1) {
         va.role = role;
         role = kFollow;
-        hipLaunchKernelGGL(RowRunClassesKernel, dim3(unsigned(total_blocks)), dim3(kBlock), 0, s, va);
+        hipLaunchKernelGGL(RowRunClassesKernel, dim3(unsigned(total_blocks)), dim3(kBlock), 0, rs, va);
         EPS_HIP_LAUNCHED("row update (all classes)");
       } else {
         for (uint32_t cls = 0; cls + 1 < kClasses; ++cls) {
@@ -1619,8 +1625,13 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
           va.cls = cls;
           va.role = role;
           role = kFollow;
-          EPS_HIP_TRY(LaunchVectorUpdate(cls, 0, va.class_grid[cls], va, s));
+          EPS_HIP_TRY(LaunchVectorUpdate(cls, 0, va.class_grid[cls], va, rs));
         }
+      }
+      if (overlap) EPS_HIP_TRY(Check(hipEventRecord(ov->join, ov->side), "update join"));
+      if (hot_units && rows_beside) {
+        va.role = hot_role;
+        EPS_HIP_TRY(LaunchVectorUpdate(0, slice, unsigned(hot_blocks), va, s));
       }
     }
   }
