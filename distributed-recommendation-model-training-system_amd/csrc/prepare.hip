@@ -48,7 +48,17 @@ struct PrepArgs {
   uint32_t* hist;
   uint32_t* keys;
   uint32_t* vals;
-  uint64_t* refscale;
+  uint64_t* refscale;  // reference words with their scales (8 bytes), or
+  uint32_t* refs;      // without (4 bytes: no weighted-sum feature; the scale is derived)
+};
+
+// What the last pass needs to put each reference word's scale back (pushes
+// with no weighted-sum feature sort 4-byte words without it): the mean
+// features and their valid lengths.  The scale is then exactly what keygen
+// computes: 1.0f / (float)len for a mean bag of nonzero length, else 1.0f.
+struct ScaleArgs {
+  const uint64_t* lengths[EPS_HIP_MAX_FEATURES];
+  uint32_t mean_mask;  // bit f: feature f is mean-pooled
 };
 
 __global__ void __launch_bounds__(kBlock) KeygenKernel(PrepArgs args) {
@@ -164,8 +174,9 @@ __global__ void __launch_bounds__(kBlock) KeygenKernel(PrepArgs args) {
     if (s != kHole) scale_max = max(scale_max, AbsBits(scale[k]));
     args.keys[gi] = key;
     if (args.vals) args.vals[gi] = uint32_t(gi);
-    args.refscale[gi] = (uint64_t(__float_as_uint(scale[k])) << 32) |
-                        (uint64_t(f.feature) << kRefRowBits) | row;
+    const uint32_t ref = (f.feature << kRefRowBits) | uint32_t(row);
+    if (args.refs) args.refs[gi] = ref;
+    else args.refscale[gi] = (uint64_t(__float_as_uint(scale[k])) << 32) | ref;
     for (uint32_t p = 0; p < args.passes; ++p)
       atomicAdd(&s_hist[p][(key >> args.shift[p]) & ((1u << args.bits[p]) - 1)], 1u);
   }
@@ -207,14 +218,24 @@ __device__ __forceinline__ uint32_t BlockExclusiveScan(uint32_t x, uint32_t* s_w
 
 // kVals: the occurrence indices travel with the keys (for eps_hip_unique and
 // eps_hip_reduce, which map sorted positions back to occurrences); a push
-// needs only the keys and reference words.
-template <bool kVals>
+// needs only the keys and reference words.  kWords: the reference words are
+// 8 bytes with their scales (kWide), 4 bytes without (kNarrow), or 4 bytes
+// in and 8 bytes out (kWiden, the last pass of a sort of 4-byte words, which
+// puts each word's scale back from ScaleArgs).
+enum WordForm : int { kWide = 0, kNarrow = 1, kWiden = 2 };
+template <int kWords> struct WordTypes;
+template <> struct WordTypes<kWide> { typedef uint64_t In; typedef uint64_t Out; };
+template <> struct WordTypes<kNarrow> { typedef uint32_t In; typedef uint32_t Out; };
+template <> struct WordTypes<kWiden> { typedef uint32_t In; typedef uint64_t Out; };
+
+template <bool kVals, int kWords>
 __global__ void __launch_bounds__(kBlock) RadixPassKernel(
     const uint32_t* __restrict__ keys_in, const uint32_t* __restrict__ vals_in,
     uint32_t* __restrict__ keys_out, uint32_t* __restrict__ vals_out,
-    const uint64_t* __restrict__ rs_in, uint64_t* __restrict__ rs_out, uint32_t n,
-    uint32_t shift, uint32_t bits, const uint32_t* __restrict__ hist, uint32_t* look,
-    uint32_t* group_look, uint32_t tiles, uint32_t* tile_counter) {
+    const typename WordTypes<kWords>::In* __restrict__ rs_in, typename WordTypes<kWords>::Out* __restrict__ rs_out,
+    uint32_t n, uint32_t shift, uint32_t bits, const uint32_t* __restrict__ hist, uint32_t* look,
+    uint32_t* group_look, uint32_t tiles, uint32_t* tile_counter, ScaleArgs sc) {
+  typedef typename WordTypes<kWords>::In InWord;
   __shared__ uint32_t s_tile;
   __shared__ uint32_t s_wcount[4][kDigits];
   __shared__ uint32_t s_tile_start[kDigits];
@@ -222,7 +243,7 @@ __global__ void __launch_bounds__(kBlock) RadixPassKernel(
   __shared__ uint32_t s_scan[4];
   __shared__ uint32_t s_keys[kSortTile];
   __shared__ uint32_t s_vals[kVals ? kSortTile : 1];
-  __shared__ uint64_t s_rs[kSortTile];
+  __shared__ InWord s_rs[kSortTile];
 
   const uint32_t t = threadIdx.x, lane = t & (kWave - 1), wave = t / kWave;
   if (t == 0) s_tile = atomicAdd(tile_counter, 1u);
@@ -240,13 +261,13 @@ __global__ void __launch_bounds__(kBlock) RadixPassKernel(
   const uint32_t mask = (1u << bits) - 1;
   const uint32_t base = tile * kSortTile + wave * (kSortTile / 4);
   uint32_t key[kSortItems], val[kSortItems], rank[kSortItems];
-  uint64_t rs[kSortItems];
+  InWord rs[kSortItems];
 #pragma unroll
   for (uint32_t i = 0; i < kSortItems; ++i) {
     const uint32_t p = base + i * kWave + lane;
     key[i] = p < n ? keys_in[p] : 0u;
     val[i] = kVals && p < n ? vals_in[p] : 0u;
-    rs[i] = p < n ? rs_in[p] : 0ull;
+    rs[i] = p < n ? rs_in[p] : InWord(0);
   }
   const uint64_t lt_mask = (1ull << lane) - 1;
 #pragma unroll
@@ -412,12 +433,33 @@ __global__ void __launch_bounds__(kBlock) RadixPassKernel(
     const uint32_t digit = (key[i] >> shift) & mask;
     dest[i] = s_global[digit] + (q - s_tile_start[digit]);
   }
+  if (kWords == kWiden) {
+    // Each word's scale: the valid length of a mean feature's bag (all
+    // loaded before any is used), as keygen computed it.
+    uint64_t len[kSortItems];
+#pragma unroll
+    for (uint32_t i = 0; i < kSortItems; ++i) {
+      const uint32_t feature = uint32_t(rs[i]) >> kRefRowBits;
+      const bool mean = i * kBlock + t < tile_n && ((sc.mean_mask >> feature) & 1u);
+      len[i] = mean ? sc.lengths[feature][uint32_t(rs[i]) & ((1u << kRefRowBits) - 1u)] : 0ull;
+    }
+#pragma unroll
+    for (uint32_t i = 0; i < kSortItems; ++i) {
+      if (i * kBlock + t < tile_n) {
+        const float scale = len[i] ? 1.0f / (float)len[i] : 1.0f;  // batch_access.cpp:79-80
+        keys_out[dest[i]] = key[i];
+        if (kVals) vals_out[dest[i]] = val[i];
+        rs_out[dest[i]] = typename WordTypes<kWords>::Out((uint64_t(__float_as_uint(scale)) << 32) | uint32_t(rs[i]));
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (uint32_t i = 0; i < kSortItems; ++i) {
     if (i * kBlock + t < tile_n) {
       keys_out[dest[i]] = key[i];
       if (kVals) vals_out[dest[i]] = val[i];
-      rs_out[dest[i]] = rs[i];
+      rs_out[dest[i]] = typename WordTypes<kWords>::Out(rs[i]);
     }
   }
 }
@@ -703,10 +745,22 @@ int Prepare(const eps_hip_table* tables, uint32_t table_count, const eps_hip_pus
   args.vals = with_vals ? reinterpret_cast<uint32_t*>(ws + L.vals_a) : nullptr;
   // Reference words ping-pong between two buffers through the passes and
   // end in sorted_rs: keygen writes them where an even number of swaps
-  // before the end starts.
+  // before the end starts.  A push with no weighted-sum feature sorts them
+  // as 4-byte words without their scales (a third less sort traffic) and the
+  // last pass puts the scales back.
   uint64_t* rs[2] = {reinterpret_cast<uint64_t*>(ws + (plan.passes % 2 ? L.refscale : L.sorted_rs)),
                      reinterpret_cast<uint64_t*>(ws + (plan.passes % 2 ? L.sorted_rs : L.refscale))};
-  args.refscale = rs[0];
+  ScaleArgs sc{};
+  bool narrow = true;
+  for (uint32_t i = 0; i < feature_count; ++i) {
+    if (features[i].pooling == EPS_HIP_POOL_WEIGHTED_SUM) narrow = false;
+    if (features[i].pooling == EPS_HIP_POOL_MEAN) {
+      sc.mean_mask |= 1u << i;
+      sc.lengths[i] = features[i].valid_lengths;
+    }
+  }
+  args.refscale = narrow ? nullptr : rs[0];
+  args.refs = narrow ? reinterpret_cast<uint32_t*>(rs[0]) : nullptr;
   uint64_t occ = 0, blocks = 0;
   for (uint32_t i = 0; i < feature_count; ++i) {
     const auto& in = features[i];
@@ -728,13 +782,24 @@ int Prepare(const eps_hip_table* tables, uint32_t table_count, const eps_hip_pus
   auto* group_look = reinterpret_cast<uint32_t*>(ws + L.group_look);
   const uint32_t n = uint32_t(plan.occurrences);
   for (uint32_t p = 0; p < plan.passes; ++p) {
-    hipLaunchKernelGGL(with_vals ? RadixPassKernel<true> : RadixPassKernel<false>, dim3(unsigned(L.tiles)),
-                       dim3(kBlock), 0, s, keys[p % 2], vals[p % 2],
-                       keys[(p + 1) % 2], vals[(p + 1) % 2], rs[p % 2], rs[(p + 1) % 2], n,
-                       plan.shift[p], plan.bits[p],
-                       args.hist + p * kDigits, look + uint64_t(p) * L.tiles * kDigits,
-                       group_look + uint64_t(p) * L.groups * kDigits, uint32_t(L.tiles),
-                       &ctrl->tile_counter[p]);
+    const int form = !narrow ? kWide : (p + 1 < plan.passes ? kNarrow : kWiden);
+    auto launch = [&](auto kernel, const auto* in, auto* out) {
+      hipLaunchKernelGGL(kernel, dim3(unsigned(L.tiles)), dim3(kBlock), 0, s, keys[p % 2], vals[p % 2],
+                         keys[(p + 1) % 2], vals[(p + 1) % 2], in, out, n, plan.shift[p], plan.bits[p],
+                         args.hist + p * kDigits, look + uint64_t(p) * L.tiles * kDigits,
+                         group_look + uint64_t(p) * L.groups * kDigits, uint32_t(L.tiles), &ctrl->tile_counter[p],
+                         sc);
+    };
+    const uint64_t* in8 = rs[p % 2];
+    uint64_t* out8 = rs[(p + 1) % 2];
+    const uint32_t* in4 = reinterpret_cast<const uint32_t*>(rs[p % 2]);
+    uint32_t* out4 = reinterpret_cast<uint32_t*>(rs[(p + 1) % 2]);
+    if (form == kWide)
+      launch(with_vals ? RadixPassKernel<true, kWide> : RadixPassKernel<false, kWide>, in8, out8);
+    else if (form == kNarrow)
+      launch(with_vals ? RadixPassKernel<true, kNarrow> : RadixPassKernel<false, kNarrow>, in4, out4);
+    else
+      launch(with_vals ? RadixPassKernel<true, kWiden> : RadixPassKernel<false, kWiden>, in4, out8);
     EPS_HIP_LAUNCHED("radix pass");
   }
   // Hot rows of the sorted keys.
