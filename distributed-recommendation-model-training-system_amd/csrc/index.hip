@@ -12,6 +12,14 @@
 // from a mixed hash of the key; a probe ends at the first empty bucket.
 // Inserts and removals of one launch touch distinct keys (callers guarantee
 // it); launches are stream ordered, so lookups never meet a partial insert.
+// Nothing turns a kGone bucket back into kEmpty: under insert/remove churn
+// they replace the empty buckets until a miss walks the whole cluster.  An
+// owner that removes keys rebuilds the index (clear, then insert the live
+// keys) after removals to a quarter of the buckets, which keeps at least a
+// quarter of them empty at a load of at most one half.  HipCacheBackend does.
+// (A removal that empties its bucket when the next one is empty was tried:
+// under steady churn on a CPU model of this index it saved 5-10 % of a
+// miss's probes and still lost every empty bucket, so it was left out.)
 #include "common.hpp"
 
 namespace eps_hip {

@@ -38,6 +38,7 @@ struct HipMemoryStats {
   std::uint64_t staging_device_bytes;
   std::uint64_t outstanding_output_bytes;
   std::uint64_t output_allocations;
+  std::uint64_t index_rebuilds = 0;  // key-index rebuilds after eviction churn, all tables
   bool operator==(const HipMemoryStats&) const = default;
 };
 

@@ -257,6 +257,7 @@ struct SlotTable {
   eps_hip_table abi{};
   Memory state, index;
   std::uint64_t index_capacity = 0;
+  std::uint64_t removed_since_rebuild = 0;  // key removals since the index was last built
   std::vector<std::uint64_t> free_slots;
   std::unordered_map<Key, Resident> rows;
 
@@ -330,6 +331,49 @@ struct HipCacheBackend::Impl {
     Expect(current, "row is not resident at this generation on this HIP agent", Code::stale_generation);
     return it->second;
   }
+
+  // A removed key leaves a kGone bucket wherever later keys may sit past it;
+  // inserts reuse such buckets but nothing empties them, so under admission
+  // and eviction churn they would pile up and lengthen every probe that
+  // misses.  Once a table has seen removals to a quarter of its buckets, its
+  // index is built again from the resident map: cleared, then every resident
+  // key inserted with its slot.  Probe chains then stay bounded by the live
+  // load (at most half the buckets), at a cost of one insert per resident row
+  // per capacity/4 removals.  A rebuild that fails part-way leaves keys
+  // unfindable, so it stops the agent.
+  void RebuildIndexIfWorn(SlotTable& t) {
+    if (t.removed_since_rebuild <= t.index_capacity / 4) return;
+    try {
+      Await();  // the staging area may still feed earlier work
+      AbiOk(eps_hip_index_clear(t.index.Get(), t.index_capacity, stream));
+      ClearFlag();
+      const std::uint64_t piece = (transfer.capacity() - 2 * 256) / 16;
+      std::uint64_t left = t.rows.size();
+      auto it = t.rows.begin();
+      while (left) {
+        const std::uint64_t n = std::min(piece, left);
+        Await();  // the previous piece's upload has left the host staging
+        transfer.Reset();
+        auto keys = transfer.Take<std::uint64_t>(n);
+        auto slots = transfer.Take<std::uint64_t>(n);
+        for (std::uint64_t j = 0; j < n; ++j, ++it) {
+          keys.host[j] = it->first;
+          slots.host[j] = it->second.where.slot;
+        }
+        transfer.Upload(stream);
+        AbiOk(eps_hip_index_insert(t.index.Get(), t.index_capacity, keys.device, slots.device, n, Flag(), stream));
+        left -= n;
+      }
+      Expect(!(ReadFlag(Flag()) & EPS_HIP_STATUS_BAD_INDEX), "HIP key index rebuild overflowed", Code::run_failed);
+      transfer.Reset();
+      t.removed_since_rebuild = 0;
+      ++index_rebuilds;
+    } catch (...) {
+      stopped = true;
+      throw;
+    }
+  }
+  std::uint64_t index_rebuilds = 0;
 
   // Status flags of one request: word 0 collects the resolution and index
   // results; the push and update workspaces hold their own.
@@ -525,6 +569,7 @@ struct HipCacheBackend::Impl {
   std::vector<LocatedRow> Admit(const MigrationPlan& plan, const std::vector<std::uint64_t>& updates, Pack pack) {
     std::map<TableId, std::vector<std::size_t>> by_table;
     for (std::size_t i = 0; i < plan.rows.size(); ++i) by_table[plan.rows[i].row.table].push_back(i);
+    for (const auto& [id, members] : by_table) RebuildIndexIfWorn(Table(id));
     for (const auto& [id, members] : by_table) {
       const SlotTable& t = Table(id);
       Expect(plan.reserve_slots <= t.free_slots.size() && members.size() <= t.free_slots.size() - plan.reserve_slots,
@@ -590,6 +635,7 @@ struct HipCacheBackend::Impl {
           transfer.Upload(stream);
           (void)eps_hip_index_remove(t->index.Get(), t->index_capacity, piece.device, n, nullptr, stream);
           (void)hipStreamSynchronize(stream);
+          t->removed_since_rebuild += n;
         }
       }
       for (auto it = taken.rbegin(); it != taken.rend(); ++it) it->first->free_slots.push_back(it->second);
@@ -870,6 +916,10 @@ std::future<Result<Ack>> HipCacheBackend::CommitEviction(MigrationPlan plan) {
       SlotTable& t = I.Table(loc.row.table);
       t.free_slots.push_back(loc.slot);
       t.rows.erase(loc.row.key);
+    }
+    for (auto& [t, keys] : removals) {
+      t->removed_since_rebuild += keys.count;
+      I.RebuildIndexIfWorn(*t);
     }
     return Ack{};
   });
@@ -1290,7 +1340,7 @@ std::future<Result<HipMemoryStats>> HipCacheBackend::MemoryStats() {
     }
     const std::uint64_t staging = I.transfer.device_bytes() + I.update_ws.bytes() + I.push_ws.bytes() +
                                   I.bounds.bytes() + I.flags.bytes() + indexes;
-    return HipMemoryStats{state, staging, I.ledger->used.load(), I.ledger->blocks.load()};
+    return HipMemoryStats{state, staging, I.ledger->used.load(), I.ledger->blocks.load(), I.index_rebuilds};
   });
 }
 

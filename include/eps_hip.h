@@ -171,7 +171,10 @@ int eps_hip_move_rows(const eps_hip_row_batch* batches, uint32_t count, int32_t 
  * admissions insert into and evictions remove from, so occurrences resolve on
  * the device.  Keys of one insert or remove call must be distinct; a key must
  * not be inserted twice.  Failures (a full index, removing a key that is not
- * there) set EPS_HIP_STATUS_BAD_INDEX in `status` (device u32, may be NULL). */
+ * there) set EPS_HIP_STATUS_BAD_INDEX in `status` (device u32, may be NULL).
+ * A removed key leaves a marker bucket that inserts reuse but nothing empties,
+ * so an owner that removes keys rebuilds the index (clear, then insert the
+ * live keys) after removals to a quarter of `capacity`; HipCacheBackend does. */
 uint64_t eps_hip_index_bytes(uint64_t capacity);
 int eps_hip_index_clear(void* index, uint64_t capacity, void* stream);
 int eps_hip_index_insert(void* index, uint64_t capacity, const uint64_t* keys, const uint64_t* slots,

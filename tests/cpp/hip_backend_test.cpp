@@ -1143,7 +1143,54 @@ void StalledPushStops() {
         "a stopped agent serves no gathers");
 }
 
+// Admission and eviction churn on a 256-row table (a 512-bucket key index):
+// 40 rounds each admit 150 fresh keys beside 50 that stay, gather a sum over
+// all of them and evict the 150 again, 6,000 removals in all.  Every gather
+// resolves each occurrence through the index (a key it lost fails the
+// gather) and must match the oracle bit for bit; the index must have been
+// rebuilt along the way, and the rows that stay must still read back whole.
+void EvictionChurn() {
+  HipCacheBackend gpu(SmallOptions(256));
+  Take(gpu.Define(Table(2, 64)));
+  auto state = [](Key key) {
+    RowState r{{2, key}, std::vector<float>(64), std::vector<float>(64, 0.f), std::vector<float>(64, 0.f), 0};
+    for (std::uint32_t d = 0; d < 64; ++d) r.weights[d] = 0.001f * float((key * 7 + d) % 97);
+    return r;
+  };
+  Model model;
+  std::vector<RowState> stay;
+  for (Key k = 1; k <= 50; ++k) stay.push_back(state(k * 7919));
+  const auto stay_at = Take(gpu.Load(Plan(stay), stay));
+  for (const auto& r : stay) model.rows[{2, r.row.key}] = r;
+  for (int round = 0; round < 40; ++round) {
+    std::vector<RowState> churn;
+    for (Key j = 0; j < 150; ++j) churn.push_back(state(1000003ull * Key(round + 1) + j * 131));
+    const auto churn_at = Take(gpu.Load(Plan(churn), churn));
+    for (const auto& r : churn) model.rows[{2, r.row.key}] = r;
+    // Bag b sums churned row b and staying row b % 50.
+    AgentWork w{0, AccessRoute::resident_gpu, 0, stay_at, {}, {}};
+    w.rows.insert(w.rows.end(), churn_at.begin(), churn_at.end());
+    FeatureInput f{2, 0, Pooling::sum, {}, {0}, {}};
+    for (std::uint64_t b = 0; b < 150; ++b) {
+      f.keys.push_back(churn[b].row.key);
+      w.occurrence_to_unique.push_back(50 + b);
+      f.keys.push_back(stay[b % 50].row.key);
+      w.occurrence_to_unique.push_back(b % 50);
+      f.offsets.push_back(2 * (b + 1));
+      f.valid_lengths.push_back(2);
+    }
+    CompareGather(Take(gpu.GatherHost({w}, {f})), model, {w}, {f}, "gather under eviction churn");
+    Take(gpu.CommitEviction(MigrationPlan{"evict", 0, churn_at, Placement::cpu, 0}));
+    for (const auto& r : churn) model.rows.erase({2, r.row.key});
+  }
+  Check(Take(gpu.MemoryStats()).index_rebuilds >= 30, "key index not rebuilt under eviction churn");
+  Check(Take(gpu.FreeSlots(2)) == 206, "slots after eviction churn");
+  CompareStates(Take(gpu.ReadBack(MigrationPlan{"read", 0, stay_at, Placement::cpu, 0})), model,
+                "staying rows after eviction churn");
+}
+
 void Main() {
+  EvictionChurn();
   AtomicReserve();
   SnapshotWriteback();
   DevicePushAtScale();
@@ -1290,7 +1337,7 @@ int main() {
     Main();
     std::cout << "PASS HIP backend: " << g_checks
               << " checks (gathers, optimizer states, device push, snapshot writeback, atomic "
-                 "rejection, slot reuse, assembly, device-result lifetime)\n";
+                 "rejection, slot reuse, eviction churn, assembly, device-result lifetime)\n";
     return 0;
   } catch (const std::exception& e) {
     std::cerr << "FAIL HIP backend: " << e.what() << '\n';
