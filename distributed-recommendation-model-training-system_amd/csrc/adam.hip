@@ -570,7 +570,8 @@ __global__ void __launch_bounds__(kBlock) SortedUpdateKernel(FusedArgs a) {
 //    move half of a 64-column chunk's bytes through their CU per chunk, and
 //    the adding wave's serial chain, not the CU's memory pipeline, sets the
 //    rate; a 32-column slice of a reference is one whole 128-byte line, so
-//    no line is fetched for part of its bytes.
+//    no line is fetched for part of its bytes.  Small pushes with very long
+//    rows (their gradient rows stay in the caches) take 16-column slices.
 //  * RowRunKernel: every other row.  A block owns a window of sorted
 //    positions (RunPositions: 256, or 128 / 64 for 32- / 64-lane groups, so
 //    every group has a few rows per window whatever the width); it stages
@@ -1439,10 +1440,13 @@ int ThreadOverlap(Overlap** out) {
 // (measured on MI355X: 65,536 pairs on one table, 167 -> 133 us a push; 4 x
 // 8.4 M references, 13.4 -> 11.6 ms; 26 tables of ~43,000 references with
 // 64-column units on 256 blocks, 245 -> 236 us a step).  Pushes with a table
-// of at least this many references take 32-column units on 512 blocks, so a
-// very long row's chain data spreads over several CUs.
+// of at least this many references take 32- or 16-column units on 512 blocks,
+// so a very long row's chain data spreads over several CUs.
 constexpr uint64_t kOverlapTableRefs = 1ull << 16;
-constexpr uint32_t kNarrowSlice = 32, kWideSlice = 64;  // columns per hot-row unit
+constexpr uint32_t kFineSlice = 16, kNarrowSlice = 32, kWideSlice = 64;  // columns per hot-row unit
+// Pushes with very long rows but fewer vector references than this take
+// 16-column units (below).
+constexpr uint64_t kFinePushRefs = 1ull << 18;
 
 std::atomic<uint32_t> g_spin_limit{1u << 22};
 uint32_t SpinLimit() { return g_spin_limit.load(std::memory_order_relaxed); }
@@ -1476,6 +1480,8 @@ int LaunchVectorUpdate(uint32_t cls, uint32_t hot_slice, unsigned grid, const Ve
   if (hot_slice) {
     if (hot_slice == kWideSlice)
       hipLaunchKernelGGL(HotSliceKernel<kWideSlice>, dim3(grid), dim3(kHotBlock), 0, s, a);
+    else if (hot_slice == kFineSlice)
+      hipLaunchKernelGGL(HotSliceKernel<kFineSlice>, dim3(grid), dim3(kHotBlock), 0, s, a);
     else
       hipLaunchKernelGGL(HotSliceKernel<kNarrowSlice>, dim3(grid), dim3(kHotBlock), 0, s, a);
     EPS_HIP_LAUNCHED("hot row update");
@@ -1549,14 +1555,22 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
     uint64_t table_refs[EPS_HIP_MAX_TABLES] = {};
     for (uint32_t f = 0; f < feature_count; ++f) table_refs[features[f].table] += features[f].occurrences;
     const bool long_rows = *std::max_element(table_refs, table_refs + table_count) >= kOverlapTableRefs;
+    uint64_t vector_occurrences = 0;
+    for (uint32_t cls = 0; cls + 1 < kClasses; ++cls) vector_occurrences += plan.class_occurrences[cls];
     // Slice width: pushes with very long hot rows (some table with 65,536 or
     // more references) cut each row into 32-column units, so one row's chain
     // data spreads over several CUs (4 x 8.4 M references: 16-column units
     // 13.8 ms a step, 32-column units, each a whole line per reference, 12.8);
-    // otherwise 64-column units, whose fewer and fuller units a block's
-    // producers stage with less bookkeeping per column (26 tables of ~43,000
-    // references: 47 -> 41 us a push).
-    const uint32_t slice = long_rows ? kNarrowSlice : kWideSlice;
+    // small pushes of that kind, whose time is their hottest row's chain and
+    // whose gradient rows stay in the caches, take 16-column units, so each
+    // chunk moves half the bytes through its producers (65,536 pairs on one
+    // table: 100.6 -> 97.0 us an update; a ragged 8-table push of 525,000
+    // references lost with them, 270 -> 295 us); otherwise 64-column units,
+    // whose fewer and fuller units a block's producers stage with less
+    // bookkeeping per column (26 tables of ~43,000 references: 47 -> 41 us a
+    // push).
+    const uint32_t slice =
+        !long_rows ? kWideSlice : (vector_occurrences < kFinePushRefs ? kFineSlice : kNarrowSlice);
     // Units per hot row: the widest vector table's slices, rounded up to a
     // power of two (units past a row's dimension are skipped in the kernel).
     uint32_t slices = 1;
@@ -1565,8 +1579,6 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
         slices = std::max(slices, (tables[t].dim + slice - 1) / slice);
     va.slice_bits = 0;
     while ((1u << va.slice_bits) < slices) ++va.slice_bits;
-    uint64_t vector_occurrences = 0;
-    for (uint32_t cls = 0; cls + 1 < kClasses; ++cls) vector_occurrences += plan.class_occurrences[cls];
     const uint64_t hot_units = (vector_occurrences / (kLongRefs + 1)) << va.slice_bits;
     overlap = hot_units != 0 && !(phases & kOneStream) && t_hot_row_overlap;
     if (phases & kPrimary) {
