@@ -120,6 +120,57 @@ def test_push_steps_match_oracle(torch_gpu, pkg, dims, hot_overlap):
             assert tuple(shard.powers[t]) == stores[t].powers()[:2] or not any(f.table == t for f in feats)
 
 
+def long_row_features(W, rng, specs, long_table, long_refs, other_refs):
+    """One feature per table, Zipf(1.2) keys (hot rows everywhere); table
+    `long_table` takes `long_refs` references, the others `other_refs` each."""
+    feats = []
+    for t, spec in enumerate(specs):
+        refs = long_refs if t == long_table else other_refs
+        pooling = [W.SUM, W.MEAN, W.WEIGHTED_SUM, W.SEQUENCE][t % 4]
+        lengths = rng.integers(1, 9, int(refs / 4.5) + 1)
+        lengths = lengths[: np.searchsorted(np.cumsum(lengths), refs) + 1]
+        offsets = np.concatenate([[0], np.cumsum(lengths)]).astype(np.uint64)
+        n = int(offsets[-1])
+        keys = (rng.zipf(1.2, n) % spec.rows).astype(np.uint64)
+        weights = rng.random(n).astype(F32) if pooling == W.WEIGHTED_SUM else None
+        rows = n if pooling == W.SEQUENCE else len(lengths)
+        grad = rng.normal(0, 1e-2, (rows, spec.dim)).astype(F32)
+        feats.append(W.Feature(t, t, pooling, keys, offsets, lengths.astype(np.uint64), weights, grad))
+    return feats
+
+
+@pytest.mark.parametrize("other_refs", [10_000, 80_000])
+def test_push_long_rows_mixed_dims(torch_gpu, pkg, other_refs):
+    """A table of 70,000 references makes the hot rows narrow units: 16-column
+    units while the push has fewer than 262,144 vector references (90,000),
+    32-column units above (310,000).  Tables of dimensions 4, 32, 192 and 256,
+    so rows have 1 to 16 units and the units past a row's dimension are
+    skipped.  Two steps, every touched row bit-exact against the oracle."""
+    torch, W, H = torch_gpu, pkg.workloads, pkg.eps_hip
+    rng = np.random.default_rng(other_refs)
+    specs = [W.TableSpec(i, d, 5000, seed=60 + i) for i, d in enumerate((4, 32, 192, 256))]
+    shard = H.DeviceShard(torch, specs)
+    shard.init_rows()
+    stores = [oracle_store(s) for s in specs]
+    for step in range(2):
+        feats = long_row_features(W, rng, specs, 2, 70_000, other_refs)
+        total = sum(len(f.keys) for f in feats)
+        assert (total < 262_144) == (other_refs == 10_000), total  # 16- or 32-column units
+        print(f"case: other_refs={other_refs} step={step} refs={[len(f.keys) for f in feats]}", flush=True)
+        dev = [H.DeviceFeature(torch, f) for f in feats]
+        shard.prepare(dev)
+        status = shard.push(dev)
+        assert status & H.STATUS_ERRORS == 0, f"status {status:#x}"
+        for f in feats:
+            stores[f.table].prepare(f)
+        assert oracle.push(stores, feats, [f.table for f in feats], [f.gradient for f in feats]) == 0
+        for t, s in enumerate(specs):
+            keys = stores[t].keys()
+            want, _ = stores[t].read_many(keys)
+            got = shard.read_rows(t, torch.from_numpy(keys.view(np.int64)).cuda()).cpu().numpy()
+            assert_close(got.reshape(want.shape), want, f"state table {t} step {step}", strict_ulp=0)
+
+
 @pytest.mark.parametrize("pooling", [0, 1, 3])
 def test_push_with_long_runs_of_empty_bags(torch_gpu, pkg, pooling):
     """Thousands of bags and a run of 3000 empty ones: several preparation
