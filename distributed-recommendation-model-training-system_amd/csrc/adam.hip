@@ -1579,7 +1579,13 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
         slices = std::max(slices, (tables[t].dim + slice - 1) / slice);
     va.slice_bits = 0;
     while ((1u << va.slice_bits) < slices) ++va.slice_bits;
-    const uint64_t hot_units = (vector_occurrences / (kLongRefs + 1)) << va.slice_bits;
+    // A hot row takes more than kLongRefs references of its own table, so no
+    // table adds more hot rows than its references allow; a push with no such
+    // table (a few hundred pairs) launches no hot-row kernel and no events.
+    uint64_t hot_rows = 0;
+    for (uint32_t t = 0; t < table_count; ++t)
+      if (DimClass(tables[t].dim) < kClasses - 1) hot_rows += table_refs[t] / (kLongRefs + 1);
+    const uint64_t hot_units = hot_rows << va.slice_bits;
     overlap = hot_units != 0 && !(phases & kOneStream) && t_hot_row_overlap;
     if (phases & kPrimary) {
       // Grids are multiples of kXcds (the kernels split their work by XCD).
