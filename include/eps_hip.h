@@ -328,10 +328,14 @@ int eps_hip_read_status(void* workspace, uint32_t* status, void* stream);
 int eps_hip_fill_u32(uint32_t* target, uint32_t value, uint64_t count, void* stream);
 
 /* Where this thread's pushes run the hot-row kernel (rows with more than 128
- * references).  Enabled (the default): beside the row kernels, on a side
- * stream the library creates per thread and device, forked from and joined
- * back into the push's stream.  Disabled: on the push's stream, before the
- * row kernels (as eps_hip_push_static does).  No counterpart in the
+ * references).  Enabled (the default): beside the row kernels on two streams,
+ * the push's stream and a side stream the library creates per thread and
+ * device, forked after the gradient scan and joined before the checked apply;
+ * the side stream takes the row kernels when some table of the push has
+ * 65,536 or more references (its hot rows outlast them), else the hot-row
+ * kernel.  Disabled: both on the push's stream, hot rows first (as
+ * eps_hip_push_static does).  A push whose tables each take 128 or fewer
+ * references has no hot rows and uses no side stream.  No counterpart in the
  * reference.  The side stream pays off when it has a hardware queue of its
  * own: HIP maps a process's streams onto GPU_MAX_HW_QUEUES queues (4 by
  * default) round robin, so a caller that keeps more streams busy than there
