@@ -120,6 +120,45 @@ def test_push_steps_match_oracle(torch_gpu, pkg, dims, hot_overlap):
             assert tuple(shard.powers[t]) == stores[t].powers()[:2] or not any(f.table == t for f in feats)
 
 
+@pytest.mark.parametrize("refs", [128, 129])
+def test_push_hot_row_boundary(torch_gpu, pkg, refs):
+    """A row referenced `refs` times makes up all of its table's references:
+    128 is still a row-kernel row (and no table can then hold a hot row, so no
+    hot-row kernel or side stream is used), 129 is a hot row.  Other tables
+    take 100 references each.  Three steps, bit-exact against the oracle."""
+    torch, W, H = torch_gpu, pkg.workloads, pkg.eps_hip
+    rng = np.random.default_rng(refs)
+    specs = [W.TableSpec(i, d, 500, seed=80 + i) for i, d in enumerate((64, 32, 128))]
+    shard = H.DeviceShard(torch, specs)
+    shard.init_rows()
+    stores = [oracle_store(s) for s in specs]
+    for step in range(3):
+        feats = []
+        for t, spec in enumerate(specs):
+            n = refs if t == 0 else 100
+            lengths = np.full(n // 4, 4, np.int64)
+            lengths[-1] += n - int(lengths.sum())
+            offsets = np.concatenate([[0], np.cumsum(lengths)]).astype(np.uint64)
+            keys = np.full(n, 7, np.uint64) if t == 0 else (rng.zipf(1.2, n) % spec.rows).astype(np.uint64)
+            pooling = [W.MEAN, W.SUM, W.WEIGHTED_SUM][t]
+            weights = rng.random(n).astype(F32) if pooling == W.WEIGHTED_SUM else None
+            grad = rng.normal(0, 1e-2, (len(lengths), spec.dim)).astype(F32)
+            feats.append(W.Feature(t, t, pooling, keys, offsets, lengths.astype(np.uint64), weights, grad))
+        print(f"case: refs={refs} step={step}", flush=True)
+        dev = [H.DeviceFeature(torch, f) for f in feats]
+        shard.prepare(dev)
+        status = shard.push(dev)
+        assert status & H.STATUS_ERRORS == 0, f"status {status:#x}"
+        for f in feats:
+            stores[f.table].prepare(f)
+        assert oracle.push(stores, feats, [f.table for f in feats], [f.gradient for f in feats]) == 0
+        for t, s in enumerate(specs):
+            keys = stores[t].keys()
+            want, _ = stores[t].read_many(keys)
+            got = shard.read_rows(t, torch.from_numpy(keys.view(np.int64)).cuda()).cpu().numpy()
+            assert_close(got.reshape(want.shape), want, f"state table {t} step {step}", strict_ulp=0)
+
+
 def long_row_features(W, rng, specs, long_table, long_refs, other_refs):
     """One feature per table, Zipf(1.2) keys (hot rows everywhere); table
     `long_table` takes `long_refs` references, the others `other_refs` each."""
