@@ -120,6 +120,78 @@ def test_push_steps_match_oracle(torch_gpu, pkg, dims, hot_overlap):
             assert tuple(shard.powers[t]) == stores[t].powers()[:2] or not any(f.table == t for f in feats)
 
 
+SWEEP_DIMS = (4, 8, 12, 16, 32, 48, 64, 96, 128, 192, 256, 6, 300)
+
+
+def sweep_case(W, seed):
+    """A seeded random push layout: 1-6 tables of mixed dimensions (vector and
+    generic), 1-8 features in every pooling, Zipf skews from 1.05 to 1.5, and
+    sizes from a few thousand references up to past the 65,536-reference and
+    262,144-reference thresholds of the hot-row units."""
+    rng = np.random.default_rng(1000 + seed)
+    n_tables = int(rng.integers(1, 7))
+    specs = [W.TableSpec(i, int(rng.choice(SWEEP_DIMS)), int(rng.integers(200, 6000)), seed=200 + seed * 10 + i)
+             for i in range(n_tables)]
+    n_features = int(rng.integers(1, 9))
+    total = int(rng.choice([4_000, 30_000, 90_000, 300_000]))
+    skew = float(rng.choice([1.05, 1.2, 1.5]))
+    shares = rng.dirichlet(np.ones(n_features))
+    layout = []
+    for f in range(n_features):
+        refs = max(1, int(total * shares[f]))
+        layout.append((int(rng.integers(0, n_tables)), [W.SUM, W.MEAN, W.SEQUENCE, W.WEIGHTED_SUM][int(rng.integers(0, 4))],
+                       refs, int(rng.integers(1, 25))))
+    return rng, specs, skew, layout
+
+
+def sweep_features(W, rng, specs, skew, layout):
+    feats = []
+    for i, (t, pooling, refs, max_len) in enumerate(layout):
+        lengths = rng.integers(0, max_len + 1, int(refs / max(1, max_len / 2)) + 1)
+        offsets = np.concatenate([[0], np.cumsum(lengths)]).astype(np.uint64)
+        n = int(offsets[-1])
+        keys = (rng.zipf(skew, n) % specs[t].rows).astype(np.uint64)
+        weights = rng.random(n).astype(F32) if pooling == W.WEIGHTED_SUM else None
+        rows = n if pooling == W.SEQUENCE else len(lengths)
+        valid = (lengths + (rng.random(len(lengths)) < 0.1)).astype(np.uint64)
+        grad = rng.normal(0, 1e-2, (rows, specs[t].dim)).astype(F32)
+        feats.append(W.Feature(t, i, pooling, keys, offsets, valid, weights, grad))
+    return feats
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_push_random_sweep(torch_gpu, pkg, seed):
+    """Seeded random pushes (sweep_case) over two steps, every touched row
+    bit-exact against the oracle: table counts, dimensions, poolings, skews and
+    sizes together, so the hot-row unit widths, both stream placements and the
+    dimension classes meet in combinations no single-purpose test builds.
+    Every third case runs the hot-row kernel on the push's stream."""
+    torch, W, H = torch_gpu, pkg.workloads, pkg.eps_hip
+    rng, specs, skew, layout = sweep_case(W, seed)
+    hot_overlap = seed % 3 != 2
+    shard = H.DeviceShard(torch, specs)
+    shard.init_rows()
+    stores = [oracle_store(s) for s in specs]
+    for step in range(2):
+        feats = sweep_features(W, rng, specs, skew, layout)
+        print(f"case: seed={seed} step={step} dims={[s.dim for s in specs]} skew={skew} "
+              f"refs={[len(f.keys) for f in feats]} hot_overlap={hot_overlap}", flush=True)
+        dev = [H.DeviceFeature(torch, f) for f in feats]
+        shard.prepare(dev)
+        status = shard.push(dev, hot_overlap=hot_overlap)
+        assert status & H.STATUS_ERRORS == 0, f"status {status:#x}"
+        for f in feats:
+            stores[f.table].prepare(f)
+        assert oracle.push(stores, feats, [f.table for f in feats], [f.gradient for f in feats]) == 0
+        for t, s in enumerate(specs):
+            keys = stores[t].keys()
+            if len(keys) == 0:
+                continue
+            want, _ = stores[t].read_many(keys)
+            got = shard.read_rows(t, torch.from_numpy(keys.view(np.int64)).cuda()).cpu().numpy()
+            assert_close(got.reshape(want.shape), want, f"state table {t} step {step}", strict_ulp=0)
+
+
 @pytest.mark.parametrize("refs", [128, 129])
 def test_push_hot_row_boundary(torch_gpu, pkg, refs):
     """A row referenced `refs` times makes up all of its table's references:
