@@ -56,6 +56,32 @@ def test_gather_matches_oracle(torch_gpu, pkg, dim, pooling):
     assert_close(out.cpu().numpy(), want, f"gather dim={dim} pooling={pooling}", strict_ulp=0)
 
 
+@pytest.mark.parametrize("dim", [4, 64, 256, 300])
+@pytest.mark.parametrize("pooling", [0, 1, 3])
+def test_gather_long_bags(torch_gpu, pkg, dim, pooling):
+    """Bags of up to 400 occurrences (sum, mean, weighted sum: the pooled
+    modes, whose blocks own bags): a block's bags then hold more than the
+    1,024 occurrences it stages in LDS, so their slots are resolved per
+    occurrence in the summing loop (the gather's unstaged path)."""
+    torch, W, H = torch_gpu, pkg.workloads, pkg.eps_hip
+    rng = np.random.default_rng(500 + dim * 10 + pooling)
+    spec = W.TableSpec(3, dim, 3000, seed=91 + dim)
+    f = random_feature(W, rng, spec, pooling, bags=90, max_len=400)
+    rows_per_block = 8 if dim % 4 or dim > 256 else 256 // max(4, 1 << (dim // 4 - 1).bit_length())
+    per_block = [int(f.offsets[min(b + rows_per_block, len(f.valid_lengths))] - f.offsets[b])
+                 for b in range(0, len(f.valid_lengths), rows_per_block)]
+    assert max(per_block) > 1024, per_block  # at least one unstaged block
+    print(f"case: dim={dim} pooling={pooling} occurrences={len(f.keys)} block max {max(per_block)}", flush=True)
+    shard = H.DeviceShard(torch, [spec])
+    shard.init_rows()
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
+    out = shard.lookup([H.DeviceFeature(torch, f)], status=status)[0]
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0
+    want = expected(oracle_store(spec), f, dim)
+    assert_close(out.cpu().numpy(), want, f"long bags dim={dim} pooling={pooling}", strict_ulp=0)
+
+
 def test_gather_many_parts_one_call(torch_gpu, pkg):
     """Up to 32 features of different tables/dims in one launch, 40 -> two calls."""
     torch, W, H = torch_gpu, pkg.workloads, pkg.eps_hip
