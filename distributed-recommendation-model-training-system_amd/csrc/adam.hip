@@ -582,20 +582,32 @@ __global__ void __launch_bounds__(kBlock) SortedUpdateKernel(FusedArgs a) {
 constexpr uint32_t kHotBlock = 256;                       // threads of a hot-row block
 constexpr uint32_t kHotRing = 4;                          // chunks staged in LDS per block
 constexpr uint32_t kUnitCache = 512;                      // unit headers a block stages in LDS
-constexpr uint32_t kHotPitch = kHotChunk + 4;             // floats per tile row (one column)
-// Shape of a hot-row unit of kS columns (32 or 64): lanes per reference in a
-// producer's row load, references per row load, row loads per producer lane
-// per chunk.
-template <uint32_t kS>
+// Shape of a hot-row unit of kS columns (16, 32 or 64) in chunks of kC
+// references (kS * kC = 4,096 or fewer products a tile): lanes per reference
+// in a producer's row load, references per row load, row loads per producer
+// lane per chunk, reference words per producer lane per chunk, floats per
+// tile row (one column), and the parts the adding wave reads a tile in (of
+// kPart references: 32 for 16-column units, whose 256-reference chunks would
+// otherwise need more registers than the kernel has, 64 for the others).
+template <uint32_t kS, uint32_t kC>
 struct HotShape {
   static constexpr uint32_t kQuads = kS / 4;
   static constexpr uint32_t kRefsPerLoad = kWave / kQuads;
-  static constexpr uint32_t kLoads = kHotChunk / kRefsPerLoad;
-  static_assert(kHotChunk == kWave && kS <= kWave && kWave % kQuads == 0 && kLoads % 4 == 0,
+  static constexpr uint32_t kLoads = kC / kRefsPerLoad;
+  static constexpr uint32_t kWords = kC / kWave;
+  static constexpr uint32_t kPitch = kC + 4;
+  static constexpr uint32_t kPart = kS < 32 ? kWave / 2 : kWave;
+  // Own chunks each producer keeps in flight: two (four measured no faster),
+  // one for 16-column units, whose chunks of 256 references keep as many
+  // bytes in flight and leave the registers for their longer reference lists.
+  static constexpr uint32_t kDepth = kS < 32 ? 1 : 2;
+  static constexpr uint32_t kParts = kC / kPart;
+  static_assert(kC % kWave == 0 && kS <= kWave && kWave % kQuads == 0 && kLoads % 4 == 0 &&
+                    kLoads <= 16 && kS * kC <= kWave * kWave,
                 "hot-row tile shape");
 };
 constexpr uint32_t kProducers = kHotBlock / kWave - 1;
-constexpr uint32_t kDepth = 2;  // own chunks each producer keeps in flight (4 measured no faster)
+
 // Sorted positions per row-run window for groups of 2^log2g lanes: about 5
 // rows per group at the usual ~3 references per row.  Wider groups take
 // narrower windows, so a class of wide rows still spreads over many blocks.
@@ -621,13 +633,14 @@ struct VecArgs {
 };
 static_assert(sizeof(VecArgs) <= 4096, "update arguments fit the kernel-argument segment");
 
-// Position of (column c, reference r) in a hot-row tile.  Groups of four
-// references are rotated by the column's 16-column group (XOR; the identity
-// for slices of 16 columns), so a producer's stores of one row load hit
-// distinct banks, and the adding wave's 16-byte reads of four consecutive
-// references stay aligned.
+// Position of (column c, reference r) in a hot-row tile of kPitch floats a
+// column.  Groups of four references are rotated by the column's 16-column
+// group (XOR; the identity for slices of 16 columns), so a producer's stores
+// of one row load hit distinct banks, and the adding wave's 16-byte reads of
+// four consecutive references stay aligned.
+template <uint32_t kPitch>
 __device__ __forceinline__ uint32_t TileAt(uint32_t c, uint32_t r) {
-  return c * kHotPitch + 4u * ((r >> 2) ^ (c >> 4)) + (r & 3u);
+  return c * kPitch + 4u * ((r >> 2) ^ (c >> 4)) + (r & 3u);
 }
 
 __device__ __forceinline__ const float* RefSource(const float* const* grad, uint64_t word,
@@ -648,7 +661,7 @@ __device__ __forceinline__ bool VecPrologue(const VecArgs& a, TableDesc* s_t, co
   return LaunchGate(a.ctrl, s_t, a.gs, a.role, s_mode, write);
 }
 
-// One chunk of a hot work unit: positions [cbase, cbase + kHotChunk) of the
+// One chunk of a hot work unit: positions [cbase, cbase + chunk) of the
 // row whose references are the sorted positions [start, end), for the kSlice
 // columns from col0.  `ok` is false past the stream's last unit.  Every field
 // is the same in all lanes of a wavefront.
@@ -661,11 +674,11 @@ struct HotSlot {
 // 4*quad .. 4*quad+3 of reference kHotRefsPerLoad*k + sub, with its scale;
 // wmv is lane l's column of the unit's w, m, v (used when the chunk ends its
 // unit).
-template <uint32_t kS>
+template <uint32_t kS, uint32_t kC>
 struct HotRows {
   HotSlot c;
-  float4 x[HotShape<kS>::kLoads];
-  float s[HotShape<kS>::kLoads];
+  float4 x[HotShape<kS, kC>::kLoads];
+  float s[HotShape<kS, kC>::kLoads];
   float wmv[3];
 };
 
@@ -673,10 +686,10 @@ struct HotRows {
 // order the row loads use them: entry [sub][k] is reference
 // kHotRefsPerLoad*k + sub, so a lane reads its kHotLoads pointers and scales
 // with a few 16-byte reads.
-template <uint32_t kS>
+template <uint32_t kS, uint32_t kC>
 struct HotRefs {
-  const float* src[HotShape<kS>::kRefsPerLoad][HotShape<kS>::kLoads];
-  float scale[HotShape<kS>::kRefsPerLoad][HotShape<kS>::kLoads];
+  const float* src[HotShape<kS, kC>::kRefsPerLoad][HotShape<kS, kC>::kLoads];
+  float scale[HotShape<kS, kC>::kRefsPerLoad][HotShape<kS, kC>::kLoads];
 };
 
 // s_waitcnt operand that waits for LDS (and scalar memory) accesses only:
@@ -708,16 +721,21 @@ __device__ __forceinline__ void PostCounter(uint32_t* counter, uint32_t value) {
     __hip_atomic_store(counter, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-template <uint32_t kSlice>
+template <uint32_t kSlice, uint32_t kChunk>
 __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
-  constexpr uint32_t kHotQuads = HotShape<kSlice>::kQuads;
-  constexpr uint32_t kHotRefsPerLoad = HotShape<kSlice>::kRefsPerLoad;
-  constexpr uint32_t kHotLoads = HotShape<kSlice>::kLoads;
+  using Shape = HotShape<kSlice, kChunk>;
+  constexpr uint32_t kHotQuads = Shape::kQuads;
+  constexpr uint32_t kHotRefsPerLoad = Shape::kRefsPerLoad;
+  constexpr uint32_t kHotLoads = Shape::kLoads;
+  constexpr uint32_t kPitch = Shape::kPitch;
+  constexpr uint32_t kPart = Shape::kPart;
+  constexpr uint32_t kParts = Shape::kParts;
+  constexpr uint32_t kDepth = Shape::kDepth;
   __shared__ TableDesc s_t[EPS_HIP_MAX_TABLES];
   __shared__ const float* s_grad[EPS_HIP_MAX_FEATURES];
-  __shared__ __align__(16) float s_tile[kHotRing][kSlice * kHotPitch];
+  __shared__ __align__(16) float s_tile[kHotRing][kSlice * kPitch];
   __shared__ float s_wmv[kHotRing][3][kSlice];
-  __shared__ __align__(16) HotRefs<kSlice> s_ref[kProducers];
+  __shared__ __align__(16) HotRefs<kSlice, kChunk> s_ref[kProducers];
   // ready[t]: chunks staged in tile t so far; used[t]: chunks added from it.
   __shared__ uint32_t s_ready[kHotRing], s_used[kHotRing];
   __shared__ uint4 s_unit[kUnitCache];  // {start, end, key, col0} of the block's first units
@@ -832,9 +850,9 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
     }
   };
   auto after = [&](const HotSlot& c) {  // the chunk that follows c in the stream
-    if (c.ok && c.cbase + kHotChunk < c.end) {
+    if (c.ok && c.cbase + kChunk < c.end) {
       HotSlot t = c;
-      t.cbase += kHotChunk;
+      t.cbase += kChunk;
       return t;
     }
     return take();
@@ -854,39 +872,67 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
     HotSlot cn = after(c);       // chunk j + 1
     HotSlot cnn = after(cn);     // chunk j + 2
     float acc = 0.f;
-    auto read_tile = [&](uint32_t j, float4* x) {  // lanes past the slice read nothing
+    // Part h (references kPart * h onwards) of chunk j's tile into x.  With
+    // one part a chunk, lanes past the slice read nothing.  With several,
+    // they read a copy of a slice column and drop it: every lane then writes
+    // all of x, so no old contents of a buffer stay live from part to part
+    // (which would make the compiler copy whole buffers).
+    const uint32_t sl = lane % kSlice;
+    auto read_part = [&](uint32_t j, uint32_t h, float4* x) {
       const float* tile = s_tile[j % kHotRing];
-      if (lane < kSlice) {
+      if (kParts > 1 || lane < kSlice) {
 #pragma unroll
-        for (uint32_t g = 0; g < kHotChunk / 4; ++g)
-          x[g] = *reinterpret_cast<const float4*>(tile + TileAt(lane, 4 * g));
+        for (uint32_t g = 0; g < kPart / 4; ++g)
+          x[g] = *reinterpret_cast<const float4*>(tile + TileAt<kPitch>(sl, kPart * h + 4 * g));
       }
     };
     auto ready = [&](uint32_t j) {
       if (!stalled && !WaitCounter(&s_ready[j % kHotRing], j / kHotRing + 1, 0, a.spin_limit)) stalled = true;
     };
-    // Adds chunk j (values in x, chunk c); reads chunk j + 1 into y.
-    auto add = [&](uint32_t j, const float4* x, float4* y) {
-      // x arrived during the previous adds.  Wait for it here, before more
-      // reads are issued: the LDS counter tracks at most 15 accesses, so a
-      // wait placed after the next tile's 16 reads would wait for those too.
-      __builtin_amdgcn_s_waitcnt(kLgkmZero);
-      __builtin_amdgcn_sched_barrier(0);
+    // Adds chunk j (chunk c) part by part: part h is in x for even h and in y
+    // for odd h, and each part's adds overlap the reads of the next part (of
+    // chunk j + 1's first part after the last), which go to the other buffer.
+    // So a chunk of an even number of parts starts and ends in x.  The
+    // hand-over (tile release, readiness poll, walk to the next chunk) comes
+    // once per chunk, whatever its length.  With several parts a chunk, the
+    // next tile is read after the stream's last chunk all the same (plain LDS
+    // reads, dropped), for the same reason.
+    auto add = [&](uint32_t j, float4* x, float4* y) {
       const uint32_t t = j % kHotRing;
-      const uint32_t sl = lane % kSlice;  // lanes past the slice read a copy and drop it
-      float w = s_wmv[t][0][sl], m = s_wmv[t][1][sl], v = s_wmv[t][2][sl];
-      const uint32_t peek = __hip_atomic_load(&s_ready[(j + 2) % kHotRing], __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_WORKGROUP);
-      if (cn.ok) read_tile(j + 1, y);
-      __builtin_amdgcn_sched_barrier(0);
+      float w = 0.f, m = 0.f, v = 0.f;
+      uint32_t peek = 0;
 #pragma unroll
-      for (uint32_t g = 0; g < kHotChunk / 4; ++g) {
-        acc = acc + x[g].x;
-        acc = acc + x[g].y;
-        acc = acc + x[g].z;
-        acc = acc + x[g].w;
+      for (uint32_t h = 0; h < kParts; ++h) {
+        const float4* cur = h % 2 ? y : x;
+        float4* nxt = h % 2 ? x : y;
+        // cur arrived during the previous adds.  Wait for it here, before more
+        // reads are issued: the LDS counter tracks at most 15 accesses, so a
+        // wait placed after the next part's 16 reads would wait for those too.
+        __builtin_amdgcn_s_waitcnt(kLgkmZero);
+        __builtin_amdgcn_sched_barrier(0);
+        if (h + 1 < kParts) {
+          read_part(j, h + 1, nxt);
+        } else {
+          w = s_wmv[t][0][sl];
+          m = s_wmv[t][1][sl];
+          v = s_wmv[t][2][sl];
+          peek = __hip_atomic_load(&s_ready[(j + 2) % kHotRing], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          if (kParts > 1 || cn.ok) read_part(j + 1, 0, nxt);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (uint32_t g = 0; g < kPart / 4; ++g) {
+          acc = acc + cur[g].x;
+          acc = acc + cur[g].y;
+          acc = acc + cur[g].z;
+          acc = acc + cur[g].w;
+        }
+        // With several parts, each part's sum is taken here: otherwise the
+        // compiler sinks every part's adds below the last part's reads, which
+        // then holds all the chunk's values in registers at once.
+        if constexpr (kParts > 1) asm volatile("" : "+v"(acc));
+        __builtin_amdgcn_sched_barrier(0);
       }
-      __builtin_amdgcn_sched_barrier(0);
       // Tile t is free once chunk j's values and w, m, v are read: they were
       // read before tile j + 1's reads, and a wavefront's LDS accesses are
       // performed in order, so the counter store needs no wait for the reads
@@ -896,7 +942,7 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
       if (lane == 0)
         __hip_atomic_store(&s_used[t], j / kHotRing + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       __builtin_amdgcn_sched_barrier(0);
-      if (c.cbase + kHotChunk >= c.end) {  // the unit's last chunk
+      if (c.cbase + kChunk >= c.end) {  // the unit's last chunk
         const KeyParts kp = SplitKey(c.key, a.row_bits);
         const TableDesc& T = s_t[min(kp.table, a.tables - 1)];
         if (!KeyInRange(kp, a.tables, T.rows)) s_bad = 1;
@@ -918,16 +964,19 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
       cn = cnn;
       cnn = after(cnn);
     };
-    float4 xa[kHotChunk / 4], xb[kHotChunk / 4];
+    float4 xa[kPart / 4], xb[kPart / 4];
     if (c.ok) {
       ready(0);
-      read_tile(0, xa);
+      read_part(0, 0, xa);
       if (cn.ok) ready(1);
     }
     for (uint32_t j = 0; c.ok && !stalled; j += 2) {
       add(j, xa, xb);
       if (!c.ok || stalled) break;
-      add(j + 1, xb, xa);
+      if constexpr (kParts % 2 == 1)
+        add(j + 1, xb, xa);
+      else
+        add(j + 1, xa, xb);
     }
   } else {
     // Producer p stages chunks p, p + kProducers, ... (its own chunks, counted
@@ -940,7 +989,7 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
     const uint32_t p = wave - 1;
     const uint32_t quad = lane % kHotQuads, sub = lane / kHotQuads;
     const float* idle = reinterpret_cast<const float*>(a.rs);
-    HotRefs<kSlice>& slots = s_ref[p];
+    HotRefs<kSlice, kChunk>& slots = s_ref[p];
     fetch();
     HotSlot cur = take();  // cursor over the stream, at chunk jc
     uint32_t jc = 0, total = cur.ok ? ~0u : 0u;
@@ -951,37 +1000,44 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
         if (!cur.ok && total == ~0u) total = jc;
       }
     };
-    // Reference words of one chunk in flight (lane l: reference l).
+    // Reference words of one chunk in flight (lane l: references l, l + 64, ...).
     struct Words {
       HotSlot c;
-      uint64_t word;
+      uint64_t word[Shape::kWords];
     };
     HotSlot dc{};  // chunk whose references are in the LDS slots
     auto load_words = [&](Words& w) {
       w.c = cur;
-      const uint32_t pos = cur.ok ? min(cur.cbase + lane, cur.end - 1) : 0u;  // end <= n (sane)
-      w.word = a.rs[pos];
+#pragma unroll
+      for (uint32_t k = 0; k < Shape::kWords; ++k) {
+        const uint32_t pos = cur.ok ? min(cur.cbase + kWave * k + lane, cur.end - 1) : 0u;  // end <= n (sane)
+        w.word[k] = a.rs[pos];
+      }
     };
-    // Lane l decodes the word of reference l: its gradient row (from the
-    // slice's first column) and scale.
+    // Lane l decodes the words of references l, l + 64, ...: their gradient
+    // rows (from the slice's first column) and scales.
     auto decode = [&](const Words& w) {
       const HotSlot& wc = w.c;
       dc = wc;
       const TableDesc& T = s_t[min(wc.key >> a.row_bits, a.tables - 1)];
-      const RefParts rp = SplitRef(w.word);
-      const bool ref_ok = RefInRange(rp, a.features, s_rows[min(rp.feature, a.features - 1)]);
-      if (wc.ok && !ref_ok) s_bad = 1;
-      float scale;
-      const float* src = RefSource(s_grad, w.word, T.dim, wc.col0, scale);
-      slots.src[lane % kHotRefsPerLoad][lane / kHotRefsPerLoad] = wc.ok && ref_ok ? src : idle;
-      slots.scale[lane % kHotRefsPerLoad][lane / kHotRefsPerLoad] = scale;
+#pragma unroll
+      for (uint32_t k = 0; k < Shape::kWords; ++k) {
+        const uint32_t r = kWave * k + lane;
+        const RefParts rp = SplitRef(w.word[k]);
+        const bool ref_ok = RefInRange(rp, a.features, s_rows[min(rp.feature, a.features - 1)]);
+        if (wc.ok && !ref_ok) s_bad = 1;
+        float scale;
+        const float* src = RefSource(s_grad, w.word[k], T.dim, wc.col0, scale);
+        slots.src[r % kHotRefsPerLoad][r / kHotRefsPerLoad] = wc.ok && ref_ok ? src : idle;
+        slots.scale[r % kHotRefsPerLoad][r / kHotRefsPerLoad] = scale;
+      }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
     };
     // Lanes whose columns lie past the row's dimension read the slice's first
     // columns; their products are never stored by the adding wave.
-    auto load_rows = [&](HotRows<kSlice>& r) {
+    auto load_rows = [&](HotRows<kSlice, kChunk>& r) {
       r.c = dc;
       const KeyParts kp = SplitKey(dc.key, a.row_bits);
       const TableDesc& T = s_t[min(kp.table, a.tables - 1)];
@@ -1008,33 +1064,33 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
       const uint32_t ms = dc.ok && key_ok ? dim : 0u;
       r.wmv[0] = LoadF(row); r.wmv[1] = LoadF(row + ms); r.wmv[2] = LoadF(row + 2 * ms);
     };
-    auto stage = [&](const HotRows<kSlice>& r, uint32_t j) {
+    auto stage = [&](const HotRows<kSlice, kChunk>& r, uint32_t j) {
       const uint32_t t = j % kHotRing;
       if (!stalled && !WaitCounter(&s_used[t], j / kHotRing, 1, a.spin_limit)) stalled = true;
       if (stalled) return;  // nothing more is staged
       // Load k brings columns 4*quad .. 4*quad+3 of reference
       // kHotRefsPerLoad*k + sub; each lands at TileAt(column, reference).
       float* tile = s_tile[t];
-      if (r.c.cbase + kHotChunk <= r.c.end) {  // every reference inside the row
+      if (r.c.cbase + kChunk <= r.c.end) {  // every reference inside the row
 #pragma unroll
         for (uint32_t k = 0; k < kHotLoads; ++k) {
           const float sv = r.s[k];
-          float* q = tile + TileAt(4 * quad, kHotRefsPerLoad * k + sub);
+          float* q = tile + TileAt<kPitch>(4 * quad, kHotRefsPerLoad * k + sub);
           q[0] = r.x[k].x * sv;
-          q[kHotPitch] = r.x[k].y * sv;
-          q[2 * kHotPitch] = r.x[k].z * sv;
-          q[3 * kHotPitch] = r.x[k].w * sv;
+          q[kPitch] = r.x[k].y * sv;
+          q[2 * kPitch] = r.x[k].z * sv;
+          q[3 * kPitch] = r.x[k].w * sv;
         }
       } else {  // references past the row's end add -0.0f, the identity
 #pragma unroll
         for (uint32_t k = 0; k < kHotLoads; ++k) {
           const bool in = r.c.cbase + kHotRefsPerLoad * k + sub < r.c.end;
           const float sv = r.s[k];
-          float* q = tile + TileAt(4 * quad, kHotRefsPerLoad * k + sub);
+          float* q = tile + TileAt<kPitch>(4 * quad, kHotRefsPerLoad * k + sub);
           q[0] = in ? r.x[k].x * sv : -0.f;
-          q[kHotPitch] = in ? r.x[k].y * sv : -0.f;
-          q[2 * kHotPitch] = in ? r.x[k].z * sv : -0.f;
-          q[3 * kHotPitch] = in ? r.x[k].w * sv : -0.f;
+          q[kPitch] = in ? r.x[k].y * sv : -0.f;
+          q[2 * kPitch] = in ? r.x[k].z * sv : -0.f;
+          q[3 * kPitch] = in ? r.x[k].w * sv : -0.f;
         }
       }
       if (lane < kSlice) {
@@ -1048,7 +1104,7 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
     // prologue leaves the loads in the loop's own order (words(D), rows(0),
     // words(D+1), rows(1), ...), so the compiler's load waits inside the loop
     // can be exact.
-    HotRows<kSlice> rows[kDepth];
+    HotRows<kSlice, kChunk> rows[kDepth];
     Words words[kDepth];
     advance(p);  // own chunk 0
 #pragma unroll
@@ -1068,7 +1124,7 @@ __global__ void __launch_bounds__(kHotBlock) HotSliceKernel(VecArgs a) {
     // Words and rows both get D own chunks to arrive (the decode needs no
     // wait of its own: its words were issued before the rows the stage
     // waited for).  D own chunks per pass keep the buffers static.
-    auto own = [&](HotRows<kSlice>& r, Words& w, uint32_t j) {
+    auto own = [&](HotRows<kSlice, kChunk>& r, Words& w, uint32_t j) {
       stage(r, j);
       decode(w);
       load_words(w);
@@ -1444,6 +1500,15 @@ int ThreadOverlap(Overlap** out) {
 // so a very long row's chain data spreads over several CUs.
 constexpr uint64_t kOverlapTableRefs = 1ull << 16;
 constexpr uint32_t kFineSlice = 16, kNarrowSlice = 32, kWideSlice = 64;  // columns per hot-row unit
+// References per hot-row chunk of each unit width.  16-column units take
+// chunks of 256 references (a tile of 4,096 products, like a 64-column
+// chunk), so their blocks hand a tile over (release, readiness poll, walk to
+// the next chunk) once per 256 references instead of once per 64: 65,536
+// pairs on one table, fused update 98-102 -> 84-91 us.  32-column units keep
+// 64: with 128 the kernel needs 256 registers and 84 KB of LDS, one block per
+// CU instead of two, and 4 x 8.4 M references lost (update 7.4-8.2 -> 8.1-8.3
+// ms).
+constexpr uint32_t kFineChunk = 256, kNarrowChunk = 64, kWideChunk = 64;
 // Pushes with very long rows but fewer vector references than this take
 // 16-column units (below).
 constexpr uint64_t kFinePushRefs = 1ull << 18;
@@ -1479,11 +1544,11 @@ int LaunchRowRun(unsigned grid, const VecArgs& a, hipStream_t s) {
 int LaunchVectorUpdate(uint32_t cls, uint32_t hot_slice, unsigned grid, const VecArgs& a, hipStream_t s) {
   if (hot_slice) {
     if (hot_slice == kWideSlice)
-      hipLaunchKernelGGL(HotSliceKernel<kWideSlice>, dim3(grid), dim3(kHotBlock), 0, s, a);
+      hipLaunchKernelGGL((HotSliceKernel<kWideSlice, kWideChunk>), dim3(grid), dim3(kHotBlock), 0, s, a);
     else if (hot_slice == kFineSlice)
-      hipLaunchKernelGGL(HotSliceKernel<kFineSlice>, dim3(grid), dim3(kHotBlock), 0, s, a);
+      hipLaunchKernelGGL((HotSliceKernel<kFineSlice, kFineChunk>), dim3(grid), dim3(kHotBlock), 0, s, a);
     else
-      hipLaunchKernelGGL(HotSliceKernel<kNarrowSlice>, dim3(grid), dim3(kHotBlock), 0, s, a);
+      hipLaunchKernelGGL((HotSliceKernel<kNarrowSlice, kNarrowChunk>), dim3(grid), dim3(kHotBlock), 0, s, a);
     EPS_HIP_LAUNCHED("hot row update");
     return EPS_HIP_OK;
   }
