@@ -1473,21 +1473,18 @@ uint64_t SpanBlocks(uint64_t count, SpanKind kind = kGradientSpan) {
 // and device (created on first use, default priority, never destroyed), so
 // concurrent callers never share an event.
 // The side stream of a calling thread on one device, and how a push orders
-// it against the push stream: the fork (the side stream waits for the push
+// it against the push stream.  The fork (the side stream waits for the push
 // stream's gradient scan) and the join (the push stream waits for the side
-// stream's kernels).  Both can go through a device word: the signalling
-// stream writes the push's sequence number to it once its earlier work is
-// done, and the waiting stream waits until the word reaches it.  A stream's
-// wait on an event that is still pending costs ~14 us of host time on MI355X,
-// a write-value or wait-value command ~2 us; and the push stream resumes
-// sooner after a word than after an event.  Measured: 65,536 pairs on one
-// table (whose step the host's issue rate sets), fork by word 0.095 -> 0.086
-// ms a step, fork and join by word 0.105-0.111 -> 0.084-0.090 ms on another
-// box; 26 tables of ~43,000 references, join by word: fused update 197-203
-// -> 189-196 us.  The fork goes by word only for small pushes (fewer than
-// kFinePushRefs vector references): a side stream that waited on a word
+// stream's kernels) are event waits, or, for small pushes (fewer than
+// kFinePushRefs vector references, whose step the host's issue rate sets),
+// waits on a device word: the signalling stream writes the push's sequence
+// number to it once its earlier work is done, and the waiting stream waits
+// until the word reaches it.  A stream's wait on an event that is still
+// pending costs ~14 us of host time on MI355X, a write-value or wait-value
+// command ~2 us (65,536 pairs on one table, fork by word: 0.095 -> 0.086 ms a
+// step).  Large pushes keep the events: a side stream that waited on a word
 // through a long gradient scan started late (4 x 8.4 M references, fused
-// update 7.7-8.5 -> 9.0-9.7 ms), so large pushes fork by event.
+// update 7.7-8.5 -> 9.0-9.7 ms).
 struct Overlap {
   hipStream_t side = nullptr;
   hipEvent_t fork = nullptr, join = nullptr;
@@ -1616,7 +1613,7 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
   // The first kernel of the primary phase makes the guard decision.
   uint32_t role = kDecide;
   bool overlap = false;  // hot rows (on the side stream, joined before the checked apply)
-  bool join_by_word = false;  // the join goes through a device word (see Overlap)
+  bool by_value = false;  // fork and join by device word (see Overlap)
   uint64_t seq = 0;
   Overlap* ov = nullptr;
   for (uint32_t k = 0; k < table_count; ++k) {
@@ -1702,9 +1699,9 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
           hot_units ? xcd_grid(std::min<uint64_t>(hot_units, long_rows ? kHotGrid : kWideHotGrid)) : 0;
       if (overlap) {
         EPS_HIP_TRY(ThreadOverlap(&ov));
-        seq = ++ov->seq;
-        join_by_word = ov->words != nullptr;
-        if (ov->words && vector_occurrences < kFinePushRefs) {
+        by_value = ov->words && vector_occurrences < kFinePushRefs;
+        if (by_value) {
+          seq = ++ov->seq;
           EPS_HIP_TRY(Check(hipStreamWriteValue64(s, ov->words, seq, 0), "update fork"));
           EPS_HIP_TRY(Check(hipStreamWaitValue64(ov->side, ov->words, seq, hipStreamWaitValueGte, ~0ull),
                             "update fork wait"));
@@ -1752,7 +1749,7 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
           EPS_HIP_TRY(LaunchVectorUpdate(cls, 0, va.class_grid[cls], va, rs));
         }
       }
-      if (overlap && join_by_word)
+      if (overlap && by_value)
         EPS_HIP_TRY(Check(hipStreamWriteValue64(ov->side, ov->words + 1, seq, 0), "update join"));
       else if (overlap)
         EPS_HIP_TRY(Check(hipEventRecord(ov->join, ov->side), "update join"));
@@ -1780,7 +1777,7 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
     }
   }
   if (overlap && (phases & kPrimary)) {
-    if (join_by_word)
+    if (by_value)
       EPS_HIP_TRY(Check(hipStreamWaitValue64(s, ov->words + 1, seq, hipStreamWaitValueGte, ~0ull), "hot-row join wait"));
     else
       EPS_HIP_TRY(Check(hipStreamWaitEvent(s, ov->join, 0), "hot-row join wait"));
