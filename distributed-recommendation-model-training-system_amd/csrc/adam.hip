@@ -555,8 +555,7 @@ __global__ void __launch_bounds__(kBlock) SortedUpdateKernel(FusedArgs a) {
 //
 //  * HotSliceKernel: rows with more than kLongRefs references (listed at
 //    prepare time).  Work unit = (hot row, kSlice-column slice); a block
-//    works through a stream of units chunk by chunk (64 references; 256 for
-//    16-column units, so a chunk's tile holds the same 4,096 products).
+//    works through a stream of units chunk by chunk (kHotChunk references).
 //    Wave 0 adds: lane c < kSlice owns column col0 + c, adds the chunk's
 //    products in reference order (one dependent add per reference) and
 //    applies Adam after the unit's last chunk.  Waves 1..kProducers produce:
@@ -566,7 +565,7 @@ __global__ void __launch_bounds__(kBlock) SortedUpdateKernel(FusedArgs a) {
 //    the unit's w, m, v when the chunk is its last.  Tiles change hands
 //    through two LDS counters per tile (staged / added), so the waves never
 //    meet at a block barrier, and each producer keeps two chunks of rows in
-//    flight (one of the longer 16-column chunks).  For very long rows the slices are narrow (32 columns) so that a
+//    flight.  For very long rows the slices are narrow (32 columns) so that a
 //    hot row's chain data spreads over several CUs: a block's producers then
 //    move half of a 64-column chunk's bytes through their CU per chunk, and
 //    the adding wave's serial chain, not the CU's memory pipeline, sets the
@@ -1472,24 +1471,9 @@ uint64_t SpanBlocks(uint64_t count, SpanKind kind = kGradientSpan) {
 // The hot-row kernel's side stream and fork/join events, per calling thread
 // and device (created on first use, default priority, never destroyed), so
 // concurrent callers never share an event.
-// The side stream of a calling thread on one device, and how a push orders
-// it against the push stream.  The fork (the side stream waits for the push
-// stream's gradient scan) and the join (the push stream waits for the side
-// stream's kernels) are event waits, or, for small pushes (fewer than
-// kFinePushRefs vector references, whose step the host's issue rate sets),
-// waits on a device word: the signalling stream writes the push's sequence
-// number to it once its earlier work is done, and the waiting stream waits
-// until the word reaches it.  A stream's wait on an event that is still
-// pending costs ~14 us of host time on MI355X, a write-value or wait-value
-// command ~2 us (65,536 pairs on one table, fork by word: 0.095 -> 0.086 ms a
-// step).  Large pushes keep the events: a side stream that waited on a word
-// through a long gradient scan started late (4 x 8.4 M references, fused
-// update 7.7-8.5 -> 9.0-9.7 ms).
 struct Overlap {
   hipStream_t side = nullptr;
   hipEvent_t fork = nullptr, join = nullptr;
-  uint64_t* words = nullptr;  // {fork, join}; nullptr: the device has no stream wait-value
-  uint64_t seq = 0;
 };
 int ThreadOverlap(Overlap** out) {
   constexpr int kDevices = 64;
@@ -1499,21 +1483,9 @@ int ThreadOverlap(Overlap** out) {
   if (device < 0 || device >= kDevices) return Fail(EPS_HIP_UNAVAILABLE, "device ordinal out of range");
   Overlap& o = per_device[device];
   if (!o.side) {
-    hipStream_t side = nullptr;
-    EPS_HIP_TRY(Check(hipStreamCreateWithFlags(&side, hipStreamNonBlocking), "hot-row stream"));
+    EPS_HIP_TRY(Check(hipStreamCreateWithFlags(&o.side, hipStreamNonBlocking), "hot-row stream"));
     EPS_HIP_TRY(Check(hipEventCreateWithFlags(&o.fork, hipEventDisableTiming), "hot-row fork event"));
     EPS_HIP_TRY(Check(hipEventCreateWithFlags(&o.join, hipEventDisableTiming), "hot-row join event"));
-    int wait_value = 0;
-    EPS_HIP_TRY(Check(hipDeviceGetAttribute(&wait_value, hipDeviceAttributeCanUseStreamWaitValue, device),
-                      "stream wait-value attribute"));
-    if (wait_value) {
-      void* words = nullptr;
-      EPS_HIP_TRY(Check(hipMalloc(&words, 2 * sizeof(uint64_t)), "hot-row order words"));
-      EPS_HIP_TRY(Check(hipMemsetAsync(words, 0, 2 * sizeof(uint64_t), side), "hot-row order words"));
-      EPS_HIP_TRY(Check(hipStreamSynchronize(side), "hot-row order words"));
-      o.words = static_cast<uint64_t*>(words);
-    }
-    o.side = side;  // set up: later calls use it as it is
   }
   *out = &o;
   return EPS_HIP_OK;
@@ -1613,8 +1585,6 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
   // The first kernel of the primary phase makes the guard decision.
   uint32_t role = kDecide;
   bool overlap = false;  // hot rows (on the side stream, joined before the checked apply)
-  bool by_value = false;  // fork and join by device word (see Overlap)
-  uint64_t seq = 0;
   Overlap* ov = nullptr;
   for (uint32_t k = 0; k < table_count; ++k) {
     const uint32_t t = plan.table_of_key[k];
@@ -1699,16 +1669,8 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
           hot_units ? xcd_grid(std::min<uint64_t>(hot_units, long_rows ? kHotGrid : kWideHotGrid)) : 0;
       if (overlap) {
         EPS_HIP_TRY(ThreadOverlap(&ov));
-        by_value = ov->words && vector_occurrences < kFinePushRefs;
-        if (by_value) {
-          seq = ++ov->seq;
-          EPS_HIP_TRY(Check(hipStreamWriteValue64(s, ov->words, seq, 0), "update fork"));
-          EPS_HIP_TRY(Check(hipStreamWaitValue64(ov->side, ov->words, seq, hipStreamWaitValueGte, ~0ull),
-                            "update fork wait"));
-        } else {
-          EPS_HIP_TRY(Check(hipEventRecord(ov->fork, s), "update fork"));
-          EPS_HIP_TRY(Check(hipStreamWaitEvent(ov->side, ov->fork, 0), "update fork wait"));
-        }
+        EPS_HIP_TRY(Check(hipEventRecord(ov->fork, s), "update fork"));
+        EPS_HIP_TRY(Check(hipStreamWaitEvent(ov->side, ov->fork, 0), "update fork wait"));
       }
       if (hot_units && !rows_beside) {
         va.role = role;
@@ -1749,10 +1711,7 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
           EPS_HIP_TRY(LaunchVectorUpdate(cls, 0, va.class_grid[cls], va, rs));
         }
       }
-      if (overlap && by_value)
-        EPS_HIP_TRY(Check(hipStreamWriteValue64(ov->side, ov->words + 1, seq, 0), "update join"));
-      else if (overlap)
-        EPS_HIP_TRY(Check(hipEventRecord(ov->join, ov->side), "update join"));
+      if (overlap) EPS_HIP_TRY(Check(hipEventRecord(ov->join, ov->side), "update join"));
       if (hot_units && rows_beside) {
         va.role = hot_role;
         EPS_HIP_TRY(LaunchVectorUpdate(0, slice, unsigned(hot_blocks), va, s));
@@ -1776,12 +1735,7 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
       EPS_HIP_LAUNCHED("sorted update");
     }
   }
-  if (overlap && (phases & kPrimary)) {
-    if (by_value)
-      EPS_HIP_TRY(Check(hipStreamWaitValue64(s, ov->words + 1, seq, hipStreamWaitValueGte, ~0ull), "hot-row join wait"));
-    else
-      EPS_HIP_TRY(Check(hipStreamWaitEvent(s, ov->join, 0), "hot-row join wait"));
-  }
+  if (overlap && (phases & kPrimary)) EPS_HIP_TRY(Check(hipStreamWaitEvent(s, ov->join, 0), "hot-row join wait"));
   // The checked apply (after a validate-only pass) is one launch over every
   // class, one wavefront per row: it usually exits at once, and when it runs
   // it adds each row's references in the same order as the passes above.
