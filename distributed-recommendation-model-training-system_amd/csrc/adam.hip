@@ -555,7 +555,8 @@ __global__ void __launch_bounds__(kBlock) SortedUpdateKernel(FusedArgs a) {
 //
 //  * HotSliceKernel: rows with more than kLongRefs references (listed at
 //    prepare time).  Work unit = (hot row, kSlice-column slice); a block
-//    works through a stream of units chunk by chunk (kHotChunk references).
+//    works through a stream of units chunk by chunk (64 references; 256 for
+//    16-column units, so a chunk's tile holds the same 4,096 products).
 //    Wave 0 adds: lane c < kSlice owns column col0 + c, adds the chunk's
 //    products in reference order (one dependent add per reference) and
 //    applies Adam after the unit's last chunk.  Waves 1..kProducers produce:
@@ -565,7 +566,7 @@ __global__ void __launch_bounds__(kBlock) SortedUpdateKernel(FusedArgs a) {
 //    the unit's w, m, v when the chunk is its last.  Tiles change hands
 //    through two LDS counters per tile (staged / added), so the waves never
 //    meet at a block barrier, and each producer keeps two chunks of rows in
-//    flight.  For very long rows the slices are narrow (32 columns) so that a
+//    flight (one of the longer 16-column chunks).  For very long rows the slices are narrow (32 columns) so that a
 //    hot row's chain data spreads over several CUs: a block's producers then
 //    move half of a 64-column chunk's bytes through their CU per chunk, and
 //    the adding wave's serial chain, not the CU's memory pipeline, sets the

@@ -34,7 +34,6 @@ constexpr uint32_t kSrcSlots = 64;        // spread of the gradient/scale maximu
 constexpr uint32_t kHistCopies = 16;      // spread of the keygen histogram atomics
 constexpr uint32_t kXcds = 8;             // XCDs of an MI355X
 constexpr uint32_t kHotBuckets = 8;       // hot-row lists per XCD, by length (longest first)
-constexpr uint32_t kHotChunk = 64;        // references per chunk of the hot-row kernel
 
 // Control block at offset 0 of a push or update workspace (1 KiB).  Values
 // that many blocks update are kept in several copies (slots) written round
