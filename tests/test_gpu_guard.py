@@ -86,14 +86,19 @@ def test_bad_compact_scales_reject(torch_gpu, pkg):
     assert shard.adam_compact(0, slots, offsets, sources, scales, values) & H.STATUS_ERRORS == 0
 
 
-def test_forced_stall_reports_and_writes_no_hot_row(torch_gpu, pkg):
+@pytest.mark.parametrize("bags,overlap", [(24000, True), (90000, True), (24000, False)])
+def test_forced_stall_reports_and_writes_no_hot_row(torch_gpu, pkg, bags, overlap):
     """Spin limit 0: every hand-over wait of the hot-row kernel times out (it
-    runs for pushes with a table of 65,536 or more references, beside the row
-    kernels).  The push must report STALLED, in its status and in the
-    workspace history, and write none of the hot rows it stalled on; the row
-    kernels beside it do write theirs, so such a push is partial -- the C++
-    backend stops after one (tests/cpp/hip_backend_test.cpp).  From fresh
-    state, the same push with the default limit applies bit-exact."""
+    runs for pushes with a table of 65,536 or more references: in 16-column
+    units of 256-reference chunks under 262,144 vector references, 24,000
+    bags here, else in 32-column units of 64-reference chunks, 90,000 bags).
+    The push must report STALLED, in its status and in the workspace history,
+    and write none of the hot rows it stalled on.  Beside the row kernels
+    (`overlap`) those write theirs, so such a push is partial -- the C++
+    backend stops after one (tests/cpp/hip_backend_test.cpp); on one stream
+    the hot-row kernel runs first and the row kernels after it see the stall,
+    so nothing is written.  From fresh state, the same push with the default
+    limit applies bit-exact."""
     torch, W, H = torch_gpu, pkg.workloads, pkg.eps_hip
     rng = np.random.default_rng(12)
     spec = W.TableSpec(0, 64, 3000, seed=6)
@@ -101,8 +106,9 @@ def test_forced_stall_reports_and_writes_no_hot_row(torch_gpu, pkg):
     shard.init_rows()
     everything = torch.arange(spec.rows, device="cuda")
     before = shard.read_rows(0, everything).clone()
-    f = hot_feature(W, rng, spec, W.MEAN, bags=24000, hot_refs=3000)
+    f = hot_feature(W, rng, spec, W.MEAN, bags=bags, hot_refs=3000)
     assert len(f.keys) >= 65536
+    assert (len(f.keys) < 1 << 18) == (bags == 24000), len(f.keys)
     ids, counts = np.unique(f.keys, return_counts=True)
     hot = torch.from_numpy(ids[counts > 128].astype(np.int64)).cuda()
     assert hot.numel() > 0, "no hot row"
@@ -111,17 +117,19 @@ def test_forced_stall_reports_and_writes_no_hot_row(torch_gpu, pkg):
     try:
         H.check(L.eps_hip_debug_set_spin_limit(0))
         shard.prepare(dev)
-        status = shard.push(dev)
+        status = shard.push(dev, hot_overlap=overlap)
     finally:
         H.check(L.eps_hip_debug_set_spin_limit(1 << 22))
-    print(f"forced stall: status {status:#x}", flush=True)
+    print(f"forced stall: bags {bags}, overlap {overlap}, status {status:#x}", flush=True)
     assert status & H.STATUS_STALLED, f"{status:#x}"
     assert shard.history() & H.STATUS_STALLED
     assert torch.equal(shard.read_rows(0, hot), before[hot]), "a stalled hot row was written"
+    if not overlap:
+        assert torch.equal(shard.read_rows(0, everything), before), "a row was written after the stall"
     shard.clear_history()
     shard.init_rows()  # fresh state: the stalled push was partial
     shard.prepare(dev)
-    status = shard.push(dev)
+    status = shard.push(dev, hot_overlap=overlap)
     assert status & H.STATUS_ERRORS == 0, f"{status:#x}"
     assert shard.history() == 0
     store = oracle_store(spec)
