@@ -50,7 +50,12 @@ struct PrepArgs {
   uint32_t* vals;
   uint64_t* refscale;  // reference words with their scales (8 bytes), or
   uint32_t* refs;      // without (4 bytes: no weighted-sum feature; the scale is derived)
+  // Words that keygen's blocks clear (the group look-back flags of the
+  // passes, which only the passes after keygen read): one fill launch fewer.
+  uint32_t* zero;
+  uint64_t zero_words;
 };
+static_assert(sizeof(PrepArgs) <= 4096, "keygen arguments fit the kernel-argument segment");
 
 // What the last pass needs to put each reference word's scale back (pushes
 // with no weighted-sum feature sort 4-byte words without it): the mean
@@ -67,6 +72,9 @@ __global__ void __launch_bounds__(kBlock) KeygenKernel(PrepArgs args) {
   __shared__ uint32_t s_misc[2];  // [0] bad, [1] max scale
   __shared__ uint64_t s_off[kStageBags];  // offsets[b0 .. b0 + staged)
   __shared__ uint64_t s_b0;
+  for (uint64_t i = uint64_t(blockIdx.x) * kBlock + threadIdx.x; i < args.zero_words;
+       i += uint64_t(gridDim.x) * kBlock)
+    args.zero[i] = 0;
   for (uint32_t i = threadIdx.x; i < kMaxPasses * kDigits; i += kBlock) (&s_hist[0][0])[i] = 0;
   if (threadIdx.x < 2) s_misc[threadIdx.x] = 0;
 
@@ -726,12 +734,12 @@ int Prepare(const eps_hip_table* tables, uint32_t table_count, const eps_hip_pus
   auto* ctrl = reinterpret_cast<Control*>(ws);
   const hipStream_t s = AsStream(stream);
   // Control block (but its status history), histograms and the look-back
-  // flags of the passes this push sorts with start at zero.
+  // flags of the passes this push sorts with start at zero (the group
+  // look-back flags are cleared by keygen, below).
   if (!plan.occurrences)
     return LaunchFill(reinterpret_cast<uint32_t*>(ws), 0, sizeof(Control) / 4, s, kHistoryWord);
   EPS_HIP_TRY(LaunchFill(reinterpret_cast<uint32_t*>(ws), 0, (L.look + plan.passes * L.tiles * kDigits * 4) / 4, s,
                          kHistoryWord));
-  EPS_HIP_TRY(LaunchFill(reinterpret_cast<uint32_t*>(ws + L.group_look), 0, plan.passes * L.groups * kDigits, s));
 
   PrepArgs args{};
   args.count = feature_count;
@@ -743,6 +751,8 @@ int Prepare(const eps_hip_table* tables, uint32_t table_count, const eps_hip_pus
   args.hist = reinterpret_cast<uint32_t*>(ws + L.hist);
   args.keys = reinterpret_cast<uint32_t*>(ws + L.keys_a);
   args.vals = with_vals ? reinterpret_cast<uint32_t*>(ws + L.vals_a) : nullptr;
+  args.zero = reinterpret_cast<uint32_t*>(ws + L.group_look);
+  args.zero_words = uint64_t(plan.passes) * L.groups * kDigits;
   // Reference words ping-pong between two buffers through the passes and
   // end in sorted_rs: keygen writes them where an even number of swaps
   // before the end starts.  A push with no weighted-sum feature sorts them
