@@ -60,7 +60,9 @@ class StepPipeline:
         # own: HIP maps streams onto GPU_MAX_HW_QUEUES queues round robin, and
         # a hot-row kernel queued behind a host-link copy waits for it
         # (ragged mixed-dim step with tier moves on 4 queues: side stream
-        # 0.47 ms, in-stream 0.44 ms).
+        # 0.47 ms, in-stream 0.44 ms).  More queues do not help that step:
+        # with GPU_MAX_HW_QUEUES=8 (every stream on a queue of its own, the
+        # hot rows beside) it ran 0.66-0.67 ms against 0.44-0.50 on 4.
         queues = int(os.environ.get("GPU_MAX_HW_QUEUES", "4"))
         self.hot_overlap = 3 + (2 if moves else 0) <= queues
 
