@@ -1650,7 +1650,9 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
     // whose gradient rows stay in the caches, take 16-column units, so each
     // chunk moves half the bytes through its producers (65,536 pairs on one
     // table: 100.6 -> 97.0 us an update; a ragged 8-table push of 525,000
-    // references lost with them, 270 -> 295 us); otherwise 64-column units,
+    // references lost with them, 270 -> 295 us, and with 256-reference chunks
+    // it still did, 264 -> 296 us, as did 4 x 8.4 M references, 9.9 -> 10.8 ms
+    // a step); otherwise 64-column units,
     // whose fewer and fuller units a block's producers stage with less
     // bookkeeping per column (26 tables of ~43,000 references: 47 -> 41 us a
     // push).
