@@ -159,7 +159,7 @@ def sweep_features(W, rng, specs, skew, layout):
     return feats
 
 
-@pytest.mark.parametrize("seed", range(12))
+@pytest.mark.parametrize("seed", range(60))
 def test_push_random_sweep(torch_gpu, pkg, seed):
     """Seeded random pushes (sweep_case) over two steps, every touched row
     bit-exact against the oracle: table counts, dimensions, poolings, skews and
