@@ -104,6 +104,44 @@ def test_gather_many_parts_one_call(torch_gpu, pkg):
         assert_close(out.cpu().numpy(), want, f"part {i}", strict_ulp=0)
 
 
+GATHER_SWEEP_DIMS = [1, 3, 4, 8, 12, 16, 20, 32, 48, 64, 96, 128, 160, 192, 256, 300, 520]
+
+
+@pytest.mark.parametrize("seed", range(20))
+def test_gather_random_sweep(torch_gpu, pkg, seed):
+    """Seeded random pulls: 1-8 tables of dimensions 1-520 (vector and generic
+    shapes), 1-40 features of every pooling (past 32, the pull takes two
+    launches), bag counts, bag lengths (up to long bags past what a block
+    stages), hole and padded-length rates all drawn per case; every output
+    bit-exact against the oracle."""
+    torch, W, H = torch_gpu, pkg.workloads, pkg.eps_hip
+    rng = np.random.default_rng(7000 + seed)
+    n_tables = int(rng.integers(1, 9))
+    specs = [W.TableSpec(i, int(rng.choice(GATHER_SWEEP_DIMS)), int(rng.integers(50, 5000)), seed=300 + seed * 10 + i)
+             for i in range(n_tables)]
+    feats = []
+    for i in range(int(rng.integers(1, 41))):
+        t = int(rng.integers(0, n_tables))
+        max_len = int(rng.choice([0, 3, 12, 40, 200]))
+        f = random_feature(W, rng, specs[t], int(rng.integers(0, 4)), bags=int(rng.integers(1, 400)),
+                           max_len=max_len, holes=float(rng.choice([0.0, 0.05, 0.3])),
+                           pad=float(rng.choice([0.0, 0.2, 0.6])))
+        f.table = t
+        feats.append(f)
+    print(f"case: seed={seed} dims={[s.dim for s in specs]} features={len(feats)} "
+          f"occurrences={sum(len(f.keys) for f in feats)}", flush=True)
+    shard = H.DeviceShard(torch, specs)
+    shard.init_rows()
+    status = torch.zeros(1, dtype=torch.int32, device="cuda")
+    outs = shard.lookup([H.DeviceFeature(torch, f) for f in feats], status=status)
+    torch.cuda.synchronize()
+    assert int(status.item()) == 0
+    stores = [oracle_store(s) for s in specs]
+    for i, (f, out) in enumerate(zip(feats, outs)):
+        want = expected(stores[f.table], f, specs[f.table].dim)
+        assert_close(out.cpu().numpy(), want, f"seed {seed} feature {i}", strict_ulp=0)
+
+
 def test_gather_remap_and_transferred_vectors(torch_gpu, pkg):
     """transfer_unique route: source = unique vectors (stride dim), indices are
     unique indices mapped through `remap` (cache_backend.cu:264-300)."""
