@@ -63,6 +63,27 @@ def test_unique_and_reduce_match_oracle(torch_gpu, pkg, dims):
     specs = [W.TableSpec(i, d, 5000 + 1000 * i, seed=20 + i) for i, d in enumerate(dims)]
     feats = random_features(W, rng, specs, 7, holes=0.05)
     print(f"case: dims={dims} occurrences={sum(len(f.keys) for f in feats)}", flush=True)
+    check_unique_reduce(torch, W, H, specs, feats)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_unique_and_reduce_random_sweep(torch_gpu, pkg, seed):
+    """The push sweep's random layouts (sweep_case: 1-6 tables of mixed
+    dimensions, every pooling, skews 1.05-1.5, 4,000-300,000 references) with
+    0-10 % of the keys made holes: first-occurrence unique rows, the occurrence
+    map and the reduced gradients against the oracle."""
+    torch, W, H = torch_gpu, pkg.workloads, pkg.eps_hip
+    rng, specs, skew, layout = sweep_case(W, 500 + seed)
+    feats = sweep_features(W, rng, specs, skew, layout)
+    holes = float(rng.choice([0.0, 0.03, 0.1]))
+    for f in feats:
+        f.keys[rng.random(len(f.keys)) < holes] = HOLE
+    print(f"case: seed={seed} dims={[s.dim for s in specs]} holes={holes} "
+          f"occurrences={sum(len(f.keys) for f in feats)}", flush=True)
+    check_unique_reduce(torch, W, H, specs, feats)
+
+
+def check_unique_reduce(torch, W, H, specs, feats):
     shard = H.DeviceShard(torch, specs)
     shard.init_rows()
     dev = [H.DeviceFeature(torch, f) for f in feats]
