@@ -1175,7 +1175,10 @@ __device__ __forceinline__ void RowRuns(const VecArgs& a, RunShared& sh, const T
   // Safe address for reads a damaged workspace would point elsewhere: the
   // control block and what follows it (far more than a row of 3 x 256 floats).
   const float* safe = reinterpret_cast<const float*>(a.ctrl);
-  const uint32_t begin = ctrl->class_start[cls], end = ctrl->class_start[cls + 1];
+  // The class's sorted positions, from the workspace: kept inside the push's
+  // positions, so a damaged workspace cannot send the staging reads past them.
+  const uint32_t first = ctrl->class_start[cls], last = ctrl->class_start[cls + 1];
+  const uint32_t end = min(last, a.n), begin = min(first, end);
   const uint32_t row_mask = (1u << a.row_bits) - 1;
   const uint32_t lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
   const uint32_t lig = threadIdx.x & (G - 1), gid = threadIdx.x >> kLog2G;
