@@ -441,8 +441,9 @@ __global__ void __launch_bounds__(kBlock) SortedUpdateKernel(FusedArgs a) {
   Control* ctrl = a.ctrl;
   bool write = true;
   if (!a.reduce && !LaunchGate(ctrl, s_t, a.gs, a.role, &s_mode, write)) return;
-  const uint32_t start = ctrl->class_start[a.cls];
-  const uint32_t end = ctrl->class_start[a.cls_end];
+  // The classes' sorted positions, from the workspace, kept inside the push's.
+  const uint32_t first = ctrl->class_start[a.cls], last = ctrl->class_start[a.cls_end];
+  const uint32_t end = min(last, a.n), start = min(first, end);
   const uint32_t G = kGeneric ? kWave : (1u << a.log2g);
   const uint32_t lig = threadIdx.x & (G - 1);
   const uint32_t gid = threadIdx.x / G, ngroups = kBlock / G;
