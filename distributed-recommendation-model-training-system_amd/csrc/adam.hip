@@ -601,9 +601,11 @@ struct HotShape {
   static constexpr uint32_t kWords = kC / kWave;
   static constexpr uint32_t kPitch = kC + 4;
   static constexpr uint32_t kPart = kS < 32 ? kWave / 2 : kWave;
-  // Own chunks each producer keeps in flight: two (four measured no faster),
-  // one for 16-column units, whose chunks of 256 references keep as many
-  // bytes in flight and leave the registers for their longer reference lists.
+  // Own chunks each producer keeps in flight: two (four measured no faster,
+  // and for the HBM-bound chains of 4 x 8.4 M references three or four made
+  // the step 9.8 -> 11.3-11.7 ms), one for 16-column units, whose chunks of
+  // 256 references keep as many bytes in flight and leave the registers for
+  // their longer reference lists.
   static constexpr uint32_t kDepth = kS < 32 ? 1 : 2;
   static constexpr uint32_t kParts = kC / kPart;
   static_assert(kC % kWave == 0 && kS <= kWave && kWave % kQuads == 0 && kLoads % 4 == 0 &&
