@@ -1698,6 +1698,14 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
       if (overlap) {
         EPS_HIP_TRY(ThreadOverlap(&ov));
         EPS_HIP_TRY(Check(hipEventRecord(ov->fork, s), "update fork"));
+        // With the rows beside, the hot rows (the longer part) go out on this
+        // stream before the side stream's wait is set up (the wait on a
+        // pending event takes ~14 us of host time): they use no class fields
+        // of `va`, and they decide from the same snapshot as the rows.
+        if (hot_units && rows_beside) {
+          va.role = role;
+          EPS_HIP_TRY(LaunchVectorUpdate(0, slice, unsigned(hot_blocks), va, s));
+        }
         EPS_HIP_TRY(Check(hipStreamWaitEvent(ov->side, ov->fork, 0), "update fork wait"));
       }
       // The side stream's last kernel records the join as it completes.
@@ -1728,7 +1736,6 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
       }
       va.class_block[kClasses - 1] = uint32_t(total_blocks);
       va.class_grid[kClasses - 1] = 0;
-      const uint32_t hot_role = role;  // the hot rows beside the row runs decide too
       // With the rows beside, their launch is the side stream's last (one
       // launch at most: several classes share one).
       const hipEvent_t rows_done = rows_beside ? ov->join : nullptr;
@@ -1749,10 +1756,6 @@ int RunSorted(const eps_hip_table* tables, const eps_hip_optimizer* optimizers, 
         }
       }
       if (overlap && !joined) EPS_HIP_TRY(Check(hipEventRecord(ov->join, ov->side), "update join"));
-      if (hot_units && rows_beside) {
-        va.role = hot_role;
-        EPS_HIP_TRY(LaunchVectorUpdate(0, slice, unsigned(hot_blocks), va, s));
-      }
     }
   }
   for (uint32_t cls = 0; cls < kClasses; ++cls) {
